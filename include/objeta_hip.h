@@ -1,0 +1,232 @@
+/*
+ * objeta_hip.h — C ABI of the MI355X (gfx950) selected-expert MoE decode path.
+ *
+ * This is the drop-in boundary for the reference's objeta-cuda crate
+ * (crates/objeta-cuda/src). Every entry point takes plain pointers and sizes and
+ * returns an int32 status: 0 on success, otherwise the reference's CudaErrorKind
+ * ordinal + 1 (crates/objeta-cuda/src/lib.rs:39-48). The failing call's details
+ * (the fields of the reference's CudaError, lib.rs:50-79) are kept per thread and
+ * read back with objeta_hip_last_error().
+ *
+ * Ownership: the caller owns every host buffer and output array; the library
+ * owns device memory it allocates (cache residents, workspaces). Device pointers
+ * passed in ("d_" arguments) stay owned by the caller.
+ *
+ * Threading: a context may be used from one thread at a time (the reference's
+ * QuantBackend / MoeExecutor are &self but serialise on their stream). A cache
+ * handle is not internally locked, matching the reference's `&mut CudaExpertCache`.
+ *
+ * Streams: `objeta_hip_stream` is a hipStream_t. NULL means the context's stream 0.
+ * All *_device entry points are asynchronous on the given stream, allocate
+ * nothing on the hot path and may be captured into a hipGraph.
+ */
+#ifndef OBJETA_HIP_H
+#define OBJETA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OBJETA_HIP_ABI_VERSION 1
+
+/* ------------------------------------------------------------------ errors */
+/* CudaErrorKind + 1 (lib.rs:39-48). */
+enum {
+    OBJETA_HIP_OK = 0,
+    OBJETA_HIP_ERR_DRIVER = 1,
+    OBJETA_HIP_ERR_RUNTIME = 2,
+    OBJETA_HIP_ERR_NVRTC = 3, /* kept for ordinal parity; this library compiles ahead of time */
+    OBJETA_HIP_ERR_IO = 4,
+    OBJETA_HIP_ERR_INVALID_INPUT = 5,
+    OBJETA_HIP_ERR_UNSUPPORTED = 6,
+    OBJETA_HIP_ERR_INTERNAL = 7
+};
+
+/* CudaError{kind, action, file, line, module, source_message} (lib.rs:50-79). */
+typedef struct {
+    int32_t kind; /* CudaErrorKind ordinal (status - 1); -1 when no error recorded */
+    uint32_t line;
+    char action[160];
+    char file[96];
+    char module[64];
+    char source_message[320];
+} objeta_hip_error;
+
+/* Copies this thread's last error; returns its status (0 if none). */
+int32_t objeta_hip_last_error(objeta_hip_error* out);
+void objeta_hip_clear_error(void);
+int32_t objeta_hip_abi_version(void);
+
+/* ----------------------------------------------------------------- formats */
+/* QuantFormat (crates/objeta-cuda/src/quant.rs:25-31). */
+enum {
+    OBJETA_HIP_Q4_0 = 0,     /* 18-byte blocks: f16 scale + 16 nibble bytes */
+    OBJETA_HIP_Q5_0 = 1,     /* 22-byte blocks: f16 scale + 4-byte high mask + 16 nibble bytes */
+    OBJETA_HIP_IQ3_0 = 2,    /* 14-byte blocks: f16 scale + 8 bytes 2-bit lows + 4 bytes highs */
+    OBJETA_HIP_FP4_E2M1 = 3  /* 17-byte interleaved blocks: E8M0 scale + 16 nibble bytes */
+};
+
+/* QuantFormat::block_size / block_bytes (quant.rs:34-51); -1 for an unknown format. */
+int32_t objeta_hip_block_size(int32_t format);
+int32_t objeta_hip_block_bytes(int32_t format);
+/* QGemvShape::quantized_matrix_bytes (quant.rs:140-142); -1 if cols % 32 != 0. */
+int64_t objeta_hip_quantized_matrix_bytes(int32_t format, uint64_t rows, uint64_t cols);
+
+/* ----------------------------------------------------------------- devices */
+typedef struct objeta_hip_context objeta_hip_context;
+typedef void* objeta_hip_stream; /* hipStream_t */
+typedef void* objeta_hip_event;  /* hipEvent_t */
+typedef void* objeta_hip_graph;  /* hipGraphExec_t */
+
+/* BackendInitOptions (crates/objeta-cuda/src/ffi.rs:1-7) / CudaBackendBuilder
+ * (context.rs:37-70). stream_count is clamped to >= 1. */
+typedef struct {
+    uint64_t device_ordinal;
+    uint64_t stream_count;
+} objeta_hip_init_options;
+
+/* CudaDeviceInfo (context.rs:16-24) plus the CDNA facts the kernels size for.
+ * compute_capability_major/minor carry the gfx major/minor (9, 5 for gfx950). */
+typedef struct {
+    uint64_t ordinal;
+    char name[256];
+    char arch[64];
+    uint64_t total_global_mem_bytes;
+    int32_t compute_capability_major;
+    int32_t compute_capability_minor;
+    int32_t driver_version;
+    int32_t runtime_version;
+    int32_t compute_units;
+    int32_t wavefront_size;
+    int32_t l2_cache_bytes;
+    int32_t max_shared_memory_per_block;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width_bits;
+    int32_t reserved;
+} objeta_hip_device_info;
+
+/* CudaBackend::discover_devices (context.rs:73-104). */
+int32_t objeta_hip_device_count(int32_t* out);
+int32_t objeta_hip_discover_device(uint64_t ordinal, objeta_hip_device_info* out);
+/* CudaBackend::new (context.rs:106-141). */
+int32_t objeta_hip_init(const objeta_hip_init_options* opts, objeta_hip_context** out);
+int32_t objeta_hip_destroy(objeta_hip_context* ctx);
+int32_t objeta_hip_device_info_get(const objeta_hip_context* ctx, objeta_hip_device_info* out);
+/* CudaStreamPool::stream (stream.rs:38-51). */
+int32_t objeta_hip_stream_get(objeta_hip_context* ctx, uint64_t index, objeta_hip_stream* out);
+/* CudaStreamHandle::synchronize (stream.rs:67-74). */
+int32_t objeta_hip_stream_synchronize(objeta_hip_context* ctx, objeta_hip_stream stream);
+
+/* ------------------------------------------------------------------ memory */
+/* DeviceBuffer / alloc_zeros / alloc_uninit (memory.rs:8-28, stream.rs:76-102). */
+int32_t objeta_hip_malloc(objeta_hip_context* ctx, uint64_t bytes, void** d_out);
+int32_t objeta_hip_free(objeta_hip_context* ctx, void* d_ptr);
+/* PinnedHostBuffer (memory.rs:31-80, context.rs:143-165). */
+int32_t objeta_hip_alloc_pinned_host(objeta_hip_context* ctx, uint64_t bytes, void** h_out);
+int32_t objeta_hip_free_pinned_host(objeta_hip_context* ctx, void* h_ptr);
+/* copy_from_slice / copy_to_vec / copy_dtod (stream.rs:104-201), asynchronous on
+ * `stream` (pageable host memory makes the HIP runtime stage the copy). */
+int32_t objeta_hip_copy_h2d(objeta_hip_context* ctx, objeta_hip_stream stream, void* d_dst,
+                            const void* h_src, uint64_t bytes);
+int32_t objeta_hip_copy_d2h(objeta_hip_context* ctx, objeta_hip_stream stream, void* h_dst,
+                            const void* d_src, uint64_t bytes);
+int32_t objeta_hip_copy_d2d(objeta_hip_context* ctx, objeta_hip_stream stream, void* d_dst,
+                            const void* d_src, uint64_t bytes);
+/* Zero-fill with a kernel (safe to capture into a graph). */
+int32_t objeta_hip_zero_device(objeta_hip_context* ctx, objeta_hip_stream stream, void* d_dst,
+                               uint64_t bytes);
+
+/* ------------------------------------------------------- events and graphs */
+/* CudaEventTimer (telemetry.rs:14-44) split into its parts. */
+int32_t objeta_hip_event_create(objeta_hip_context* ctx, objeta_hip_event* out);
+int32_t objeta_hip_event_record(objeta_hip_context* ctx, objeta_hip_event ev, objeta_hip_stream stream);
+/* Waits for `end` and returns the elapsed milliseconds between the two events. */
+int32_t objeta_hip_event_elapsed_ms(objeta_hip_context* ctx, objeta_hip_event start,
+                                    objeta_hip_event end, float* ms_out);
+int32_t objeta_hip_event_destroy(objeta_hip_context* ctx, objeta_hip_event ev);
+/* hipGraph capture of everything enqueued on `stream` between begin and end. No
+ * reference counterpart: the reference syncs after every launch. */
+int32_t objeta_hip_graph_begin_capture(objeta_hip_context* ctx, objeta_hip_stream stream);
+int32_t objeta_hip_graph_end_capture(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                     objeta_hip_graph* out);
+int32_t objeta_hip_graph_launch(objeta_hip_context* ctx, objeta_hip_graph graph,
+                                objeta_hip_stream stream);
+int32_t objeta_hip_graph_destroy(objeta_hip_context* ctx, objeta_hip_graph graph);
+
+/* -------------------------------------------------------------------- GEMV */
+/* QGemvTelemetry (quant.rs:145-154). bytes_read = W + 4*cols, as quant.rs:282. */
+typedef struct {
+    float h2d_ms;
+    float kernel_ms;
+    float d2h_ms;
+    float unaccounted_ms;
+    float total_ms;
+    float effective_gbps;
+    uint64_t bytes_read;
+} objeta_hip_qgemv_telemetry;
+
+/* QuantBackend::gemv (quant.rs:256-302): host qweights and x in, host y out.
+ * Validation and messages follow validate_quant_inputs (quant.rs:751-793).
+ * format: any block format (Q4_0, Q5_0, IQ3_0, FP4_E2M1 interleaved). tel may be NULL. */
+int32_t objeta_hip_qgemv(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                         const uint8_t* qweights, uint64_t qweights_len, const float* x,
+                         uint64_t x_len, uint64_t rows, uint64_t cols, float* y,
+                         objeta_hip_qgemv_telemetry* tel);
+
+/* QuantBackend::launch_kernel (quant.rs:324-366) generalised to `batch` activation
+ * vectors: d_x is [batch][cols] f32, d_y is [batch][rows] f32 (overwritten). */
+int32_t objeta_hip_qgemv_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                const void* d_qweights, const float* d_x, float* d_y,
+                                uint64_t rows, uint64_t cols, uint64_t batch);
+
+/* QuantBackend::launch_kernel_split_fp4 (quant.rs:368-408): DeepSeek split FP4
+ * layout, d_w [rows][cols/2] nibbles, d_scales [rows][cols/32] E8M0 bytes. */
+int32_t objeta_hip_fp4_gemv_split_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                         const void* d_w, const void* d_scales, const float* d_x,
+                                         float* d_y, uint64_t rows, uint64_t cols, uint64_t batch);
+
+/* --------------------------------------------------- quantizer / generators */
+/* quantize_matrix_cpu (quant.rs:506-581) on the device; bytes identical to the
+ * CPU quantizer. d_m: [rows][cols] f32; d_out: quantized_matrix_bytes. */
+int32_t objeta_hip_quantize_matrix_device(objeta_hip_context* ctx, int32_t format,
+                                          objeta_hip_stream stream, const float* d_m,
+                                          uint64_t rows, uint64_t cols, void* d_out);
+/* Synthetic inputs (no reference counterpart; the reference generates on the CPU
+ * with seeded_f32s, bench_qgemv.rs:39-49). Element i is sigma * z(seed, first + i)
+ * with z a counter-based Irwin-Hall(12) draw; the CPU recipe gives the same bits. */
+int32_t objeta_hip_fill_gauss_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                     float* d_out, uint64_t n, uint64_t seed, uint64_t first,
+                                     float sigma);
+/* Generate a [rows][cols] matrix as above (element r*cols+c) and quantize it in
+ * one pass; bytes equal quantize_matrix_cpu of the generated matrix. */
+int32_t objeta_hip_fill_gauss_quantized_device(objeta_hip_context* ctx, int32_t format,
+                                               objeta_hip_stream stream, void* d_out,
+                                               uint64_t rows, uint64_t cols, uint64_t seed,
+                                               float sigma);
+/* The E8M0 exponent rule of the device FP4 quantizer (fp4_quantize_block,
+ * quant.rs:913-918) evaluated on the host, element-wise over n block maxima. */
+int32_t objeta_hip_fp4_scale_raw_host(const float* amax, uint8_t* out, uint64_t n);
+
+/* ------------------------------------------------------------------ router */
+/* Router for n_tokens activation rows: logits = W_r x (+ bias), softmax over all
+ * experts, stable top-k by probability (ties keep the lower expert id), then the
+ * k probabilities renormalised to sum 1 when `renormalize` != 0. Follows cpu_router
+ * (crates/objeta-cuda/src/bin/deepseek_single_layer_moe.rs:687-743) and the
+ * renormalised top-k of router_topk_cpu
+ * (crates/objeta-qwen36-executor/src/moe_dispatch.rs:403-435).
+ * d_w_r [n_experts][hidden] f32; d_bias [n_experts] or NULL; d_x [n_tokens][hidden];
+ * d_ids [n_tokens][k] u32; d_weights [n_tokens][k] f32. n_experts <= 1024, k <= 32. */
+int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                      const float* d_w_r, const float* d_bias, const float* d_x,
+                                      uint64_t n_tokens, uint64_t n_experts, uint64_t hidden,
+                                      uint64_t k, int32_t renormalize, uint32_t* d_ids,
+                                      float* d_weights);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OBJETA_HIP_H */

@@ -1,0 +1,117 @@
+"""ctypes loader for libobjeta_hip.so (the C ABI declared in include/objeta_hip.h).
+
+The library is built in-tree by __graft_entry__.build() (objeta_amd/csrc/Makefile)
+into objeta_amd/lib/. Loading fails loudly when it is missing: there is no CPU
+fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libobjeta_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "objeta_hip.h")
+
+_lib = None
+
+P = C.c_void_p
+I32 = C.c_int32
+U32 = C.c_uint32
+U64 = C.c_uint64
+I64 = C.c_int64
+F32 = C.c_float
+
+
+class Error(C.Structure):
+    _fields_ = [("kind", I32), ("line", U32), ("action", C.c_char * 160), ("file", C.c_char * 96),
+                ("module", C.c_char * 64), ("source_message", C.c_char * 320)]
+
+
+class InitOptions(C.Structure):
+    _fields_ = [("device_ordinal", U64), ("stream_count", U64)]
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("ordinal", U64), ("name", C.c_char * 256), ("arch", C.c_char * 64),
+                ("total_global_mem_bytes", U64), ("compute_capability_major", I32),
+                ("compute_capability_minor", I32), ("driver_version", I32), ("runtime_version", I32),
+                ("compute_units", I32), ("wavefront_size", I32), ("l2_cache_bytes", I32),
+                ("max_shared_memory_per_block", I32), ("clock_khz", I32), ("memory_clock_khz", I32),
+                ("memory_bus_width_bits", I32), ("reserved", I32)]
+
+
+class QGemvTelemetry(C.Structure):
+    _fields_ = [("h2d_ms", F32), ("kernel_ms", F32), ("d2h_ms", F32), ("unaccounted_ms", F32),
+                ("total_ms", F32), ("effective_gbps", F32), ("bytes_read", U64)]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "objeta_hip_last_error": (I32, [P]),
+    "objeta_hip_clear_error": (None, []),
+    "objeta_hip_abi_version": (I32, []),
+    "objeta_hip_block_size": (I32, [I32]),
+    "objeta_hip_block_bytes": (I32, [I32]),
+    "objeta_hip_quantized_matrix_bytes": (I64, [I32, U64, U64]),
+    "objeta_hip_device_count": (I32, [P]),
+    "objeta_hip_discover_device": (I32, [U64, P]),
+    "objeta_hip_init": (I32, [P, P]),
+    "objeta_hip_destroy": (I32, [P]),
+    "objeta_hip_device_info_get": (I32, [P, P]),
+    "objeta_hip_stream_get": (I32, [P, U64, P]),
+    "objeta_hip_stream_synchronize": (I32, [P, P]),
+    "objeta_hip_malloc": (I32, [P, U64, P]),
+    "objeta_hip_free": (I32, [P, P]),
+    "objeta_hip_alloc_pinned_host": (I32, [P, U64, P]),
+    "objeta_hip_free_pinned_host": (I32, [P, P]),
+    "objeta_hip_copy_h2d": (I32, [P, P, P, P, U64]),
+    "objeta_hip_copy_d2h": (I32, [P, P, P, P, U64]),
+    "objeta_hip_copy_d2d": (I32, [P, P, P, P, U64]),
+    "objeta_hip_zero_device": (I32, [P, P, P, U64]),
+    "objeta_hip_event_create": (I32, [P, P]),
+    "objeta_hip_event_record": (I32, [P, P, P]),
+    "objeta_hip_event_elapsed_ms": (I32, [P, P, P, P]),
+    "objeta_hip_event_destroy": (I32, [P, P]),
+    "objeta_hip_graph_begin_capture": (I32, [P, P]),
+    "objeta_hip_graph_end_capture": (I32, [P, P, P]),
+    "objeta_hip_graph_launch": (I32, [P, P, P]),
+    "objeta_hip_graph_destroy": (I32, [P, P]),
+    "objeta_hip_qgemv": (I32, [P, I32, P, P, U64, P, U64, U64, U64, P, P]),
+    "objeta_hip_qgemv_device": (I32, [P, I32, P, P, P, P, U64, U64, U64]),
+    "objeta_hip_fp4_gemv_split_device": (I32, [P, P, P, P, P, P, U64, U64, U64]),
+    "objeta_hip_quantize_matrix_device": (I32, [P, I32, P, P, U64, U64, P]),
+    "objeta_hip_fill_gauss_device": (I32, [P, P, P, U64, U64, U64, F32]),
+    "objeta_hip_fill_gauss_quantized_device": (I32, [P, I32, P, P, U64, U64, U64, F32]),
+    "objeta_hip_fp4_scale_raw_host": (I32, [P, P, U64]),
+    "objeta_hip_router_topk_device": (I32, [P, P, P, P, P, U64, U64, U64, U64, I32, P, P]),
+}
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def header_functions(path: str = HEADER) -> list:
+    """Names of every function declared in include/objeta_hip.h."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(objeta_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def load():
+    """Load libobjeta_hip.so (raises LibraryMissing if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryMissing(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

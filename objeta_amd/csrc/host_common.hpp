@@ -1,0 +1,94 @@
+// host_common.hpp — host-side plumbing shared by the C-ABI translation units:
+// the per-thread error record, HIP error mapping and the context object.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/objeta_hip.h"
+
+namespace objeta {
+
+// CudaErrorKind ordinals (crates/objeta-cuda/src/lib.rs:39-48).
+enum Kind : int32_t {
+    kDriver = 0,
+    kRuntime = 1,
+    kNvrtc = 2,
+    kIo = 3,
+    kInvalidInput = 4,
+    kUnsupported = 5,
+    kInternal = 6
+};
+
+// Records the error for this thread and returns its status (kind + 1).
+int32_t set_error(Kind kind, const char* file, unsigned line, const char* module,
+                  const std::string& action, const std::string& message);
+std::string strf(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+#define OBJ_FAIL(kind, action, msg) \
+    return ::objeta::set_error((kind), __FILE__, __LINE__, __func__, (action), (msg))
+
+#define OBJ_HIP(call, action)                                                          \
+    do {                                                                               \
+        hipError_t e_ = (call);                                                        \
+        if (e_ != hipSuccess) {                                                        \
+            (void)hipGetLastError();                                                   \
+            return ::objeta::set_error(::objeta::kDriver, __FILE__, __LINE__, __func__, \
+                                       (action), hipGetErrorString(e_));               \
+        }                                                                              \
+    } while (0)
+
+#define OBJ_TRY(expr)               \
+    do {                            \
+        int32_t rc_ = (expr);       \
+        if (rc_ != 0) return rc_;   \
+    } while (0)
+
+// Wraps a C entry point body so that no C++ exception crosses the C boundary.
+#define OBJ_GUARD_BEGIN try {
+#define OBJ_GUARD_END                                                                  \
+    }                                                                                  \
+    catch (const std::bad_alloc&) {                                                    \
+        return ::objeta::set_error(::objeta::kInternal, __FILE__, __LINE__, __func__,  \
+                                   "host allocation", "std::bad_alloc");              \
+    }                                                                                  \
+    catch (const std::exception& ex) {                                                 \
+        return ::objeta::set_error(::objeta::kInternal, __FILE__, __LINE__, __func__,  \
+                                   "host exception", ex.what());                      \
+    }
+
+// Device scratch owned by the context, grown only outside graph capture.
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace objeta
+
+struct objeta_hip_context {
+    int device = 0;
+    objeta_hip_device_info info{};
+    std::vector<hipStream_t> streams;  // streams[0] is the default compute stream
+    hipStream_t copy_stream = nullptr;  // side stream for cache H2D traffic
+    objeta::Workspace ws;               // scratch for multi-kernel entry points
+    uint32_t* counters = nullptr;       // zero-initialised device counters (self-resetting)
+    size_t counter_words = 0;
+    std::mutex mu;
+};
+
+namespace objeta {
+
+int32_t check_ctx(const objeta_hip_context* ctx, const char* action);
+hipStream_t resolve_stream(objeta_hip_context* ctx, objeta_hip_stream s);
+// Makes sure the context workspace holds at least `bytes`; fails (Unsupported) if it
+// would have to grow while `stream` is capturing.
+int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, size_t bytes);
+
+}  // namespace objeta

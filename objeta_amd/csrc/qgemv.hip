@@ -1,0 +1,597 @@
+// qgemv.hip — block-dequant GEMV for Q4_0 / Q5_0 / IQ3_0 / FP4-E2M1 on gfx950.
+//
+// Replaces q4_gemv_f32_accum / q5_gemv_f32_accum / iq3_gemv_f32_accum /
+// fp4_e2m1_gemv / fp4_e2m1_gemv_split (crates/objeta-cuda/kernels/*.cu) and the
+// host paths QuantBackend::gemv / launch_kernel / launch_kernel_split_fp4
+// (crates/objeta-cuda/src/quant.rs:256-408).
+//
+// Fast path (cols % 64 == 0, 4-byte aligned weights): a wave64 lane owns one
+// *pair* of consecutive blocks (36 / 44 / 28 bytes, always 4-byte aligned) and
+// streams it with dwordx4 loads; consecutive lanes own consecutive pairs, so a
+// wave reads contiguous bytes. A lane keeps U rows of the same pair in flight and
+// reuses each activation read from LDS across them. Activations are staged once
+// per workgroup in LDS with 4 floats of padding per 64 so that lanes reading
+// different pairs hit different banks. Row sums are reduced across the lanes of
+// a row with DPP/permute shuffles.
+#include "device_common.hpp"
+#include "host_common.hpp"
+#include "kernels.hpp"
+
+namespace objeta {
+namespace dev {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kPad = 68;  // floats per 64-activation pair slot in LDS
+
+// Stages NT activation vectors of `cols` floats into LDS, padded per 64.
+template <int NT>
+__device__ __forceinline__ void stage_x(float* __restrict__ lds, const float* __restrict__ x,
+                                        uint32_t cols, uint32_t pairs) {
+    const uint32_t n4 = NT * cols / 4;
+    for (uint32_t i = threadIdx.x; i < n4; i += kThreads) {
+        const uint32_t t = (i * 4) / cols;
+        const uint32_t c = i * 4 - t * cols;
+        const float4 v = reinterpret_cast<const float4*>(x)[i];
+        float* dst = lds + t * pairs * kPad + (c >> 6) * kPad + (c & 63);
+        *reinterpret_cast<float4*>(dst) = v;
+    }
+}
+
+template <int F, int NT, int U>
+__global__ __launch_bounds__(kThreads) void qgemv_fast(const uint8_t* __restrict__ q,
+                                                       const float* __restrict__ x,
+                                                       float* __restrict__ y, uint32_t rows,
+                                                       uint32_t cols, uint32_t lpr) {
+    extern __shared__ float lds[];
+    const uint32_t pairs = cols >> 6;
+    constexpr int kPairBytes = 2 * Fmt<F>::kBlockBytes;
+    const size_t row_bytes = static_cast<size_t>(pairs) * kPairBytes;
+    stage_x<NT>(lds, x, cols, pairs);
+    __syncthreads();
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const uint32_t g = 64 / lpr;  // row slots per wave
+    const uint32_t slot = lane / lpr;
+    const uint32_t lp = lane - slot * lpr;
+    const bool active = slot < g;
+    const uint32_t row0 = wave * g * U + slot;
+
+    float acc[U][NT];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[u][t] = 0.f;
+
+    if (active) {
+        for (uint32_t p = lp; p < pairs; p += lpr) {
+            uint32_t d[U][Fmt<F>::kPairDw];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t r = row0 + u * g;
+                if (r < rows) {
+                    const uint32_t* src = reinterpret_cast<const uint32_t*>(
+                        q + static_cast<size_t>(r) * row_bytes + static_cast<size_t>(p) * kPairBytes);
+                    load_dwords<Fmt<F>::kPairDw>(src, d[u]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < Fmt<F>::kPairDw; ++i) d[u][i] = 0;
+                }
+            }
+            const float* xs[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) xs[t] = lds + (t * pairs + p) * kPad;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                pair_dot<F, NT>(d[u], q + static_cast<size_t>(row0 + u * g) * row_bytes + static_cast<size_t>(p) * kPairBytes,
+                                xs, acc[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float v = acc[u][t];
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                float o = __shfl_down(v, off, 64);
+                v += (lp + off < lpr) ? o : 0.0f;
+            }
+            acc[u][t] = v;
+        }
+    }
+    if (active && lp == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t r = row0 + u * g;
+            if (r < rows) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + r] = acc[u][t];
+            }
+        }
+    }
+}
+
+// Generic path: any cols % 32 == 0 and any alignment, including the interleaved
+// 17-byte FP4 layout. One wave per row, lanes stride over blocks, byte loads.
+template <int F, int NT>
+__global__ __launch_bounds__(kThreads) void qgemv_generic(const uint8_t* __restrict__ q,
+                                                          const float* __restrict__ x,
+                                                          float* __restrict__ y, uint32_t rows,
+                                                          uint32_t cols) {
+    constexpr int BB = Fmt<F>::kBlockBytes;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint32_t nb = cols >> 5;
+    const uint8_t* rq = q + static_cast<size_t>(row) * nb * BB;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.f;
+    for (uint32_t b = lane; b < nb; b += 64) {
+        const uint8_t* blk = rq + static_cast<size_t>(b) * BB;
+        float scale;
+        if constexpr (F == kFP4) scale = e8m0_to_f32(blk[0]);
+        else scale = f16_to_f32(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
+        for (int i = 0; i < 32; ++i) {
+            float w;
+            if constexpr (F == kQ4) {
+                const uint32_t pk = blk[2 + i / 2];
+                w = static_cast<float>(static_cast<int>((i & 1) ? (pk >> 4) : (pk & 15)) - 8);
+            } else if constexpr (F == kQ5) {
+                const uint32_t pk = blk[6 + i / 2];
+                const uint32_t lo = (i & 1) ? (pk >> 4) : (pk & 15);
+                const uint32_t hi = (blk[2 + i / 8] >> (i & 7)) & 1u;
+                w = static_cast<float>(static_cast<int>(lo | (hi << 4)) - 16);
+            } else if constexpr (F == kIQ3) {
+                const uint32_t lo = (blk[2 + i / 4] >> (2 * (i & 3))) & 3u;
+                const uint32_t hi = (blk[10 + i / 8] >> (i & 7)) & 1u;
+                w = static_cast<float>(static_cast<int>(lo | (hi << 2)) - 4);
+            } else {
+                const uint32_t pk = blk[1 + i / 2];
+                const uint32_t c = (i & 1) ? (pk >> 4) : (pk & 15);
+                w = f16_to_f32(((c & 7u) << 9) | ((c & 8u) << 12)) * 16384.0f;
+            }
+            // the reference's w = value * scale, then sum += w * x (quant.rs:928-1019)
+            w *= scale;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                acc[t] = __builtin_fmaf(w, x[static_cast<size_t>(t) * cols + b * 32 + i], acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float v = wave_reduce(acc[t]);
+        if (lane == 0) y[static_cast<size_t>(t) * rows + row] = v;
+    }
+}
+
+// DeepSeek split FP4: w [rows][cols/2], scales [rows][cols/32]. Fast path when
+// cols % 64 == 0: a lane owns two blocks (32 nibble bytes + 2 scale bytes).
+template <int NT, int U>
+__global__ __launch_bounds__(kThreads) void fp4_split_fast(const uint8_t* __restrict__ w,
+                                                           const uint8_t* __restrict__ sc,
+                                                           const float* __restrict__ x,
+                                                           float* __restrict__ y, uint32_t rows,
+                                                           uint32_t cols, uint32_t lpr) {
+    extern __shared__ float lds[];
+    const uint32_t pairs = cols >> 6;
+    stage_x<NT>(lds, x, cols, pairs);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const uint32_t g = 64 / lpr;
+    const uint32_t slot = lane / lpr;
+    const uint32_t lp = lane - slot * lpr;
+    const bool active = slot < g;
+    const uint32_t row0 = wave * g * U + slot;
+    const size_t wrow = cols >> 1, srow = cols >> 5;
+
+    float acc[U][NT];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[u][t] = 0.f;
+
+    if (active) {
+        for (uint32_t p = lp; p < pairs; p += lpr) {
+            uint32_t d[U][8];
+            uint32_t s2[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t r = row0 + u * g;
+                if (r < rows) {
+                    load_dwords<8>(reinterpret_cast<const uint32_t*>(w + r * wrow + p * 32), d[u]);
+                    s2[u] = *reinterpret_cast<const uint16_t*>(sc + r * srow + p * 2);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) d[u][i] = 0;
+                    s2[u] = 0;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk) {
+                    float a[NT];
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) a[t] = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        float4 xa[NT], xb[NT];
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            const float* xs = lds + (t * pairs + p) * kPad + blk * 32 + 8 * j;
+                            xa[t] = *reinterpret_cast<const float4*>(xs);
+                            xb[t] = *reinterpret_cast<const float4*>(xs + 4);
+                        }
+                        fp4_dot8<NT>(d[u][blk * 4 + j], xa, xb, a);
+                    }
+                    const float scale = e8m0_to_f32((s2[u] >> (8 * blk)) & 0xFFu);
+                    if (__builtin_isfinite(scale)) {
+#pragma unroll
+                        for (int t = 0; t < NT; ++t)
+                            acc[u][t] = __builtin_fmaf(scale, a[t] * 16384.0f, acc[u][t]);
+                    } else {
+                        // reference form w = table[q] * scale per weight (deepseek.rs:866-918)
+                        for (int i = 0; i < 32; ++i) {
+                            const uint32_t c = (d[u][blk * 4 + i / 8] >> (4 * (i & 7))) & 15u;
+                            const float wv = f16_to_f32(((c & 7u) << 9) | ((c & 8u) << 12)) * 16384.0f * scale;
+#pragma unroll
+                            for (int t = 0; t < NT; ++t)
+                                acc[u][t] = __builtin_fmaf(wv, lds[(t * pairs + p) * kPad + blk * 32 + i], acc[u][t]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float v = acc[u][t];
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                float o = __shfl_down(v, off, 64);
+                v += (lp + off < lpr) ? o : 0.0f;
+            }
+            acc[u][t] = v;
+        }
+    }
+    if (active && lp == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t r = row0 + u * g;
+            if (r < rows) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + r] = acc[u][t];
+            }
+        }
+    }
+}
+
+template <int NT>
+__global__ __launch_bounds__(kThreads) void fp4_split_generic(const uint8_t* __restrict__ w,
+                                                              const uint8_t* __restrict__ sc,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, uint32_t rows,
+                                                              uint32_t cols) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint32_t nb = cols >> 5;
+    const uint8_t* rw = w + static_cast<size_t>(row) * (cols >> 1);
+    const uint8_t* rs = sc + static_cast<size_t>(row) * nb;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.f;
+    for (uint32_t b = lane; b < nb; b += 64) {
+        const float scale = e8m0_to_f32(rs[b]);
+        for (int i = 0; i < 32; ++i) {
+            const uint32_t pk = rw[b * 16 + i / 2];
+            const uint32_t c = (i & 1) ? (pk >> 4) : (pk & 15);
+            const float wv = f16_to_f32(((c & 7u) << 9) | ((c & 8u) << 12)) * 16384.0f * scale;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                acc[t] = __builtin_fmaf(wv, x[static_cast<size_t>(t) * cols + b * 32 + i], acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float v = wave_reduce(acc[t]);
+        if (lane == 0) y[static_cast<size_t>(t) * rows + row] = v;
+    }
+}
+
+}  // namespace dev
+
+// ------------------------------------------------------------------ launchers
+namespace {
+
+using namespace dev;
+
+uint32_t pick_lpr(uint32_t pairs) { return pairs >= 64 ? 64u : pairs; }
+
+// Rows per wave pass for the fast kernels.
+int pick_u(const objeta_hip_context* ctx, uint32_t rows, uint32_t g) {
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    const uint32_t rows_per_wg_u1 = g * kWaves;
+    const uint32_t wgs_u4 = (rows + rows_per_wg_u1 * 4 - 1) / (rows_per_wg_u1 * 4);
+    const uint32_t wgs_u2 = (rows + rows_per_wg_u1 * 2 - 1) / (rows_per_wg_u1 * 2);
+    if (wgs_u4 >= 2 * cus) return 4;
+    if (wgs_u2 >= 2 * cus) return 2;
+    return 1;
+}
+
+template <int F, int NT>
+hipError_t launch_fast_nt(hipStream_t s, const uint8_t* q, const float* x, float* y, uint32_t rows,
+                          uint32_t cols, int u, uint32_t lpr, size_t lds) {
+    const uint32_t g = 64 / lpr;
+    const uint32_t per_wg = g * kWaves * static_cast<uint32_t>(u);
+    const dim3 grid((rows + per_wg - 1) / per_wg);
+    if constexpr (NT == 1) {
+        if (u == 4) hipLaunchKernelGGL((qgemv_fast<F, 1, 4>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
+        else if (u == 2) hipLaunchKernelGGL((qgemv_fast<F, 1, 2>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
+        else hipLaunchKernelGGL((qgemv_fast<F, 1, 1>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
+    } else {
+        hipLaunchKernelGGL((qgemv_fast<F, NT, 1>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
+    }
+    return hipGetLastError();
+}
+
+template <int NT>
+hipError_t launch_fp4_fast_nt(hipStream_t s, const uint8_t* w, const uint8_t* sc, const float* x, float* y,
+                              uint32_t rows, uint32_t cols, int u, uint32_t lpr, size_t lds) {
+    const uint32_t g = 64 / lpr;
+    const uint32_t per_wg = g * kWaves * static_cast<uint32_t>(u);
+    const dim3 grid((rows + per_wg - 1) / per_wg);
+    if constexpr (NT == 1) {
+        if (u == 4) hipLaunchKernelGGL((fp4_split_fast<1, 4>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
+        else if (u == 2) hipLaunchKernelGGL((fp4_split_fast<1, 2>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
+        else hipLaunchKernelGGL((fp4_split_fast<1, 1>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
+    } else {
+        hipLaunchKernelGGL((fp4_split_fast<NT, 1>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
+    }
+    return hipGetLastError();
+}
+
+template <int F>
+hipError_t launch_generic(hipStream_t s, const uint8_t* q, const float* x, float* y, uint32_t rows,
+                          uint32_t cols, int nt) {
+    const dim3 grid((rows + kWaves - 1) / kWaves);
+    switch (nt) {
+        case 8: hipLaunchKernelGGL((qgemv_generic<F, 8>), grid, dim3(kThreads), 0, s, q, x, y, rows, cols); break;
+        case 4: hipLaunchKernelGGL((qgemv_generic<F, 4>), grid, dim3(kThreads), 0, s, q, x, y, rows, cols); break;
+        case 2: hipLaunchKernelGGL((qgemv_generic<F, 2>), grid, dim3(kThreads), 0, s, q, x, y, rows, cols); break;
+        default: hipLaunchKernelGGL((qgemv_generic<F, 1>), grid, dim3(kThreads), 0, s, q, x, y, rows, cols); break;
+    }
+    return hipGetLastError();
+}
+
+int max_nt_for_lds(size_t per_token, size_t limit, uint64_t remaining) {
+    for (int nt : {8, 4, 2, 1})
+        if (static_cast<uint64_t>(nt) <= remaining && per_token * nt <= limit) return nt;
+    return 0;
+}
+
+}  // namespace
+
+int32_t launch_qgemv(objeta_hip_context* ctx, int32_t format, hipStream_t s, const void* d_q,
+                     const float* d_x, float* d_y, uint64_t rows, uint64_t cols, uint64_t batch) {
+    const char* action = "launch quantized GEMV";
+    if (objeta_hip_block_bytes(format) < 0) OBJ_FAIL(kInvalidInput, action, strf("unknown format %d", format));
+    if (cols % 32 != 0)
+        OBJ_FAIL(kInvalidInput, action, strf("cols %llu must be a multiple of block_size 32", (unsigned long long)cols));
+    if (rows == 0 || batch == 0) return 0;
+    if (!d_q || !d_x || !d_y) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    if (rows > 0x7FFFFFFFull || cols > 0x7FFFFFFFull)
+        OBJ_FAIL(kInvalidInput, action, "rows/cols exceed 2^31");
+    const uint32_t r = static_cast<uint32_t>(rows), c = static_cast<uint32_t>(cols);
+    const uint8_t* q = static_cast<const uint8_t*>(d_q);
+    const bool aligned = (reinterpret_cast<uintptr_t>(q) % 4 == 0) && (reinterpret_cast<uintptr_t>(d_x) % 16 == 0);
+    const bool fast = format != OBJETA_HIP_FP4_E2M1 && cols % 64 == 0 && aligned;
+    const size_t lds_limit = ctx->info.max_shared_memory_per_block > 0
+                                 ? static_cast<size_t>(ctx->info.max_shared_memory_per_block) : 65536;
+    uint64_t done = 0;
+    while (done < batch) {
+        const uint64_t rem = batch - done;
+        const float* xb = d_x + done * cols;
+        float* yb = d_y + done * rows;
+        hipError_t e = hipSuccess;
+        int nt;
+        if (fast) {
+            const uint32_t pairs = c / 64;
+            const size_t per_token = static_cast<size_t>(pairs) * kPad * sizeof(float);
+            nt = max_nt_for_lds(per_token, lds_limit, rem);
+            if (nt == 0) OBJ_FAIL(kUnsupported, action, strf("cols %u exceed the LDS activation stage", c));
+            const uint32_t lpr = pick_lpr(pairs);
+            const int u = nt > 1 ? 1 : pick_u(ctx, r, 64 / lpr);
+            const size_t lds = per_token * nt;
+#define OBJ_FAST(F)                                                                              \
+    switch (nt) {                                                                                \
+        case 8: e = launch_fast_nt<F, 8>(s, q, xb, yb, r, c, u, lpr, lds); break;                 \
+        case 4: e = launch_fast_nt<F, 4>(s, q, xb, yb, r, c, u, lpr, lds); break;                 \
+        case 2: e = launch_fast_nt<F, 2>(s, q, xb, yb, r, c, u, lpr, lds); break;                 \
+        default: e = launch_fast_nt<F, 1>(s, q, xb, yb, r, c, u, lpr, lds); break;                \
+    }
+            if (format == OBJETA_HIP_Q4_0) { OBJ_FAST(kQ4) }
+            else if (format == OBJETA_HIP_Q5_0) { OBJ_FAST(kQ5) }
+            else { OBJ_FAST(kIQ3) }
+#undef OBJ_FAST
+        } else {
+            nt = rem >= 8 ? 8 : rem >= 4 ? 4 : rem >= 2 ? 2 : 1;
+            switch (format) {
+                case OBJETA_HIP_Q4_0: e = launch_generic<kQ4>(s, q, xb, yb, r, c, nt); break;
+                case OBJETA_HIP_Q5_0: e = launch_generic<kQ5>(s, q, xb, yb, r, c, nt); break;
+                case OBJETA_HIP_IQ3_0: e = launch_generic<kIQ3>(s, q, xb, yb, r, c, nt); break;
+                default: e = launch_generic<kFP4>(s, q, xb, yb, r, c, nt); break;
+            }
+        }
+        if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+        done += static_cast<uint64_t>(nt);
+    }
+    return 0;
+}
+
+int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w, const void* d_s,
+                         const float* d_x, float* d_y, uint64_t rows, uint64_t cols, uint64_t batch) {
+    const char* action = "launch fp4_e2m1_gemv_split";
+    if (cols % 32 != 0)
+        OBJ_FAIL(kInvalidInput, action, strf("cols %llu must be a multiple of block_size 32", (unsigned long long)cols));
+    if (rows == 0 || batch == 0) return 0;
+    if (!d_w || !d_s || !d_x || !d_y) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    if (rows > 0x7FFFFFFFull || cols > 0x7FFFFFFFull) OBJ_FAIL(kInvalidInput, action, "rows/cols exceed 2^31");
+    const uint32_t r = static_cast<uint32_t>(rows), c = static_cast<uint32_t>(cols);
+    const uint8_t* w = static_cast<const uint8_t*>(d_w);
+    const uint8_t* sc = static_cast<const uint8_t*>(d_s);
+    const bool fast = cols % 64 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(sc) % 2 == 0 && reinterpret_cast<uintptr_t>(d_x) % 16 == 0;
+    const size_t lds_limit = ctx->info.max_shared_memory_per_block > 0
+                                 ? static_cast<size_t>(ctx->info.max_shared_memory_per_block) : 65536;
+    uint64_t done = 0;
+    while (done < batch) {
+        const uint64_t rem = batch - done;
+        const float* xb = d_x + done * cols;
+        float* yb = d_y + done * rows;
+        hipError_t e = hipSuccess;
+        int nt;
+        if (fast) {
+            const uint32_t pairs = c / 64;
+            const size_t per_token = static_cast<size_t>(pairs) * kPad * sizeof(float);
+            nt = max_nt_for_lds(per_token, lds_limit, rem);
+            if (nt == 0) OBJ_FAIL(kUnsupported, action, strf("cols %u exceed the LDS activation stage", c));
+            const uint32_t lpr = pick_lpr(pairs);
+            const int u = nt > 1 ? 1 : pick_u(ctx, r, 64 / lpr);
+            const size_t lds = per_token * nt;
+            switch (nt) {
+                case 8: e = launch_fp4_fast_nt<8>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
+                case 4: e = launch_fp4_fast_nt<4>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
+                case 2: e = launch_fp4_fast_nt<2>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
+                default: e = launch_fp4_fast_nt<1>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
+            }
+        } else {
+            nt = rem >= 8 ? 8 : rem >= 4 ? 4 : rem >= 2 ? 2 : 1;
+            const dim3 grid((r + kWaves - 1) / kWaves);
+            switch (nt) {
+                case 8: hipLaunchKernelGGL((fp4_split_generic<8>), grid, dim3(kThreads), 0, s, w, sc, xb, yb, r, c); break;
+                case 4: hipLaunchKernelGGL((fp4_split_generic<4>), grid, dim3(kThreads), 0, s, w, sc, xb, yb, r, c); break;
+                case 2: hipLaunchKernelGGL((fp4_split_generic<2>), grid, dim3(kThreads), 0, s, w, sc, xb, yb, r, c); break;
+                default: hipLaunchKernelGGL((fp4_split_generic<1>), grid, dim3(kThreads), 0, s, w, sc, xb, yb, r, c); break;
+            }
+            e = hipGetLastError();
+        }
+        if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+        done += static_cast<uint64_t>(nt);
+    }
+    return 0;
+}
+
+}  // namespace objeta
+
+using namespace objeta;
+
+extern "C" {
+
+int32_t objeta_hip_qgemv_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                const void* d_qweights, const float* d_x, float* d_y, uint64_t rows,
+                                uint64_t cols, uint64_t batch) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "qgemv_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    return launch_qgemv(ctx, format, resolve_stream(ctx, stream), d_qweights, d_x, d_y, rows, cols, batch);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_fp4_gemv_split_device(objeta_hip_context* ctx, objeta_hip_stream stream, const void* d_w,
+                                         const void* d_scales, const float* d_x, float* d_y, uint64_t rows,
+                                         uint64_t cols, uint64_t batch) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "fp4_gemv_split_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    return launch_fp4_split(ctx, resolve_stream(ctx, stream), d_w, d_scales, d_x, d_y, rows, cols, batch);
+    OBJ_GUARD_END
+}
+
+// QuantBackend::gemv (quant.rs:256-302) with validate_quant_inputs (quant.rs:751-793).
+int32_t objeta_hip_qgemv(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                         const uint8_t* qweights, uint64_t qweights_len, const float* x, uint64_t x_len,
+                         uint64_t rows, uint64_t cols, float* y, objeta_hip_qgemv_telemetry* tel) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "qgemv"));
+    const int32_t bb = objeta_hip_block_bytes(format);
+    if (bb < 0) OBJ_FAIL(kInvalidInput, "validate format", strf("unknown format %d", format));
+    static const char* labels[] = {"q4_0", "q5_0", "iq3_0", "deepseek_fp4_e2m1"};
+    const char* label = labels[format];
+    if (cols % 32 != 0)
+        OBJ_FAIL(kInvalidInput, strf("validate %s column alignment", label),
+                 strf("cols %llu must be a multiple of block_size 32", (unsigned long long)cols));
+    const uint64_t expected = rows * (cols / 32) * static_cast<uint64_t>(bb);
+    if (qweights_len != expected)
+        OBJ_FAIL(kInvalidInput, strf("validate %s quantized matrix size", label),
+                 strf("qweights len %llu != expected %llu", (unsigned long long)qweights_len,
+                      (unsigned long long)expected));
+    if (x_len != cols)
+        OBJ_FAIL(kInvalidInput, strf("validate %s GEMV vector size", label),
+                 strf("x len %llu != cols %llu", (unsigned long long)x_len, (unsigned long long)cols));
+    if ((rows && !y) || (expected && !qweights) || (cols && !x)) OBJ_FAIL(kInvalidInput, "qgemv", "NULL host pointer");
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    if (rows == 0) {
+        if (tel) *tel = objeta_hip_qgemv_telemetry{};
+        return 0;
+    }
+    void *dq = nullptr, *dx = nullptr, *dy = nullptr;
+    hipEvent_t ev[6] = {};
+    int32_t rc = 0;
+    auto cleanup = [&]() {
+        (void)hipStreamSynchronize(s);
+        if (dq) (void)hipFree(dq);
+        if (dx) (void)hipFree(dx);
+        if (dy) (void)hipFree(dy);
+        for (auto& e : ev) if (e) (void)hipEventDestroy(e);
+    };
+    do {
+        hipError_t e = hipSuccess;
+        for (auto& v : ev) if (e == hipSuccess) e = hipEventCreate(&v);
+        if (e == hipSuccess) e = hipMalloc(&dq, expected ? expected : 4);
+        if (e == hipSuccess) e = hipMalloc(&dx, cols * sizeof(float) + 16);
+        if (e == hipSuccess) e = hipMalloc(&dy, rows * sizeof(float));
+        if (e != hipSuccess) { rc = set_error(kDriver, __FILE__, __LINE__, __func__, "allocate GEMV buffers", hipGetErrorString(e)); break; }
+        e = hipEventRecord(ev[0], s);                                        // total start
+        if (e == hipSuccess) e = hipEventRecord(ev[1], s);                   // h2d start
+        if (e == hipSuccess) e = hipMemcpyAsync(dq, qweights, expected, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(dx, x, cols * sizeof(float), hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipEventRecord(ev[2], s);                   // h2d end / kernel start
+        if (e != hipSuccess) { rc = set_error(kDriver, __FILE__, __LINE__, __func__, strf("%s_h2d", label), hipGetErrorString(e)); break; }
+        rc = launch_qgemv(ctx, format, s, dq, static_cast<const float*>(dx), static_cast<float*>(dy), rows, cols, 1);
+        if (rc) break;
+        e = hipEventRecord(ev[3], s);                                        // kernel end / d2h start
+        if (e == hipSuccess) e = hipMemcpyAsync(y, dy, rows * sizeof(float), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipEventRecord(ev[4], s);                   // d2h end
+        if (e == hipSuccess) e = hipEventRecord(ev[5], s);                   // total end
+        if (e == hipSuccess) e = hipEventSynchronize(ev[5]);
+        if (e != hipSuccess) { rc = set_error(kDriver, __FILE__, __LINE__, __func__, strf("%s_d2h", label), hipGetErrorString(e)); break; }
+        if (tel) {
+            float h2d = 0, ker = 0, d2h = 0, tot = 0;
+            (void)hipEventElapsedTime(&h2d, ev[1], ev[2]);
+            (void)hipEventElapsedTime(&ker, ev[2], ev[3]);
+            (void)hipEventElapsedTime(&d2h, ev[3], ev[4]);
+            (void)hipEventElapsedTime(&tot, ev[0], ev[5]);
+            tel->h2d_ms = h2d;
+            tel->kernel_ms = ker;
+            tel->d2h_ms = d2h;
+            tel->total_ms = tot;
+            const float un = tot - h2d - ker - d2h;
+            tel->unaccounted_ms = un > 0.f ? un : 0.f;
+            tel->bytes_read = expected + cols * sizeof(float);
+            tel->effective_gbps = ker > 0.f ? static_cast<float>(tel->bytes_read) / (ker / 1000.0f) / 1.0e9f : 0.f;
+        }
+    } while (false);
+    cleanup();
+    return rc;
+    OBJ_GUARD_END
+}
+
+}  // extern "C"

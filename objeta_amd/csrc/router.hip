@@ -1,0 +1,271 @@
+// router.hip — router logits, softmax and top-k on gfx950.
+//
+// Reference semantics: cpu_router (crates/objeta-cuda/src/bin/
+// deepseek_single_layer_moe.rs:687-743) computes each logit as a *sequential*
+// fp32 sum of rounded products, takes a softmax over all experts and a stable
+// descending sort (ties keep the lower expert id); the k selected probabilities
+// are then renormalised (crates/objeta-qwen36-executor/src/moe_dispatch.rs:403-435).
+//
+// A sequential 2048-term sum per expert is a ~2048-deep dependency chain, far
+// too slow for the decode critical path. Instead each wave computes one expert's
+// exact sum S of the rounded products in double precision together with a
+// rigorous bound B on |S - sequential fp32 sum| (Higham's recursive-summation
+// bound u * sum_k |S_k| / (1 - n u), with the prefix sums S_k from a wave scan).
+// The last workgroup of a token ranks the experts; if every decision the top-k
+// depends on is separated by more than the bounds, the ids are provably those of
+// the sequential sums. Otherwise it recomputes every logit in the reference's
+// sequential order (one lane per expert) and ranks those exact values.
+#include "device_common.hpp"
+#include "host_common.hpp"
+#include "kernels.hpp"
+
+namespace objeta {
+namespace {
+
+constexpr int kRThreads = 256;
+constexpr int kRWaves = kRThreads / 64;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopK = 32;
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Inclusive scan over the wave (Hillis-Steele; exact enough in double).
+__device__ __forceinline__ double wave_scan_d(double v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const double o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+// Ranks n values (descending, lower index first on ties) and writes the ids of
+// the first `want` into sel[]. Values live in LDS.
+__device__ void rank_select(const float* vals, int n, int want, int* sel) {
+    for (int e = threadIdx.x; e < n; e += kRThreads) {
+        const float v = vals[e];
+        int r = 0;
+        for (int j = 0; j < n; ++j) {
+            const float o = vals[j];
+            r += (o > v) || (o == v && j < e);
+        }
+        if (r < want) sel[r] = e;
+    }
+}
+
+__device__ float block_max(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int w = 1; w < kRWaves; ++w) m = fmaxf(m, red[w]);
+    __syncthreads();
+    return m;
+}
+
+__device__ float block_sum(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+    for (int w = 1; w < kRWaves; ++w) s += red[w];
+    __syncthreads();
+    return s;
+}
+
+// grid = (ceil(E / 4), T). Wave w of block b handles expert b*4 + w of token y.
+__global__ __launch_bounds__(kRThreads) void router_kernel(
+    const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
+    uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
+    float* __restrict__ weights, float* __restrict__ ws_logit, float* __restrict__ ws_bound,
+    uint32_t* __restrict__ counters) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t e = blockIdx.x * kRWaves + (threadIdx.x >> 6);
+    const float* xt = x + static_cast<size_t>(t) * hidden;
+
+    if (e < n_experts) {
+        const float* row = w_r + static_cast<size_t>(e) * hidden;
+        // Lane owns the contiguous chunk [c0, c1) of the sequential order.
+        const uint32_t chunk = (hidden + 63) / 64;
+        const uint32_t c0 = lane * chunk < hidden ? lane * chunk : hidden;
+        const uint32_t c1 = c0 + chunk < hidden ? c0 + chunk : hidden;
+        double local = 0.0;
+        for (uint32_t h = c0; h < c1; ++h) local += static_cast<double>(__fmul_rn(row[h], xt[h]));
+        const double incl = wave_scan_d(local, lane);
+        const double base = incl - local;
+        double abs_prefix = 0.0;
+        double run = base;
+        for (uint32_t h = c0; h < c1; ++h) {
+            run += static_cast<double>(__fmul_rn(row[h], xt[h]));
+            abs_prefix += fabs(run);
+        }
+        abs_prefix = wave_sum_d(abs_prefix);
+        const double total = __shfl(incl, 63, 64);
+        if (lane == 0) {
+            const double b = bias ? static_cast<double>(bias[e]) : 0.0;
+            const float lhat = static_cast<float>(total + b);
+            const double u = 5.9604644775390625e-08;  // 2^-24
+            const double n = static_cast<double>(hidden);
+            double bound = u * abs_prefix / (1.0 - n * u);
+            bound += u * (fabs(total + b) + fabs(static_cast<double>(lhat))) * 1.0001;
+            bound += 1e-12 * abs_prefix + 1e-30;
+            ws_logit[static_cast<size_t>(t) * n_experts + e] = lhat;
+            ws_bound[static_cast<size_t>(t) * n_experts + e] = static_cast<float>(bound * 1.0001);
+        }
+    }
+
+    __shared__ uint32_t s_ticket;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_ticket = atomicAdd(&counters[t], 1u);
+    __syncthreads();
+    if (s_ticket != gridDim.x - 1) return;
+    __threadfence();
+
+    // ---- last workgroup of token t: select
+    __shared__ float s_val[kMaxExperts];
+    __shared__ float s_bnd[kMaxExperts];
+    __shared__ int s_sel[kMaxTopK + 1];
+    __shared__ float s_red[kRWaves];
+    __shared__ int s_uncertain;
+    const uint32_t want = k + 1 <= n_experts ? k + 1 : n_experts;
+    const volatile float* lg = ws_logit + static_cast<size_t>(t) * n_experts;
+    const volatile float* bd = ws_bound + static_cast<size_t>(t) * n_experts;
+    for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) {
+        s_val[j] = lg[j];
+        s_bnd[j] = bd[j];
+    }
+    if (threadIdx.x == 0) s_uncertain = 0;
+    __syncthreads();
+    rank_select(s_val, static_cast<int>(n_experts), static_cast<int>(want), s_sel);
+    __syncthreads();
+
+    // Certainty: consecutive selected logits must be separated beyond their bounds
+    // plus a margin that keeps their softmax probabilities distinct after rounding,
+    // and the k-th selected must beat every unselected expert likewise.
+    float mx = -INFINITY;
+    for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) mx = fmaxf(mx, s_val[j]);
+    mx = block_max(mx, s_red);
+    const float kmin_lo = s_val[s_sel[k - 1]] - s_bnd[s_sel[k - 1]];
+    for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) {
+        bool sel = false;
+        for (uint32_t r = 0; r < k; ++r) sel |= (s_sel[r] == static_cast<int>(j));
+        if (!sel) {
+            const float margin = 9.5367431640625e-07f * (1.0f + fabsf(s_val[j] - mx) + fabsf(s_val[s_sel[k - 1]] - mx));
+            if (!(s_val[j] + s_bnd[j] + margin < kmin_lo)) s_uncertain = 1;
+        }
+    }
+    if (threadIdx.x < k - 1) {
+        const int a = s_sel[threadIdx.x], b = s_sel[threadIdx.x + 1];
+        const float margin = 9.5367431640625e-07f * (1.0f + fabsf(s_val[a] - mx) + fabsf(s_val[b] - mx));
+        if (!(s_val[a] - s_bnd[a] > s_val[b] + s_bnd[b] + margin)) s_uncertain = 1;
+    }
+    __syncthreads();
+
+    __shared__ float s_sum_exp;
+    if (s_uncertain) {
+        // Reference order throughout (cpu_router): logits[e] = sum_h fl(W[e,h] * x[h])
+        // accumulated left to right in fp32 (+ bias); probs = exp(l - max) / sum with
+        // the sum taken in expert order; stable descending sort of the probs. exp is
+        // evaluated in double and rounded once, which agrees with glibc's expf on all
+        // but ~0.03% of arguments (only a probability tie could expose that).
+        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) {
+            const float* row = w_r + static_cast<size_t>(j) * hidden;
+            float s = 0.0f;
+            for (uint32_t h = 0; h < hidden; ++h) s = __fadd_rn(s, __fmul_rn(row[h], xt[h]));
+            if (bias) s = __fadd_rn(s, bias[j]);
+            s_val[j] = s;
+        }
+        __syncthreads();
+        mx = -INFINITY;
+        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) mx = fmaxf(mx, s_val[j]);
+        mx = block_max(mx, s_red);
+        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads)
+            s_bnd[j] = static_cast<float>(exp(static_cast<double>(__fsub_rn(s_val[j], mx))));
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float sum = 0.0f;
+            for (uint32_t j = 0; j < n_experts; ++j) sum = __fadd_rn(sum, s_bnd[j]);
+            s_sum_exp = sum;
+        }
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) s_bnd[j] = __fdiv_rn(s_bnd[j], s_sum_exp);
+        __syncthreads();
+        rank_select(s_bnd, static_cast<int>(n_experts), static_cast<int>(want), s_sel);
+        __syncthreads();
+    } else {
+        float part = 0.0f;
+        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads)
+            part += static_cast<float>(exp(static_cast<double>(s_val[j] - mx)));
+        const float tot = block_sum(part, s_red);
+        if (threadIdx.x == 0) s_sum_exp = tot;
+        __syncthreads();
+    }
+
+    // the k selected probabilities, renormalised in selection order
+    const float sum_exp = s_sum_exp;
+    if (threadIdx.x == 0) {
+        float p[kMaxTopK];
+        float sel_sum = 0.0f;
+        for (uint32_t r = 0; r < k; ++r) {
+            const float ev = static_cast<float>(exp(static_cast<double>(__fsub_rn(s_val[s_sel[r]], mx))));
+            p[r] = __fdiv_rn(ev, sum_exp);
+            sel_sum = __fadd_rn(sel_sum, p[r]);
+        }
+        for (uint32_t r = 0; r < k; ++r) {
+            ids[static_cast<size_t>(t) * k + r] = static_cast<uint32_t>(s_sel[r]);
+            weights[static_cast<size_t>(t) * k + r] = renormalize ? __fdiv_rn(p[r], sel_sum) : p[r];
+        }
+        counters[t] = 0u;  // ready for the next launch
+    }
+}
+
+}  // namespace
+
+int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, const float* bias,
+                      const float* x, uint64_t n_tokens, uint64_t n_experts, uint64_t hidden, uint64_t k,
+                      int32_t renormalize, uint32_t* ids, float* weights, float* ws_logit, float* ws_bound) {
+    const char* action = "launch router_topk";
+    if (n_experts == 0 || n_experts > kMaxExperts)
+        OBJ_FAIL(kInvalidInput, action, strf("num_experts %llu must be in 1..=%d", (unsigned long long)n_experts, kMaxExperts));
+    if (k == 0 || k > n_experts || k > kMaxTopK)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("top_k %llu must be in 1..=min(num_experts, %d)", (unsigned long long)k, kMaxTopK));
+    if (hidden == 0 || hidden > (1u << 24)) OBJ_FAIL(kInvalidInput, action, "hidden must be in 1..=2^24");
+    if (n_tokens == 0) return 0;
+    if (n_tokens > ctx->counter_words) OBJ_FAIL(kInvalidInput, action, strf("n_tokens > %zu", ctx->counter_words));
+    if (!w_r || !x || !ids || !weights) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    const dim3 grid(static_cast<uint32_t>((n_experts + kRWaves - 1) / kRWaves), static_cast<uint32_t>(n_tokens));
+    hipLaunchKernelGGL(router_kernel, grid, dim3(kRThreads), 0, s, w_r, bias, x, static_cast<uint32_t>(n_experts),
+                       static_cast<uint32_t>(hidden), static_cast<uint32_t>(k), renormalize, ids, weights, ws_logit,
+                       ws_bound, ctx->counters);
+    OBJ_HIP(hipGetLastError(), action);
+    return 0;
+}
+
+}  // namespace objeta
+
+using namespace objeta;
+
+extern "C" int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                                 const float* d_w_r, const float* d_bias, const float* d_x,
+                                                 uint64_t n_tokens, uint64_t n_experts, uint64_t hidden,
+                                                 uint64_t k, int32_t renormalize, uint32_t* d_ids,
+                                                 float* d_weights) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "router_topk_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    const size_t need = static_cast<size_t>(n_tokens) * n_experts * 2 * sizeof(float);
+    OBJ_TRY(ensure_workspace(ctx, s, need));
+    float* wl = static_cast<float*>(ctx->ws.ptr);
+    float* wb = wl + static_cast<size_t>(n_tokens) * n_experts;
+    return launch_router(ctx, s, d_w_r, d_bias, d_x, n_tokens, n_experts, hidden, k, renormalize, d_ids,
+                         d_weights, wl, wb);
+    OBJ_GUARD_END
+}

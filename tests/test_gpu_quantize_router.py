@@ -1,0 +1,123 @@
+"""Device quantizer, generators and router against the CPU oracle (bit-exact bytes,
+bit-exact expert ids)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from objeta_amd import QGemvShape, QuantFormat, check
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _special_matrix(rows, cols, seed):
+    m = orc.gauss(rows * cols, seed, 0.02).copy()
+    blocks = m.reshape(-1, 32)
+    blocks[1] = 0.0                                   # zero block
+    blocks[2, 5] = np.nan                             # NaN ignored by amax, q = 0
+    blocks[3, 7] = np.inf                             # inf scale
+    blocks[4] = np.float32(1e-41)                     # subnormals
+    blocks[5] = np.linspace(-7, 7, 32).astype(np.float32)       # scale exactly 1 -> ties
+    blocks[6] = (np.arange(32) - 15.5).astype(np.float32) / 2   # .25 steps
+    blocks[7, 0] = 6.0 * np.float32(2.0 ** -20) * np.float32(1 + 2 ** -23)  # FP4 exponent edge
+    return m
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("rows,cols,seed", [(16, 32, 1), (64, 256, 2), (768, 2048, 3)])
+def test_device_quantizer_bytes_equal_cpu(quant, fmt, rows, cols, seed):
+    m = _special_matrix(rows, cols, seed)
+    got = quant.quantize_matrix(QuantFormat(fmt), m, QGemvShape.new(QuantFormat(fmt), rows, cols))
+    assert np.array_equal(got, orc.quantize_matrix(fmt, m, rows, cols))
+
+
+@pytest.mark.parametrize("seed", [0, 42])
+def test_device_quantizer_reference_lcg_data(quant, seed):
+    # the reference's own test data recipe (seeded_f32s, quant.rs:1610-1662)
+    rows, cols = 128, 256
+    m = orc.seeded_f32s(rows * cols, seed ^ 0xA5A5_5A5A_1234_5678)
+    for fmt in range(4):
+        got = quant.quantize_matrix(QuantFormat(fmt), m, QGemvShape.new(QuantFormat(fmt), rows, cols))
+        assert np.array_equal(got, orc.quantize_matrix(fmt, m, rows, cols))
+
+
+def test_gauss_generators_bit_exact(backend):
+    L = backend.L
+    n = 1 << 16
+    d = backend.alloc(n * 4)
+    check(L.objeta_hip_fill_gauss_device(backend.ctx, None, d.addr(), n, 1234, 77, C.c_float(0.02)))
+    assert np.array_equal(d.download(np.float32, n), orc.gauss(n, 1234, 0.02, first=77))
+    rows, cols = 96, 512
+    for fmt in range(4):
+        nb = rows * cols // 32 * orc.BLOCK_BYTES[fmt]
+        dq = backend.alloc(nb)
+        check(L.objeta_hip_fill_gauss_quantized_device(backend.ctx, fmt, None, dq.addr(), rows, cols, 99,
+                                                       C.c_float(0.02)))
+        ref = orc.quantize_matrix(fmt, orc.gauss(rows * cols, 99, 0.02), rows, cols)
+        assert np.array_equal(dq.download(np.uint8, nb), ref)
+
+
+def _router(backend, w, x, bias, ne, hidden, k, tokens, renorm=True):
+    L = backend.L
+    dw = backend.to_device(w)
+    dx = backend.to_device(x)
+    db = backend.to_device(bias) if bias is not None else None
+    ids = backend.alloc(tokens * k * 4)
+    ws = backend.alloc(tokens * k * 4)
+    check(L.objeta_hip_router_topk_device(backend.ctx, None, dw.addr(), db.addr() if db else None, dx.addr(),
+                                          tokens, ne, hidden, k, 1 if renorm else 0, ids.addr(), ws.addr()))
+    return (ids.download(np.uint32, tokens * k).reshape(tokens, k),
+            ws.download(np.float32, tokens * k).reshape(tokens, k))
+
+
+@pytest.mark.parametrize("ne,k,hidden,tokens", [(8, 2, 2048, 16), (128, 8, 2048, 64), (256, 8, 7168, 8),
+                                                 (60, 4, 96, 32), (4, 4, 64, 4), (1000, 32, 128, 3)])
+@pytest.mark.parametrize("use_bias", [False, True])
+def test_router_ids_bit_exact(backend, ne, k, hidden, tokens, use_bias):
+    w = orc.gauss(ne * hidden, ne * 31 + hidden, 0.02)
+    x = orc.gauss(tokens * hidden, 5, 1.0)
+    bias = orc.gauss(ne, 6, 1.0) if use_bias else None
+    ids, ws = _router(backend, w, x, bias, ne, hidden, k, tokens)
+    for t in range(tokens):
+        rid, rw, _, _ = orc.router(w, x[t * hidden:(t + 1) * hidden], ne, hidden, k, bias=bias)
+        assert list(ids[t]) == list(rid), f"token {t}"
+        assert np.allclose(ws[t], rw, rtol=2e-6, atol=1e-7)
+
+
+def test_router_exact_ties_keep_lower_index(backend):
+    ne, hidden, k = 16, 256, 4
+    w = orc.gauss(ne * hidden, 3, 0.02).reshape(ne, hidden).copy()
+    for e in (3, 9, 12):
+        w[e] = 0.5  # identical rows -> exactly tied logits
+    x = np.abs(orc.gauss(hidden, 4, 1.0))
+    ids, _ = _router(backend, w.ravel(), x, None, ne, hidden, k, 1)
+    rid, _, _, _ = orc.router(w.ravel(), x, ne, hidden, k)
+    assert list(ids[0]) == list(rid)
+    assert list(ids[0][:3]) == [3, 9, 12]
+
+
+def test_router_near_ties_take_the_sequential_path(backend):
+    """Rows that differ by one ulp in one weight: the parallel bound cannot separate
+    them, so the kernel must recompute in the reference's sequential order."""
+    ne, hidden, k = 32, 2048, 8
+    base = orc.gauss(hidden, 8, 0.02)
+    w = np.tile(base, (ne, 1)).astype(np.float32)
+    rng = np.random.default_rng(1)
+    for e in range(ne):
+        j = rng.integers(0, hidden)
+        w[e, j] = np.nextafter(w[e, j], np.float32(np.inf) if e % 2 else np.float32(-np.inf))
+    tokens = 8
+    x = orc.gauss(tokens * hidden, 9, 1.0)
+    ids, ws = _router(backend, w.ravel(), x, None, ne, hidden, k, tokens)
+    for t in range(tokens):
+        rid, rw, _, _ = orc.router(w.ravel(), x[t * hidden:(t + 1) * hidden], ne, hidden, k)
+        assert list(ids[t]) == list(rid), f"token {t}"
+        assert np.allclose(ws[t], rw, rtol=2e-6, atol=1e-7)
+
+
+def test_router_validation(backend):
+    from objeta_amd import HipError
+    with pytest.raises(HipError) as e:
+        _router(backend, np.zeros(8 * 64, np.float32), np.zeros(64, np.float32), None, 8, 64, 9, 1)
+    assert e.value.kind == "InvalidInput" and "top_k" in e.value.source_message
