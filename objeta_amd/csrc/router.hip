@@ -175,10 +175,15 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
         // evaluated in double and rounded once, which agrees with glibc's expf on all
         // but ~0.03% of arguments (only a probability tie could expose that).
         for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) {
+            // every product and every add rounds on its own, as in the reference
+#pragma clang fp contract(off)
             const float* row = w_r + static_cast<size_t>(j) * hidden;
             float s = 0.0f;
-            for (uint32_t h = 0; h < hidden; ++h) s = __fadd_rn(s, __fmul_rn(row[h], xt[h]));
-            if (bias) s = __fadd_rn(s, bias[j]);
+            for (uint32_t h = 0; h < hidden; ++h) {
+                const float p = row[h] * xt[h];
+                s = s + p;
+            }
+            if (bias) s = s + bias[j];
             s_val[j] = s;
         }
         __syncthreads();

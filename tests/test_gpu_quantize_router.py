@@ -1,5 +1,10 @@
 """Device quantizer, generators and router against the CPU oracle (bit-exact bytes,
-bit-exact expert ids)."""
+bit-exact expert ids).
+
+Router weights: the device takes each logit from the exact sum of the rounded
+products, the reference from a sequential fp32 sum whose own rounding error is
+~sqrt(hidden) ulps (~3e-6 at hidden 2048); through the softmax that moves a
+weight by up to ~1e-5 relative, hence rtol=2e-5 on the weights (ids are exact)."""
 import ctypes as C
 
 import numpy as np
@@ -82,7 +87,7 @@ def test_router_ids_bit_exact(backend, ne, k, hidden, tokens, use_bias):
     for t in range(tokens):
         rid, rw, _, _ = orc.router(w, x[t * hidden:(t + 1) * hidden], ne, hidden, k, bias=bias)
         assert list(ids[t]) == list(rid), f"token {t}"
-        assert np.allclose(ws[t], rw, rtol=2e-6, atol=1e-7)
+        assert np.allclose(ws[t], rw, rtol=2e-5, atol=1e-6)
 
 
 def test_router_exact_ties_keep_lower_index(backend):
@@ -113,7 +118,7 @@ def test_router_near_ties_take_the_sequential_path(backend):
     for t in range(tokens):
         rid, rw, _, _ = orc.router(w.ravel(), x[t * hidden:(t + 1) * hidden], ne, hidden, k)
         assert list(ids[t]) == list(rid), f"token {t}"
-        assert np.allclose(ws[t], rw, rtol=2e-6, atol=1e-7)
+        assert np.allclose(ws[t], rw, rtol=2e-5, atol=1e-6)
 
 
 def test_router_validation(backend):
