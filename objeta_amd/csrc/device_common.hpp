@@ -36,38 +36,50 @@ __device__ __forceinline__ uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t by
     return __builtin_amdgcn_alignbyte(hi, lo, bytes);
 }
 
-// Loads the kPairDw dwords of a block pair starting at a 4-byte aligned address.
+// Loads N dwords starting at a 4-byte aligned address. Weight bytes are read
+// exactly once per launch, so the loads are non-temporal (they bypass cache
+// retention and leave L2/MALL to the activations).
 template <int N>
 __device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint32_t (&d)[N]) {
     int i = 0;
 #pragma unroll
     for (; i + 4 <= N; i += 4) {
-        u32x4 v = *reinterpret_cast<const u32x4*>(p + i);
+        u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + i));
         d[i] = v.x; d[i + 1] = v.y; d[i + 2] = v.z; d[i + 3] = v.w;
     }
     if constexpr (N % 4 >= 2) {
-        u32x2 v = *reinterpret_cast<const u32x2*>(p + i);
+        u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p + i));
         d[i] = v.x; d[i + 1] = v.y;
         i += 2;
     }
-    if constexpr (N % 2 == 1) d[i] = p[i];
+    if constexpr (N % 2 == 1) d[i] = __builtin_nontemporal_load(p + i);
 }
 
 // ---------------------------------------------------------------- Q4_0
 // 8 weights from one nibble dword n (byte k: weight 2k low nibble, 2k+1 high
 // nibble) against x[0..7] = xa (w0..w3), xb (w4..w7). `lo` accumulates
 // (q-8)*x for w0,w2,w4,w6; `hi` accumulates 16*(q-8)*x for w1,w3,w5,w7.
+// Constants the nibble unpacking combines in one 3-input bit op. gfx9 VOP3
+// encodings cannot carry literals, so the constants are pinned in registers
+// (the empty asm hides their values from constant folding) and the compiler
+// emits v_and_or / v_bitop3 instead of separate v_and + v_or with literals.
+struct NibbleConsts {
+    uint32_t lo_mask, hi_mask, magic;
+    __device__ __forceinline__ NibbleConsts() : lo_mask(0x000F000Fu), hi_mask(0x00F000F0u), magic(0x64006400u) {
+        asm volatile("" : "+v"(lo_mask), "+v"(hi_mask), "+v"(magic));
+    }
+};
+
 template <int NT>
 __device__ __forceinline__ void q4_dot8(uint32_t n, const float4 (&xa)[NT], const float4 (&xb)[NT],
-                                        float (&lo)[NT], float (&hi)[NT]) {
-    const uint32_t magic = 0x64006400u;  // fp16 1024 in both halves
+                                        float (&lo)[NT], float (&hi)[NT], const NibbleConsts& k) {
     const h2 k_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
     const h2 k_hi = {(_Float16)1152.0f, (_Float16)1152.0f};
     uint32_t n8 = n >> 8;
-    h2 a = as_h2((n & 0x000F000Fu) | magic) - k_lo;   // (q0-8, q4-8)
-    h2 b = as_h2((n & 0x00F000F0u) | magic) - k_hi;   // 16*(q1-8, q5-8)
-    h2 c = as_h2((n8 & 0x000F000Fu) | magic) - k_lo;  // (q2-8, q6-8)
-    h2 d = as_h2((n8 & 0x00F000F0u) | magic) - k_hi;  // 16*(q3-8, q7-8)
+    h2 a = as_h2((n & k.lo_mask) | k.magic) - k_lo;   // (q0-8, q4-8)
+    h2 b = as_h2((n & k.hi_mask) | k.magic) - k_hi;   // 16*(q1-8, q5-8)
+    h2 c = as_h2((n8 & k.lo_mask) | k.magic) - k_lo;  // (q2-8, q6-8)
+    h2 d = as_h2((n8 & k.hi_mask) | k.magic) - k_hi;  // 16*(q3-8, q7-8)
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         lo[t] = __builtin_fmaf((float)a.x, xa[t].x, lo[t]);
@@ -149,33 +161,33 @@ __device__ __forceinline__ void iq3_block_dot(uint32_t l0, uint32_t l1, uint32_t
 }
 
 // ------------------------------------------- reference-form block (specials)
-// value index of weight i in a block, as the reference decodes it
-// (quant.rs:951-1019), and the reference's w = value * scale; sum += w * x form.
+// The reference's per-weight form w = value * scale; sum += w * x
+// (quant.rs:928-1019), decoding from the block's dwords already in registers.
 // Used only when a block scale is not finite: there the per-weight products
 // (e.g. 0 * inf = NaN) decide the result, so the factored form must not be used.
+// n[0..3]: the 16 nibble bytes (Q4, Q5) or, for IQ3, n[0..1] the 8 low bytes and
+// n[2] the 4 high bytes; m: Q5 high-bit mask.
 template <int F>
-__device__ __forceinline__ int block_value(const uint8_t* blk, int i) {
+__device__ __forceinline__ int reg_value(const uint32_t (&n)[4], uint32_t m, int i) {
     if constexpr (F == kQ4) {
-        const uint32_t pk = blk[2 + i / 2];
-        return static_cast<int>((i & 1) ? (pk >> 4) : (pk & 15)) - 8;
+        return static_cast<int>((n[i >> 3] >> (4 * (i & 7))) & 15u) - 8;
     } else if constexpr (F == kQ5) {
-        const uint32_t pk = blk[6 + i / 2];
-        const uint32_t lo = (i & 1) ? (pk >> 4) : (pk & 15);
-        const uint32_t hi = (blk[2 + i / 8] >> (i & 7)) & 1u;
-        return static_cast<int>(lo | (hi << 4)) - 16;
+        const uint32_t lo = (n[i >> 3] >> (4 * (i & 7))) & 15u;
+        return static_cast<int>(lo | (((m >> i) & 1u) << 4)) - 16;
     } else {
-        const uint32_t lo = (blk[2 + i / 4] >> (2 * (i & 3))) & 3u;
-        const uint32_t hi = (blk[10 + i / 8] >> (i & 7)) & 1u;
+        const uint32_t lo = (n[i >> 4] >> (2 * (i & 15))) & 3u;
+        const uint32_t hi = (n[2] >> i) & 1u;
         return static_cast<int>(lo | (hi << 2)) - 4;
     }
 }
 
 template <int F, int NT>
-__device__ __noinline__ void block_dot_reference_form(const uint8_t* blk, float scale,
-                                                      const float* const (&xs)[NT], int xoff,
-                                                      float (&acc)[NT]) {
+__device__ __forceinline__ void block_dot_reference_form(const uint32_t (&n)[4], uint32_t m, float scale,
+                                                         const float* const (&xs)[NT], int xoff,
+                                                         float (&acc)[NT]) {
+#pragma unroll 1
     for (int i = 0; i < 32; ++i) {
-        const float w = static_cast<float>(block_value<F>(blk, i)) * scale;
+        const float w = static_cast<float>(reg_value<F>(n, m, i)) * scale;
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = __builtin_fmaf(w, xs[t][xoff + i], acc[t]);
     }
@@ -186,20 +198,33 @@ __device__ __noinline__ void block_dot_reference_form(const uint8_t* blk, float 
 // start `pair`, already loaded into d) with NT activation vectors xs[t][0..63]
 // (LDS or global), adding to acc.
 template <int F, int NT>
-__device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw], const uint8_t* pair,
+__device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw],
                                          const float* const (&xs)[NT], float (&acc)[NT]) {
     {
         const float s0 = f16_to_f32(d[0] & 0xFFFFu);
         const float s1 = F == kQ4 ? f16_to_f32(d[4] >> 16)
                                   : F == kQ5 ? f16_to_f32(d[5] >> 16) : f16_to_f32(d[3] >> 16);
         if (!__builtin_isfinite(s0) || !__builtin_isfinite(s1)) {
-            block_dot_reference_form<F, NT>(pair, s0, xs, 0, acc);
-            block_dot_reference_form<F, NT>(pair + Fmt<F>::kBlockBytes, s1, xs, 32, acc);
+            uint32_t n0[4], n1[4], m0 = 0, m1 = 0;
+            if constexpr (F == kQ4) {
+                for (int j = 0; j < 4; ++j) { n0[j] = alignb(d[j + 1], d[j], 2); n1[j] = d[5 + j]; }
+            } else if constexpr (F == kQ5) {
+                m0 = alignb(d[1], d[0], 2);
+                m1 = d[6];
+                for (int j = 0; j < 4; ++j) { n0[j] = alignb(d[j + 2], d[j + 1], 2); n1[j] = d[7 + j]; }
+            } else {
+                n0[0] = alignb(d[1], d[0], 2); n0[1] = alignb(d[2], d[1], 2); n0[2] = alignb(d[3], d[2], 2);
+                n1[0] = d[4]; n1[1] = d[5]; n1[2] = d[6];
+                n0[3] = n1[3] = 0;
+            }
+            block_dot_reference_form<F, NT>(n0, m0, s0, xs, 0, acc);
+            block_dot_reference_form<F, NT>(n1, m1, s1, xs, 32, acc);
             return;
         }
     }
     if constexpr (F == kQ4) {
         // bytes 0-1 scale0, 2-17 nibbles0, 18-19 scale1, 20-35 nibbles1
+        const NibbleConsts kc;
         const float s0 = f16_to_f32(d[0] & 0xFFFFu);
         const float s1 = f16_to_f32(d[4] >> 16);
 #pragma unroll
@@ -216,7 +241,7 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw], c
                     xa[t] = *reinterpret_cast<const float4*>(xs[t] + blk * 32 + 8 * j);
                     xb[t] = *reinterpret_cast<const float4*>(xs[t] + blk * 32 + 8 * j + 4);
                 }
-                q4_dot8<NT>(n, xa, xb, lo, hi);
+                q4_dot8<NT>(n, xa, xb, lo, hi, kc);
             }
             const float s = blk == 0 ? s0 : s1;
 #pragma unroll

@@ -15,103 +15,13 @@
 // a row with DPP/permute shuffles.
 #include "device_common.hpp"
 #include "host_common.hpp"
+#include "gemv_stream.hpp"
 #include "kernels.hpp"
+
+#include <cstdlib>
 
 namespace objeta {
 namespace dev {
-
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-constexpr int kPad = 68;  // floats per 64-activation pair slot in LDS
-
-// Stages NT activation vectors of `cols` floats into LDS, padded per 64.
-template <int NT>
-__device__ __forceinline__ void stage_x(float* __restrict__ lds, const float* __restrict__ x,
-                                        uint32_t cols, uint32_t pairs) {
-    const uint32_t n4 = NT * cols / 4;
-    for (uint32_t i = threadIdx.x; i < n4; i += kThreads) {
-        const uint32_t t = (i * 4) / cols;
-        const uint32_t c = i * 4 - t * cols;
-        const float4 v = reinterpret_cast<const float4*>(x)[i];
-        float* dst = lds + t * pairs * kPad + (c >> 6) * kPad + (c & 63);
-        *reinterpret_cast<float4*>(dst) = v;
-    }
-}
-
-template <int F, int NT, int U>
-__global__ __launch_bounds__(kThreads) void qgemv_fast(const uint8_t* __restrict__ q,
-                                                       const float* __restrict__ x,
-                                                       float* __restrict__ y, uint32_t rows,
-                                                       uint32_t cols, uint32_t lpr) {
-    extern __shared__ float lds[];
-    const uint32_t pairs = cols >> 6;
-    constexpr int kPairBytes = 2 * Fmt<F>::kBlockBytes;
-    const size_t row_bytes = static_cast<size_t>(pairs) * kPairBytes;
-    stage_x<NT>(lds, x, cols, pairs);
-    __syncthreads();
-
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    const uint32_t g = 64 / lpr;  // row slots per wave
-    const uint32_t slot = lane / lpr;
-    const uint32_t lp = lane - slot * lpr;
-    const bool active = slot < g;
-    const uint32_t row0 = wave * g * U + slot;
-
-    float acc[U][NT];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[u][t] = 0.f;
-
-    if (active) {
-        for (uint32_t p = lp; p < pairs; p += lpr) {
-            uint32_t d[U][Fmt<F>::kPairDw];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t r = row0 + u * g;
-                if (r < rows) {
-                    const uint32_t* src = reinterpret_cast<const uint32_t*>(
-                        q + static_cast<size_t>(r) * row_bytes + static_cast<size_t>(p) * kPairBytes);
-                    load_dwords<Fmt<F>::kPairDw>(src, d[u]);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < Fmt<F>::kPairDw; ++i) d[u][i] = 0;
-                }
-            }
-            const float* xs[NT];
-#pragma unroll
-            for (int t = 0; t < NT; ++t) xs[t] = lds + (t * pairs + p) * kPad;
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                pair_dot<F, NT>(d[u], q + static_cast<size_t>(row0 + u * g) * row_bytes + static_cast<size_t>(p) * kPairBytes,
-                                xs, acc[u]);
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float v = acc[u][t];
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                float o = __shfl_down(v, off, 64);
-                v += (lp + off < lpr) ? o : 0.0f;
-            }
-            acc[u][t] = v;
-        }
-    }
-    if (active && lp == 0) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t r = row0 + u * g;
-            if (r < rows) {
-#pragma unroll
-                for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + r] = acc[u][t];
-            }
-        }
-    }
-}
 
 // Generic path: any cols % 32 == 0 and any alignment, including the interleaved
 // 17-byte FP4 layout. One wave per row, lanes stride over blocks, byte loads.
@@ -167,111 +77,6 @@ __global__ __launch_bounds__(kThreads) void qgemv_generic(const uint8_t* __restr
     }
 }
 
-// DeepSeek split FP4: w [rows][cols/2], scales [rows][cols/32]. Fast path when
-// cols % 64 == 0: a lane owns two blocks (32 nibble bytes + 2 scale bytes).
-template <int NT, int U>
-__global__ __launch_bounds__(kThreads) void fp4_split_fast(const uint8_t* __restrict__ w,
-                                                           const uint8_t* __restrict__ sc,
-                                                           const float* __restrict__ x,
-                                                           float* __restrict__ y, uint32_t rows,
-                                                           uint32_t cols, uint32_t lpr) {
-    extern __shared__ float lds[];
-    const uint32_t pairs = cols >> 6;
-    stage_x<NT>(lds, x, cols, pairs);
-    __syncthreads();
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    const uint32_t g = 64 / lpr;
-    const uint32_t slot = lane / lpr;
-    const uint32_t lp = lane - slot * lpr;
-    const bool active = slot < g;
-    const uint32_t row0 = wave * g * U + slot;
-    const size_t wrow = cols >> 1, srow = cols >> 5;
-
-    float acc[U][NT];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[u][t] = 0.f;
-
-    if (active) {
-        for (uint32_t p = lp; p < pairs; p += lpr) {
-            uint32_t d[U][8];
-            uint32_t s2[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t r = row0 + u * g;
-                if (r < rows) {
-                    load_dwords<8>(reinterpret_cast<const uint32_t*>(w + r * wrow + p * 32), d[u]);
-                    s2[u] = *reinterpret_cast<const uint16_t*>(sc + r * srow + p * 2);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) d[u][i] = 0;
-                    s2[u] = 0;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-#pragma unroll
-                for (int blk = 0; blk < 2; ++blk) {
-                    float a[NT];
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) a[t] = 0.f;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        float4 xa[NT], xb[NT];
-#pragma unroll
-                        for (int t = 0; t < NT; ++t) {
-                            const float* xs = lds + (t * pairs + p) * kPad + blk * 32 + 8 * j;
-                            xa[t] = *reinterpret_cast<const float4*>(xs);
-                            xb[t] = *reinterpret_cast<const float4*>(xs + 4);
-                        }
-                        fp4_dot8<NT>(d[u][blk * 4 + j], xa, xb, a);
-                    }
-                    const float scale = e8m0_to_f32((s2[u] >> (8 * blk)) & 0xFFu);
-                    if (__builtin_isfinite(scale)) {
-#pragma unroll
-                        for (int t = 0; t < NT; ++t)
-                            acc[u][t] = __builtin_fmaf(scale, a[t] * 16384.0f, acc[u][t]);
-                    } else {
-                        // reference form w = table[q] * scale per weight (deepseek.rs:866-918)
-                        for (int i = 0; i < 32; ++i) {
-                            const uint32_t c = (d[u][blk * 4 + i / 8] >> (4 * (i & 7))) & 15u;
-                            const float wv = f16_to_f32(((c & 7u) << 9) | ((c & 8u) << 12)) * 16384.0f * scale;
-#pragma unroll
-                            for (int t = 0; t < NT; ++t)
-                                acc[u][t] = __builtin_fmaf(wv, lds[(t * pairs + p) * kPad + blk * 32 + i], acc[u][t]);
-                        }
-                    }
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float v = acc[u][t];
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                float o = __shfl_down(v, off, 64);
-                v += (lp + off < lpr) ? o : 0.0f;
-            }
-            acc[u][t] = v;
-        }
-    }
-    if (active && lp == 0) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t r = row0 + u * g;
-            if (r < rows) {
-#pragma unroll
-                for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + r] = acc[u][t];
-            }
-        }
-    }
-}
-
 template <int NT>
 __global__ __launch_bounds__(kThreads) void fp4_split_generic(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ sc,
@@ -312,49 +117,59 @@ namespace {
 
 using namespace dev;
 
-uint32_t pick_lpr(uint32_t pairs) { return pairs >= 64 ? 64u : pairs; }
+constexpr int kStreamWgsPerCu = 4;  // resident workgroups per CU for the streaming GEMV
 
-// Rows per wave pass for the fast kernels.
-int pick_u(const objeta_hip_context* ctx, uint32_t rows, uint32_t g) {
+// Persistent grid: enough workgroups to cover every group once, capped at
+// `per_cu` workgroups per compute unit so that each wave streams several items.
+template <typename K>
+uint32_t grid_for_stream(const objeta_hip_context* ctx, K kernel, size_t lds, uint32_t n_groups) {
     const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
-    const uint32_t rows_per_wg_u1 = g * kWaves;
-    const uint32_t wgs_u4 = (rows + rows_per_wg_u1 * 4 - 1) / (rows_per_wg_u1 * 4);
-    const uint32_t wgs_u2 = (rows + rows_per_wg_u1 * 2 - 1) / (rows_per_wg_u1 * 2);
-    if (wgs_u4 >= 2 * cus) return 4;
-    if (wgs_u2 >= 2 * cus) return 2;
-    return 1;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    int want = kStreamWgsPerCu;
+#ifdef OBJETA_TUNE
+    if (const char* e = getenv("OBJETA_TUNE_WGS_PER_CU")) want = atoi(e);
+#endif
+    if (per_cu > want) per_cu = want;
+    const uint32_t need = (n_groups + kWaves - 1) / kWaves;
+    const uint32_t cap = cus * static_cast<uint32_t>(per_cu);
+    return need < cap ? need : cap;
 }
 
-template <int F, int NT>
-hipError_t launch_fast_nt(hipStream_t s, const uint8_t* q, const float* x, float* y, uint32_t rows,
-                          uint32_t cols, int u, uint32_t lpr, size_t lds) {
+template <class R, int NT, int U>
+hipError_t launch_stream_u(const objeta_hip_context* ctx, hipStream_t s, const R& rm, const float* x, float* y,
+                           uint32_t rows, uint32_t cols, uint32_t lpr, size_t lds) {
     const uint32_t g = 64 / lpr;
-    const uint32_t per_wg = g * kWaves * static_cast<uint32_t>(u);
-    const dim3 grid((rows + per_wg - 1) / per_wg);
-    if constexpr (NT == 1) {
-        if (u == 4) hipLaunchKernelGGL((qgemv_fast<F, 1, 4>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
-        else if (u == 2) hipLaunchKernelGGL((qgemv_fast<F, 1, 2>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
-        else hipLaunchKernelGGL((qgemv_fast<F, 1, 1>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
-    } else {
-        hipLaunchKernelGGL((qgemv_fast<F, NT, 1>), grid, dim3(kThreads), lds, s, q, x, y, rows, cols, lpr);
-    }
+    const uint32_t n_groups = (rows + g * U - 1) / (g * U);
+    auto kern = gemv_stream<R, NT, U>;
+    const uint32_t grid = grid_for_stream(ctx, kern, lds, n_groups);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, s, rm, x, y, rows, cols, lpr, n_groups);
     return hipGetLastError();
 }
 
-template <int NT>
-hipError_t launch_fp4_fast_nt(hipStream_t s, const uint8_t* w, const uint8_t* sc, const float* x, float* y,
-                              uint32_t rows, uint32_t cols, int u, uint32_t lpr, size_t lds) {
-    const uint32_t g = 64 / lpr;
-    const uint32_t per_wg = g * kWaves * static_cast<uint32_t>(u);
-    const dim3 grid((rows + per_wg - 1) / per_wg);
+// Rows per wave item: 2 when the matrix has enough rows to keep every resident
+// wave busy, else 1 (more, smaller items).
+template <class R, int NT>
+hipError_t launch_stream(const objeta_hip_context* ctx, hipStream_t s, const R& rm, const float* x, float* y,
+                         uint32_t rows, uint32_t cols, uint32_t lpr, size_t lds) {
     if constexpr (NT == 1) {
-        if (u == 4) hipLaunchKernelGGL((fp4_split_fast<1, 4>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
-        else if (u == 2) hipLaunchKernelGGL((fp4_split_fast<1, 2>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
-        else hipLaunchKernelGGL((fp4_split_fast<1, 1>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
+        const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+        const uint32_t g = 64 / lpr;
+        const uint32_t groups_u2 = (rows + 2 * g - 1) / (2 * g);
+        uint32_t min_groups = cus * kWaves * kStreamWgsPerCu;
+#ifdef OBJETA_TUNE
+        if (const char* e = getenv("OBJETA_TUNE_U")) {
+            if (atoi(e) == 2) return launch_stream_u<R, 1, 2>(ctx, s, rm, x, y, rows, cols, lpr, lds);
+            return launch_stream_u<R, 1, 1>(ctx, s, rm, x, y, rows, cols, lpr, lds);
+        }
+#endif
+        (void)groups_u2;
+        (void)min_groups;
+        return launch_stream_u<R, 1, 1>(ctx, s, rm, x, y, rows, cols, lpr, lds);
     } else {
-        hipLaunchKernelGGL((fp4_split_fast<NT, 1>), grid, dim3(kThreads), lds, s, w, sc, x, y, rows, cols, lpr);
+        return launch_stream_u<R, NT, 1>(ctx, s, rm, x, y, rows, cols, lpr, lds);
     }
-    return hipGetLastError();
 }
 
 template <int F>
@@ -391,9 +206,8 @@ int32_t launch_qgemv(objeta_hip_context* ctx, int32_t format, hipStream_t s, con
     const uint32_t r = static_cast<uint32_t>(rows), c = static_cast<uint32_t>(cols);
     const uint8_t* q = static_cast<const uint8_t*>(d_q);
     const bool aligned = (reinterpret_cast<uintptr_t>(q) % 4 == 0) && (reinterpret_cast<uintptr_t>(d_x) % 16 == 0);
-    const bool fast = format != OBJETA_HIP_FP4_E2M1 && cols % 64 == 0 && aligned;
-    const size_t lds_limit = ctx->info.max_shared_memory_per_block > 0
-                                 ? static_cast<size_t>(ctx->info.max_shared_memory_per_block) : 65536;
+    const bool fast = format != OBJETA_HIP_FP4_E2M1 && cols % 64 == 0 && aligned && pick_lpr(c / 64) != 0;
+    const size_t lds_limit = 65536;  // at most 64 KB of staged activations per workgroup
     uint64_t done = 0;
     while (done < batch) {
         const uint64_t rem = batch - done;
@@ -403,22 +217,31 @@ int32_t launch_qgemv(objeta_hip_context* ctx, int32_t format, hipStream_t s, con
         int nt;
         if (fast) {
             const uint32_t pairs = c / 64;
+            uint32_t lpr = pick_lpr(pairs);
+#ifdef OBJETA_TUNE
+            if (const char* e = getenv("OBJETA_TUNE_LPR")) {
+                const uint32_t l = static_cast<uint32_t>(atoi(e));
+                if (l && pairs % l == 0 && l <= 64) lpr = l;
+            }
+#endif
             const size_t per_token = static_cast<size_t>(pairs) * kPad * sizeof(float);
             nt = max_nt_for_lds(per_token, lds_limit, rem);
             if (nt == 0) OBJ_FAIL(kUnsupported, action, strf("cols %u exceed the LDS activation stage", c));
-            const uint32_t lpr = pick_lpr(pairs);
-            const int u = nt > 1 ? 1 : pick_u(ctx, r, 64 / lpr);
-            const size_t lds = per_token * nt;
+            const size_t lds = per_token * nt + 4 * sizeof(float);
+            const size_t row_bytes = static_cast<size_t>(c / 32) * static_cast<size_t>(objeta_hip_block_bytes(format));
 #define OBJ_FAST(F)                                                                              \
-    switch (nt) {                                                                                \
-        case 8: e = launch_fast_nt<F, 8>(s, q, xb, yb, r, c, u, lpr, lds); break;                 \
-        case 4: e = launch_fast_nt<F, 4>(s, q, xb, yb, r, c, u, lpr, lds); break;                 \
-        case 2: e = launch_fast_nt<F, 2>(s, q, xb, yb, r, c, u, lpr, lds); break;                 \
-        default: e = launch_fast_nt<F, 1>(s, q, xb, yb, r, c, u, lpr, lds); break;                \
+    {                                                                                            \
+        const QRows<F> rm{q, row_bytes};                                                         \
+        switch (nt) {                                                                            \
+            case 8: e = launch_stream<QRows<F>, 8>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;   \
+            case 4: e = launch_stream<QRows<F>, 4>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;   \
+            case 2: e = launch_stream<QRows<F>, 2>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;   \
+            default: e = launch_stream<QRows<F>, 1>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;  \
+        }                                                                                        \
     }
-            if (format == OBJETA_HIP_Q4_0) { OBJ_FAST(kQ4) }
-            else if (format == OBJETA_HIP_Q5_0) { OBJ_FAST(kQ5) }
-            else { OBJ_FAST(kIQ3) }
+            if (format == OBJETA_HIP_Q4_0) OBJ_FAST(kQ4)
+            else if (format == OBJETA_HIP_Q5_0) OBJ_FAST(kQ5)
+            else OBJ_FAST(kIQ3)
 #undef OBJ_FAST
         } else {
             nt = rem >= 8 ? 8 : rem >= 4 ? 4 : rem >= 2 ? 2 : 1;
@@ -446,10 +269,9 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
     const uint32_t r = static_cast<uint32_t>(rows), c = static_cast<uint32_t>(cols);
     const uint8_t* w = static_cast<const uint8_t*>(d_w);
     const uint8_t* sc = static_cast<const uint8_t*>(d_s);
-    const bool fast = cols % 64 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+    const bool fast = cols % 64 == 0 && pick_lpr(c / 64) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(sc) % 2 == 0 && reinterpret_cast<uintptr_t>(d_x) % 16 == 0;
-    const size_t lds_limit = ctx->info.max_shared_memory_per_block > 0
-                                 ? static_cast<size_t>(ctx->info.max_shared_memory_per_block) : 65536;
+    const size_t lds_limit = 65536;  // at most 64 KB of staged activations per workgroup
     uint64_t done = 0;
     while (done < batch) {
         const uint64_t rem = batch - done;
@@ -459,17 +281,17 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
         int nt;
         if (fast) {
             const uint32_t pairs = c / 64;
+            const uint32_t lpr = pick_lpr(pairs);
             const size_t per_token = static_cast<size_t>(pairs) * kPad * sizeof(float);
             nt = max_nt_for_lds(per_token, lds_limit, rem);
             if (nt == 0) OBJ_FAIL(kUnsupported, action, strf("cols %u exceed the LDS activation stage", c));
-            const uint32_t lpr = pick_lpr(pairs);
-            const int u = nt > 1 ? 1 : pick_u(ctx, r, 64 / lpr);
-            const size_t lds = per_token * nt;
+            const size_t lds = per_token * nt + 4 * sizeof(float);
+            const Fp4Rows rm{w, sc, static_cast<size_t>(c / 2), static_cast<size_t>(c / 32)};
             switch (nt) {
-                case 8: e = launch_fp4_fast_nt<8>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
-                case 4: e = launch_fp4_fast_nt<4>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
-                case 2: e = launch_fp4_fast_nt<2>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
-                default: e = launch_fp4_fast_nt<1>(s, w, sc, xb, yb, r, c, u, lpr, lds); break;
+                case 8: e = launch_stream<Fp4Rows, 8>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
+                case 4: e = launch_stream<Fp4Rows, 4>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
+                case 2: e = launch_stream<Fp4Rows, 2>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
+                default: e = launch_stream<Fp4Rows, 1>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
             }
         } else {
             nt = rem >= 8 ? 8 : rem >= 4 ? 4 : rem >= 2 ? 2 : 1;
