@@ -226,6 +226,73 @@ int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta_hip_stream
                                       uint64_t k, int32_t renormalize, uint32_t* d_ids,
                                       float* d_weights);
 
+/* --------------------------------------------------------------- MoE path */
+/* Device addresses of one expert's projections: ExpertWeights (moe.rs:13-18) for
+ * the block formats, DeepSeekFp4ExpertWeights (moe.rs:27-35) for FP4. gate and up
+ * are [intermediate][hidden] matrices, down is [out_dim][intermediate]. With
+ * format OBJETA_HIP_FP4_E2M1 the MoE entry points read the split FP4 layout of
+ * execute_selected_moe_native_fp4_cuda (moe.rs:816-1280): gate/up/down hold the
+ * nibbles [rows][cols/2] and *_scale the E8M0 bytes [rows][cols/32]. For block
+ * formats the *_scale fields are ignored. */
+typedef struct {
+    const void* gate;
+    const void* up;
+    const void* down;
+    const void* gate_scale;
+    const void* up_scale;
+    const void* down_scale;
+} objeta_hip_expert_ptrs;
+
+/* The per-expert kernels of execute_selected_moe_cuda (moe.rs:587-652) fused and
+ * batched over tokens, all on the device. For token t and selection slot j the
+ * expert is e = d_ids[t*k + j], an index into d_table (n_table entries; NULL
+ * d_ids means e = t*k + j), and
+ *   act_j  = silu(gate_e x_t) * (up_e x_t)          silu_mul (moe.cu:2-22)
+ *   out_t  = residual_t + sum_j d_weights[t*k + j] * (down_e act_j)
+ * with the sum taken in slot order (weighted_accum, moe.cu:24-34). swiglu_limit
+ * > 0 applies the reference's clamp (up to [-L, L], gate to <= L). d_residual NULL
+ * means zero (the reference's zero-initialised out); d_out may alias d_residual
+ * and d_x. An expert id >= n_table makes that slot contribute NaN and sets the
+ * context's device error word (objeta_hip_device_error). Allocates nothing after
+ * the first call with a given size; graph-capturable. d_x [n_tokens][hidden],
+ * d_out/d_residual [n_tokens][out_dim] f32. */
+int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                       const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                       const uint32_t* d_ids, const float* d_weights, uint64_t n_tokens,
+                                       uint64_t k, const float* d_x, const float* d_residual, float* d_out,
+                                       uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                       float swiglu_limit);
+
+/* The two launches of objeta_hip_moe_selected_device, for callers that keep the
+ * activations: d_act [n_tokens*k][intermediate] f32 (16-byte aligned) receives
+ * silu(gate x) * (up x) per (token, slot); the down phase combines them. */
+int32_t objeta_hip_moe_gate_up_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                      const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                      const uint32_t* d_ids, uint64_t n_tokens, uint64_t k, const float* d_x,
+                                      float* d_act, uint64_t hidden, uint64_t intermediate, float swiglu_limit);
+int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                   const objeta_hip_expert_ptrs* d_table, uint64_t n_table, const uint32_t* d_ids,
+                                   const float* d_weights, uint64_t n_tokens, uint64_t k, const float* d_act,
+                                   const float* d_residual, float* d_out, uint64_t intermediate, uint64_t out_dim);
+
+/* One MoE layer on the device: the router of objeta_hip_router_topk_device over
+ * d_router_w [n_experts][hidden] (+ d_router_bias) writes d_ids_out/d_weights_out
+ * [n_tokens][k], then objeta_hip_moe_selected_device runs the selected experts of
+ * d_table (n_experts entries). No host synchronisation; graph-capturable. No
+ * reference counterpart as one call: the reference routes on the host
+ * (deepseek_single_layer_moe.rs:687-743) and then calls execute_selected_moe_cuda. */
+int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                    const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
+                                    const float* d_router_w, const float* d_router_bias, uint64_t k,
+                                    int32_t renormalize, uint64_t n_tokens, const float* d_x,
+                                    const float* d_residual, float* d_out, uint32_t* d_ids_out,
+                                    float* d_weights_out, uint64_t hidden, uint64_t intermediate,
+                                    uint64_t out_dim, float swiglu_limit);
+
+/* Reads and clears the context's device error word (non-zero after a kernel met
+ * an expert id outside its table). Synchronises the context's streams. */
+int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

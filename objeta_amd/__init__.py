@@ -4,8 +4,8 @@ The compute lives in libobjeta_hip.so (objeta_amd/csrc, include/objeta_hip.h);
 this package is the Python mirror of the reference API used by tests and the
 benchmark.
 """
-from .api import (DeviceBuffer, HipBackend, HipBackendBuilder, HipError, QGemvShape, QuantBackend,
-                  QuantFormat, check, discover_devices)
+from .api import (DeviceBuffer, ExpertTable, HipBackend, HipBackendBuilder, HipError, MoeExecutor,
+                  QGemvShape, QuantBackend, QuantFormat, check, discover_devices)
 
-__all__ = ["DeviceBuffer", "HipBackend", "HipBackendBuilder", "HipError", "QGemvShape",
-           "QuantBackend", "QuantFormat", "check", "discover_devices"]
+__all__ = ["DeviceBuffer", "ExpertTable", "HipBackend", "HipBackendBuilder", "HipError",
+           "MoeExecutor", "QGemvShape", "QuantBackend", "QuantFormat", "check", "discover_devices"]

@@ -42,6 +42,11 @@ class DeviceInfo(C.Structure):
                 ("memory_bus_width_bits", I32), ("reserved", I32)]
 
 
+class ExpertPtrs(C.Structure):
+    _fields_ = [("gate", P), ("up", P), ("down", P), ("gate_scale", P), ("up_scale", P),
+                ("down_scale", P)]
+
+
 class QGemvTelemetry(C.Structure):
     _fields_ = [("h2d_ms", F32), ("kernel_ms", F32), ("d2h_ms", F32), ("unaccounted_ms", F32),
                 ("total_ms", F32), ("effective_gbps", F32), ("bytes_read", U64)]
@@ -86,6 +91,13 @@ SIGNATURES = {
     "objeta_hip_fill_gauss_quantized_device": (I32, [P, I32, P, P, U64, U64, U64, F32]),
     "objeta_hip_fp4_scale_raw_host": (I32, [P, P, U64]),
     "objeta_hip_router_topk_device": (I32, [P, P, P, P, P, U64, U64, U64, U64, I32, P, P]),
+    "objeta_hip_moe_selected_device": (I32, [P, I32, P, P, U64, P, P, U64, U64, P, P, P, U64, U64,
+                                             U64, F32]),
+    "objeta_hip_moe_layer_device": (I32, [P, I32, P, P, U64, P, P, U64, I32, U64, P, P, P, P, P,
+                                          U64, U64, U64, F32]),
+    "objeta_hip_device_error": (I32, [P, P]),
+    "objeta_hip_moe_gate_up_device": (I32, [P, I32, P, P, U64, P, U64, U64, P, P, U64, U64, F32]),
+    "objeta_hip_moe_down_device": (I32, [P, I32, P, P, U64, P, P, U64, U64, P, P, P, U64, U64]),
 }
 
 

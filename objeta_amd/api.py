@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import DeviceInfo, Error, InitOptions, QGemvTelemetry
+from ._lib import DeviceInfo, Error, ExpertPtrs, InitOptions, QGemvTelemetry
 
 KIND_NAMES = ["Driver", "Runtime", "Nvrtc", "Io", "InvalidInput", "Unsupported", "Internal"]
 
@@ -283,3 +283,69 @@ def _addr(v):
     if isinstance(v, int):
         return C.c_void_p(v)
     return v
+
+
+class ExpertTable:
+    """Device array of objeta_hip_expert_ptrs: one entry per expert, pointing at
+    device-resident gate/up/down matrices (and E8M0 scales for split FP4)."""
+
+    def __init__(self, backend: HipBackend, entries):
+        """entries: list of (gate, up, down) or (gate, up, down, gate_s, up_s, down_s)
+        device addresses (ints or DeviceBuffers)."""
+        self.backend = backend
+        self.n = len(entries)
+        arr = (ExpertPtrs * max(1, self.n))()
+        for i, e in enumerate(entries):
+            v = [_ptr_int(p) for p in e] + [0] * (6 - len(e))
+            arr[i] = ExpertPtrs(*v)
+        raw = np.frombuffer(bytes(arr), dtype=np.uint8)
+        self.buf = backend.to_device(raw)
+
+    def addr(self):
+        return self.buf.addr()
+
+
+def _ptr_int(p) -> int:
+    if isinstance(p, DeviceBuffer):
+        return p.ptr
+    if isinstance(p, C.c_void_p):
+        return p.value or 0
+    return int(p or 0)
+
+
+class MoeExecutor:
+    """MoeExecutor (moe.rs:285-1280): the selected-expert MoE on the device."""
+
+    def __init__(self, backend: HipBackend):
+        self.backend = backend
+        self.L = backend.L
+
+    def compile(self) -> None:
+        """Kernels are compiled ahead of time (moe.rs:304-307 compiles NVRTC modules)."""
+
+    def selected_device(self, fmt, table: ExpertTable, d_ids, d_weights, n_tokens: int, k: int, d_x,
+                        d_residual, d_out, hidden: int, inter: int, out_dim: int,
+                        swiglu_limit: float = 0.0, stream=None) -> None:
+        check(self.L.objeta_hip_moe_selected_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr_or_none(d_ids),
+            _addr(d_weights), n_tokens, k, _addr(d_x), _addr_or_none(d_residual), _addr(d_out), hidden,
+            inter, out_dim, swiglu_limit))
+
+    def layer_device(self, fmt, table: ExpertTable, d_router_w, d_router_bias, k: int, n_tokens: int,
+                     d_x, d_residual, d_out, d_ids_out, d_weights_out, hidden: int, inter: int,
+                     out_dim: int, renormalize: bool = True, swiglu_limit: float = 0.0,
+                     stream=None) -> None:
+        check(self.L.objeta_hip_moe_layer_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr(d_router_w),
+            _addr_or_none(d_router_bias), k, 1 if renormalize else 0, n_tokens, _addr(d_x),
+            _addr_or_none(d_residual), _addr(d_out), _addr(d_ids_out), _addr(d_weights_out), hidden,
+            inter, out_dim, swiglu_limit))
+
+    def device_error(self) -> int:
+        v = C.c_uint32(0)
+        check(self.L.objeta_hip_device_error(self.backend.ctx, C.byref(v)))
+        return v.value
+
+
+def _addr_or_none(v):
+    return None if v is None else _addr(v)

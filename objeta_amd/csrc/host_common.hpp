@@ -64,11 +64,14 @@ std::string strf(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
                                    "host exception", ex.what());                      \
     }
 
-// Device scratch owned by the context, grown only outside graph capture.
+// Device scratch owned by the context, one region per purpose. A region grows
+// only outside graph capture, and a replaced region stays allocated until the
+// context is destroyed, so graphs captured earlier keep valid pointers.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
+enum WsSlot : int { kWsRouter = 0, kWsMoeAct = 1, kWsMoeTable = 2, kWsMoeOut = 3, kWsSlots = 4 };
 
 }  // namespace objeta
 
@@ -77,8 +80,13 @@ struct objeta_hip_context {
     objeta_hip_device_info info{};
     std::vector<hipStream_t> streams;  // streams[0] is the default compute stream
     hipStream_t copy_stream = nullptr;  // side stream for cache H2D traffic
-    objeta::Workspace ws;               // scratch for multi-kernel entry points
-    uint32_t* counters = nullptr;       // zero-initialised device counters (self-resetting)
+    objeta::Workspace ws[objeta::kWsSlots];  // scratch for multi-kernel entry points
+    std::vector<void*> retired_ws;           // replaced regions, freed at destroy
+    void* host_stage = nullptr;              // pinned host staging (expert tables)
+    size_t host_stage_bytes = 0;
+    uint32_t* counters = nullptr;       // zero-initialised device counters (self-resetting),
+                                        // followed by the device error word
+
     size_t counter_words = 0;
     std::mutex mu;
 };
@@ -87,8 +95,10 @@ namespace objeta {
 
 int32_t check_ctx(const objeta_hip_context* ctx, const char* action);
 hipStream_t resolve_stream(objeta_hip_context* ctx, objeta_hip_stream s);
-// Makes sure the context workspace holds at least `bytes`; fails (Unsupported) if it
-// would have to grow while `stream` is capturing.
-int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, size_t bytes);
+// Makes sure workspace region `slot` holds at least `bytes` and returns it in *out;
+// fails (Unsupported) if it would have to grow while `stream` is capturing.
+int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, int slot, size_t bytes, void** out);
+// Pinned host staging of at least `bytes` (grown outside capture only).
+int32_t ensure_host_stage(objeta_hip_context* ctx, size_t bytes, void** out);
 
 }  // namespace objeta

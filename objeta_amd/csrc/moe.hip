@@ -1,0 +1,626 @@
+// moe.hip — selected-expert MoE kernels for gfx950.
+//
+// Replaces the per-expert launch chain of execute_selected_moe_cuda
+// (crates/objeta-cuda/src/moe.rs:587-652): gate GEMV, up GEMV, silu_mul, down
+// GEMV and weighted_accum (kernels/moe.cu:2-34) become two launches for all
+// tokens and all selected experts:
+//
+//   moe_gate_up   one workgroup per (token, slot) assignment and row block; every
+//                 lane streams the same weight pair of the gate row and the up row,
+//                 so after the row reduction one lane holds both dot products and
+//                 writes silu(gate) * up. The token's activation vector is staged
+//                 once per workgroup in LDS while the weight loads are in flight.
+//   moe_down      one workgroup per (token, row block); wave w streams the down
+//                 rows of slots [w*JW, w*JW + JW) against their activations
+//                 (staged in LDS), the per-slot row sums meet in LDS and one lane
+//                 per row adds them into the residual in slot order. There is one
+//                 writer per output element, so no atomics and a fixed order.
+//
+// Both kernels are one-shot (every lane issues all of its weight loads before it
+// touches LDS) rather than persistent: an MoE layer at batch 1 is a few MB per
+// phase, so the whole phase is in flight at once.
+#include "device_common.hpp"
+#include "gemv_stream.hpp"
+#include "host_common.hpp"
+#include "kernels.hpp"
+
+namespace objeta {
+namespace dev {
+
+template <class R>
+struct RowsOf;
+template <int F>
+struct RowsOf<QRows<F>> {
+    static __device__ __forceinline__ QRows<F> make(const void* w, const void*, uint32_t cols) {
+        return QRows<F>{static_cast<const uint8_t*>(w), static_cast<size_t>(cols >> 5) * Fmt<F>::kBlockBytes};
+    }
+};
+template <>
+struct RowsOf<Fp4Rows> {
+    static __device__ __forceinline__ Fp4Rows make(const void* w, const void* s, uint32_t cols) {
+        return Fp4Rows{static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(s), cols >> 1, cols >> 5};
+    }
+};
+
+// silu_mul (kernels/moe.cu:2-22); the CPU reference is moe.rs:1308-1315.
+__device__ __forceinline__ float silu_mul(float g, float u, float limit) {
+    if (limit > 0.0f) {
+        u = fminf(limit, fmaxf(-limit, u));
+        g = fminf(limit, g);
+    }
+    const float silu = g / (1.0f + expf(-g));
+    return silu * u;
+}
+
+// Expert id of assignment a; ids == nullptr means the identity. Returns false
+// (and raises the device error word) when the id is outside the table.
+__device__ __forceinline__ bool expert_of(const uint32_t* __restrict__ ids, uint32_t a, uint32_t n_table,
+                                          uint32_t* __restrict__ err, uint32_t& e) {
+    e = ids ? ids[a] : a;
+    if (e < n_table) return true;
+    if ((threadIdx.x & 63) == 0) atomicOr(err, 1u);
+    e = 0;
+    return false;
+}
+
+// Wave-cooperative copy of `cols` floats (cols % 64 == 0) from global memory into
+// an LDS slot padded to kPad floats per 64 (the layout pair_dot reads).
+__device__ __forceinline__ void stage_vec_wave(float* __restrict__ dst, const float* __restrict__ src,
+                                               uint32_t cols, uint32_t lane) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    const uint32_t n4 = cols >> 2;
+    for (uint32_t i = lane; i < n4; i += 64) {
+        const uint32_t c = i << 2;
+        *reinterpret_cast<float4*>(dst + (c >> 6) * kPad + (c & 63)) = s4[i];
+    }
+}
+
+// ------------------------------------------------------------------ gate/up
+// grid.x = n_assign * blocks_per_assign, block = 256 (4 waves). A wave owns
+// g = 64 / lpr row slots (lpr lanes each) times U rows; lane lp of a slot owns
+// pairs lp + c * lpr, c < CH (pairs == CH * lpr).
+template <class R, int U, int CH>
+__global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
+    const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
+    const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
+    uint32_t lpr, uint32_t blocks_per_assign, float limit, uint32_t* __restrict__ err) {
+    extern __shared__ float lds[];
+    const uint32_t a = blockIdx.x / blocks_per_assign;
+    const uint32_t rb = blockIdx.x - a * blocks_per_assign;
+    const uint32_t t = a / k;
+    uint32_t e;
+    const bool ok = expert_of(ids, a, n_table, err, e);
+    const objeta_hip_expert_ptrs P = table[e];
+    const R gm = RowsOf<R>::make(P.gate, P.gate_scale, hidden);
+    const R um = RowsOf<R>::make(P.up, P.up_scale, hidden);
+
+    const uint32_t pairs = hidden >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t gs = 64 / lpr, slot = lane / lpr, lp = lane - slot * lpr;
+    const uint32_t row0 = (rb * kWaves + wave) * gs * U;
+
+    uint32_t dg[U][CH][R::kDw], du[U][CH][R::kDw];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t r = row0 + static_cast<uint32_t>(u) * gs + slot;
+        const uint32_t rc = r < inter ? r : inter - 1;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const uint32_t p = lp + static_cast<uint32_t>(c) * lpr;
+            gm.load(rc, p, dg[u][c]);
+            um.load(rc, p, du[u][c]);
+        }
+    }
+    stage_x<1>(lds, x + static_cast<size_t>(t) * hidden, hidden, pairs);
+    __syncthreads();
+
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        float ag[1] = {0.f}, au[1] = {0.f};
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const float* xs[1] = {lds + (lp + static_cast<uint32_t>(c) * lpr) * kPad};
+            gm.template dot<1>(dg[u][c], xs, ag);
+            um.template dot<1>(du[u][c], xs, au);
+        }
+        const float g = row_reduce(ag[0], lp, lpr);
+        const float v = row_reduce(au[0], lp, lpr);
+        const uint32_t r = row0 + static_cast<uint32_t>(u) * gs + slot;
+        if (slot < gs && lp == 0 && r < inter)
+            act[static_cast<size_t>(a) * inter + r] = ok ? silu_mul(g, v, limit) : __builtin_nanf("");
+    }
+}
+
+// -------------------------------------------------------------------- down
+// grid.x = n_tokens * blocks_per_token, block = ceil(k / JW) waves. All waves of
+// a block cover the same g * U output rows; wave w takes slots [w*JW, w*JW+JW).
+// LDS: red [k][g*U] row sums, then one padded activation slot per (wave, jj).
+template <class R, int U, int CH, int JW>
+__global__ __launch_bounds__(1024) void moe_down_kernel(
+    const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
+    const float* __restrict__ wts, const float* __restrict__ act, const float* resid, float* out,
+    uint32_t inter, uint32_t out_dim, uint32_t k, uint32_t lpr, uint32_t blocks_per_token,
+    uint32_t* __restrict__ err) {
+    extern __shared__ float lds[];
+    const uint32_t t = blockIdx.x / blocks_per_token;
+    const uint32_t rb = blockIdx.x - t * blocks_per_token;
+    const uint32_t pairs = inter >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t gs = 64 / lpr, slot = lane / lpr, lp = lane - slot * lpr;
+    const uint32_t rows_blk = gs * U;
+    const uint32_t row0 = rb * rows_blk;
+    float* red = lds;
+    float* xst = lds + ((k * rows_blk + 3u) & ~3u) + wave * JW * pairs * kPad;
+
+    R m[JW];
+    bool ok[JW];
+    uint32_t d[JW][U][CH][R::kDw];
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) {
+        const uint32_t j = wave * JW + jj;
+        const uint32_t jc = j < k ? j : k - 1;
+        uint32_t e;
+        ok[jj] = expert_of(ids, t * k + jc, n_table, err, e);
+        const objeta_hip_expert_ptrs P = table[e];
+        m[jj] = RowsOf<R>::make(P.down, P.down_scale, inter);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t r = row0 + static_cast<uint32_t>(u) * gs + slot;
+            const uint32_t rc = r < out_dim ? r : out_dim - 1;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) m[jj].load(rc, lp + static_cast<uint32_t>(c) * lpr, d[jj][u][c]);
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) {
+        const uint32_t j = wave * JW + jj;
+        const uint32_t jc = j < k ? j : k - 1;
+        stage_vec_wave(xst + jj * pairs * kPad, act + (static_cast<size_t>(t) * k + jc) * inter, inter, lane);
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) {
+        const uint32_t j = wave * JW + jj;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float acc[1] = {0.f};
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const float* xs[1] = {xst + (jj * pairs + lp + static_cast<uint32_t>(c) * lpr) * kPad};
+                m[jj].template dot<1>(d[jj][u][c], xs, acc);
+            }
+            const float v = row_reduce(acc[0], lp, lpr);
+            if (slot < gs && lp == 0 && j < k)
+                red[j * rows_blk + static_cast<uint32_t>(u) * gs + slot] = ok[jj] ? v : __builtin_nanf("");
+        }
+    }
+    __syncthreads();
+
+    if (threadIdx.x < rows_blk) {
+        const uint32_t r = row0 + threadIdx.x;
+        if (r < out_dim) {
+            const size_t o = static_cast<size_t>(t) * out_dim + r;
+            float acc = resid ? resid[o] : 0.0f;
+            for (uint32_t j = 0; j < k; ++j) acc = __builtin_fmaf(wts[t * k + j], red[j * rows_blk + threadIdx.x], acc);
+            out[o] = acc;
+        }
+    }
+}
+
+// ------------------------------------------- general shapes (cols % 32 == 0)
+// Used when hidden or intermediate is not a multiple of 64 or the activation
+// stage would not fit in LDS: one wave per row, lanes stride over blocks.
+template <int F>
+__device__ __forceinline__ float block_weight(const uint8_t* __restrict__ blk, const uint8_t* __restrict__ sb,
+                                              uint32_t i) {
+    if constexpr (F == kQ4) {
+        const uint32_t pk = blk[2 + i / 2];
+        return static_cast<float>(static_cast<int>((i & 1) ? (pk >> 4) : (pk & 15)) - 8);
+    } else if constexpr (F == kQ5) {
+        const uint32_t pk = blk[6 + i / 2];
+        const uint32_t lo = (i & 1) ? (pk >> 4) : (pk & 15);
+        const uint32_t hi = (blk[2 + i / 8] >> (i & 7)) & 1u;
+        return static_cast<float>(static_cast<int>(lo | (hi << 4)) - 16);
+    } else if constexpr (F == kIQ3) {
+        const uint32_t lo = (blk[2 + i / 4] >> (2 * (i & 3))) & 3u;
+        const uint32_t hi = (blk[10 + i / 8] >> (i & 7)) & 1u;
+        return static_cast<float>(static_cast<int>(lo | (hi << 2)) - 4);
+    } else {
+        (void)sb;
+        const uint32_t pk = blk[i / 2];
+        const uint32_t c = (i & 1) ? (pk >> 4) : (pk & 15);
+        return f16_to_f32(((c & 7u) << 9) | ((c & 8u) << 12)) * 16384.0f;
+    }
+}
+
+// Row r of an expert matrix against v[cols]; result in every lane of the wave.
+template <int F>
+__device__ __forceinline__ float row_dot_general(const uint8_t* __restrict__ w, const uint8_t* __restrict__ s,
+                                                 uint32_t r, uint32_t cols, const float* __restrict__ v,
+                                                 uint32_t lane) {
+    const uint32_t nb = cols >> 5;
+    float acc = 0.f;
+    for (uint32_t b = lane; b < nb; b += 64) {
+        const uint8_t* blk;
+        float scale;
+        if constexpr (F == kFP4) {
+            blk = w + static_cast<size_t>(r) * (cols >> 1) + b * 16;
+            scale = e8m0_to_f32(s[static_cast<size_t>(r) * nb + b]);
+        } else {
+            blk = w + (static_cast<size_t>(r) * nb + b) * Fmt<F>::kBlockBytes;
+            scale = f16_to_f32(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
+        }
+        for (uint32_t i = 0; i < 32; ++i)
+            acc = __builtin_fmaf(block_weight<F>(blk, nullptr, i) * scale, v[b * 32 + i], acc);
+    }
+    return wave_reduce(acc);
+}
+
+// grid.x = ceil(n_assign * inter / 4); one wave per (assignment, row).
+template <int F>
+__global__ __launch_bounds__(kThreads) void moe_gate_up_general(
+    const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
+    const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
+    uint32_t n_assign, float limit, uint32_t* __restrict__ err) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t item = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (item >= n_assign * inter) return;
+    const uint32_t a = item / inter, r = item - a * inter;
+    uint32_t e;
+    const bool ok = expert_of(ids, a, n_table, err, e);
+    const objeta_hip_expert_ptrs P = table[e];
+    const float* xt = x + static_cast<size_t>(a / k) * hidden;
+    const float g = row_dot_general<F>(static_cast<const uint8_t*>(P.gate), static_cast<const uint8_t*>(P.gate_scale),
+                                       r, hidden, xt, lane);
+    const float u = row_dot_general<F>(static_cast<const uint8_t*>(P.up), static_cast<const uint8_t*>(P.up_scale), r,
+                                       hidden, xt, lane);
+    if (lane == 0) act[static_cast<size_t>(a) * inter + r] = ok ? silu_mul(g, u, limit) : __builtin_nanf("");
+}
+
+// grid.x = ceil(n_tokens * out_dim / 4); one wave per (token, row), slots in order.
+template <int F>
+__global__ __launch_bounds__(kThreads) void moe_down_general(
+    const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
+    const float* __restrict__ wts, const float* __restrict__ act, const float* resid, float* out, uint32_t inter,
+    uint32_t out_dim, uint32_t k, uint32_t n_tokens, uint32_t* __restrict__ err) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t item = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (item >= n_tokens * out_dim) return;
+    const uint32_t t = item / out_dim, r = item - t * out_dim;
+    const size_t o = static_cast<size_t>(t) * out_dim + r;
+    float acc = resid ? resid[o] : 0.0f;
+    for (uint32_t j = 0; j < k; ++j) {
+        uint32_t e;
+        const bool ok = expert_of(ids, t * k + j, n_table, err, e);
+        const objeta_hip_expert_ptrs P = table[e];
+        const float v = row_dot_general<F>(static_cast<const uint8_t*>(P.down),
+                                           static_cast<const uint8_t*>(P.down_scale), r, inter,
+                                           act + (static_cast<size_t>(t) * k + j) * inter, lane);
+        acc = __builtin_fmaf(wts[t * k + j], ok ? v : __builtin_nanf(""), acc);
+    }
+    if (lane == 0) out[o] = acc;
+}
+
+}  // namespace dev
+
+// ------------------------------------------------------------------ launchers
+namespace {
+
+using namespace dev;
+
+constexpr uint32_t kMaxK = 32;  // selection slots per token (router's top-k bound)
+
+struct MoeShape {
+    uint32_t n_table, n_tokens, k, hidden, inter, out_dim;
+};
+
+size_t max_lds(const objeta_hip_context* ctx) {
+    return ctx->info.max_shared_memory_per_block > 0 ? static_cast<size_t>(ctx->info.max_shared_memory_per_block)
+                                                     : 65536u;
+}
+
+template <class R, int U, int CH>
+hipError_t gate_up_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids, const float* x,
+                        float* act, const MoeShape& sh, uint32_t lpr, float limit, uint32_t* err) {
+    const uint32_t gs = 64 / lpr;
+    const uint32_t rows_blk = kWaves * gs * U;
+    const uint32_t bpa = (sh.inter + rows_blk - 1) / rows_blk;
+    const uint32_t n_assign = sh.n_tokens * sh.k;
+    const size_t lds = static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 4 * sizeof(float);
+    hipLaunchKernelGGL((moe_gate_up_kernel<R, U, CH>), dim3(n_assign * bpa), dim3(kThreads), lds, s, table,
+                       sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k, lpr, bpa, limit, err);
+    return hipGetLastError();
+}
+
+template <class R, int U, int CH, int JW>
+hipError_t down_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids, const float* wts,
+                     const float* act, const float* resid, float* out, const MoeShape& sh, uint32_t lpr,
+                     uint32_t* err) {
+    const uint32_t gs = 64 / lpr;
+    const uint32_t rows_blk = gs * U;
+    const uint32_t bpt = (sh.out_dim + rows_blk - 1) / rows_blk;
+    const uint32_t waves = (sh.k + JW - 1) / JW;
+    const size_t lds = (((sh.k * rows_blk + 3u) & ~3u) + static_cast<size_t>(waves) * JW * (sh.inter >> 6) * kPad) *
+                       sizeof(float);
+    hipLaunchKernelGGL((moe_down_kernel<R, U, CH, JW>), dim3(sh.n_tokens * bpt), dim3(waves * 64), lds, s, table,
+                       sh.n_table, ids, wts, act, resid, out, sh.inter, sh.out_dim, sh.k, lpr, bpt, err);
+    return hipGetLastError();
+}
+
+size_t down_lds_bytes(const MoeShape& sh, uint32_t jw, uint32_t u) {
+    const uint32_t lpr = pick_lpr(sh.inter >> 6);
+    const uint32_t rows_blk = (64 / lpr) * u;
+    const uint32_t waves = (sh.k + jw - 1) / jw;
+    return (((sh.k * rows_blk + 3u) & ~3u) + static_cast<size_t>(waves) * jw * (sh.inter >> 6) * kPad) * sizeof(float);
+}
+
+// Dispatch on chunks per lane (pairs / lpr).
+template <class R>
+hipError_t launch_gate_up_rows(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids,
+                               const float* x, float* act, const MoeShape& sh, float limit, uint32_t* err,
+                               uint32_t cus) {
+    const uint32_t pairs = sh.hidden >> 6;
+    const uint32_t lpr = pick_lpr(pairs);
+    const uint32_t ch = pairs / lpr;
+    // two rows per slot when that still leaves a few workgroups per CU
+    const uint32_t gs = 64 / lpr;
+    const uint64_t blocks_u2 = static_cast<uint64_t>(sh.n_tokens) * sh.k * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2));
+    const bool u2 = blocks_u2 >= 2ull * cus && ch <= 2;
+    switch (ch) {
+        case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err)
+                          : gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err);
+        case 2: return u2 ? gate_up_fast<R, 2, 2>(s, table, ids, x, act, sh, lpr, limit, err)
+                          : gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err);
+        case 3: return gate_up_fast<R, 1, 3>(s, table, ids, x, act, sh, lpr, limit, err);
+        default: return gate_up_fast<R, 1, 4>(s, table, ids, x, act, sh, lpr, limit, err);
+    }
+}
+
+template <class R>
+hipError_t launch_down_rows(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids,
+                            const float* wts, const float* act, const float* resid, float* out, const MoeShape& sh,
+                            uint32_t jw, uint32_t* err) {
+    const uint32_t pairs = sh.inter >> 6;
+    const uint32_t lpr = pick_lpr(pairs);
+    const uint32_t ch = pairs / lpr;
+    if (jw == 2) {
+        switch (ch) {
+            case 1: return down_fast<R, 1, 1, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+            case 2: return down_fast<R, 1, 2, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+            case 3: return down_fast<R, 1, 3, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+            default: return down_fast<R, 1, 4, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+        }
+    }
+    switch (ch) {
+        case 1: return down_fast<R, 1, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+        case 2: return down_fast<R, 1, 2, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+        case 3: return down_fast<R, 1, 3, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+        default: return down_fast<R, 1, 4, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+    }
+}
+
+template <int F>
+hipError_t launch_general(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids, const float* wts,
+                          const float* x, float* act, const float* resid, float* out, const MoeShape& sh,
+                          float limit, uint32_t* err, int phase) {
+    if (phase == 0) {
+        const uint64_t items = static_cast<uint64_t>(sh.n_tokens) * sh.k * sh.inter;
+        hipLaunchKernelGGL((moe_gate_up_general<F>), dim3(static_cast<uint32_t>((items + kWaves - 1) / kWaves)),
+                           dim3(kThreads), 0, s, table, sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k,
+                           sh.n_tokens * sh.k, limit, err);
+    } else {
+        const uint64_t items = static_cast<uint64_t>(sh.n_tokens) * sh.out_dim;
+        hipLaunchKernelGGL((moe_down_general<F>), dim3(static_cast<uint32_t>((items + kWaves - 1) / kWaves)),
+                           dim3(kThreads), 0, s, table, sh.n_table, ids, wts, act, resid, out, sh.inter, sh.out_dim,
+                           sh.k, sh.n_tokens, err);
+    }
+    return hipGetLastError();
+}
+
+bool fast_shape(uint32_t cols) {
+    if (cols % 64 != 0) return false;
+    const uint32_t pairs = cols >> 6;
+    const uint32_t lpr = pick_lpr(pairs);
+    return lpr != 0 && pairs / lpr <= 4;
+}
+
+}  // namespace
+
+namespace {
+
+int32_t validate_moe(const char* action, int32_t format, uint64_t n_table, uint64_t n_tokens, uint64_t k,
+                     uint64_t hidden, uint64_t inter, uint64_t out_dim) {
+    if (format < OBJETA_HIP_Q4_0 || format > OBJETA_HIP_FP4_E2M1)
+        OBJ_FAIL(kInvalidInput, action, strf("unknown format %d", format));
+    if (hidden % 32 != 0 || inter % 32 != 0)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("hidden %llu and intermediate %llu must be multiples of block_size 32",
+                      (unsigned long long)hidden, (unsigned long long)inter));
+    if (k == 0 || k > kMaxK) OBJ_FAIL(kInvalidInput, action, strf("k %llu must be in 1..=%u", (unsigned long long)k, kMaxK));
+    if (hidden == 0 || inter == 0) OBJ_FAIL(kInvalidInput, action, "hidden and intermediate must be non-zero");
+    if (n_table == 0) OBJ_FAIL(kInvalidInput, action, "expert table is empty");
+    if (hidden > (1u << 24) || inter > (1u << 24) || out_dim > (1u << 26) || n_table > 0xFFFFFFFFull ||
+        n_tokens * k * inter > 0x7FFFFFFFull || n_tokens * out_dim > 0x7FFFFFFFull || n_tokens * k > 0x7FFFFFFFull)
+        OBJ_FAIL(kInvalidInput, action, "shape exceeds the 32-bit index range of the kernels");
+    return 0;
+}
+
+MoeShape shape_of(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden, uint64_t inter, uint64_t out_dim) {
+    return MoeShape{static_cast<uint32_t>(n_table), static_cast<uint32_t>(n_tokens), static_cast<uint32_t>(k),
+                    static_cast<uint32_t>(hidden), static_cast<uint32_t>(inter), static_cast<uint32_t>(out_dim)};
+}
+
+}  // namespace
+
+int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                           uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
+                           float* act, uint64_t hidden, uint64_t inter, float limit) {
+    const char* action = "launch MoE gate/up";
+    OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, hidden, inter, 1));
+    if (n_tokens == 0) return 0;
+    if (!table || !x || !act) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 16) OBJ_FAIL(kInvalidInput, action, "x must be 16-byte aligned");
+    const MoeShape sh = shape_of(n_table, n_tokens, k, hidden, inter, 1);
+    uint32_t* err = ctx->counters + ctx->counter_words;
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    const bool fast = fast_shape(sh.hidden) && static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 16 <= max_lds(ctx);
+    hipError_t e;
+    if (fast) {
+        switch (format) {
+            case OBJETA_HIP_Q4_0: e = launch_gate_up_rows<QRows<kQ4>>(s, table, ids, x, act, sh, limit, err, cus); break;
+            case OBJETA_HIP_Q5_0: e = launch_gate_up_rows<QRows<kQ5>>(s, table, ids, x, act, sh, limit, err, cus); break;
+            case OBJETA_HIP_IQ3_0: e = launch_gate_up_rows<QRows<kIQ3>>(s, table, ids, x, act, sh, limit, err, cus); break;
+            default: e = launch_gate_up_rows<Fp4Rows>(s, table, ids, x, act, sh, limit, err, cus); break;
+        }
+    } else {
+        switch (format) {
+            case OBJETA_HIP_Q4_0: e = launch_general<kQ4>(s, table, ids, nullptr, x, act, nullptr, nullptr, sh, limit, err, 0); break;
+            case OBJETA_HIP_Q5_0: e = launch_general<kQ5>(s, table, ids, nullptr, x, act, nullptr, nullptr, sh, limit, err, 0); break;
+            case OBJETA_HIP_IQ3_0: e = launch_general<kIQ3>(s, table, ids, nullptr, x, act, nullptr, nullptr, sh, limit, err, 0); break;
+            default: e = launch_general<kFP4>(s, table, ids, nullptr, x, act, nullptr, nullptr, sh, limit, err, 0); break;
+        }
+    }
+    if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+    return 0;
+}
+
+int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                        uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
+                        const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim) {
+    const char* action = "launch MoE down + combine";
+    OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, 32, inter, out_dim));
+    if (n_tokens == 0 || out_dim == 0) return 0;
+    if (!table || !wts || !act || !out) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    if (reinterpret_cast<uintptr_t>(act) % 16) OBJ_FAIL(kInvalidInput, action, "act must be 16-byte aligned");
+    const MoeShape sh = shape_of(n_table, n_tokens, k, 32, inter, out_dim);
+    uint32_t* err = ctx->counters + ctx->counter_words;
+    uint32_t jw = 0;
+    if (fast_shape(sh.inter)) {
+        if (down_lds_bytes(sh, 2, 1) <= max_lds(ctx) && (sh.k + 1) / 2 <= 16) jw = 2;
+        else if (down_lds_bytes(sh, 1, 1) <= max_lds(ctx) && sh.k <= 16) jw = 1;
+    }
+    hipError_t e;
+    if (jw) {
+        switch (format) {
+            case OBJETA_HIP_Q4_0: e = launch_down_rows<QRows<kQ4>>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
+            case OBJETA_HIP_Q5_0: e = launch_down_rows<QRows<kQ5>>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
+            case OBJETA_HIP_IQ3_0: e = launch_down_rows<QRows<kIQ3>>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
+            default: e = launch_down_rows<Fp4Rows>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
+        }
+    } else {
+        switch (format) {
+            case OBJETA_HIP_Q4_0: e = launch_general<kQ4>(s, table, ids, wts, nullptr, const_cast<float*>(act), resid, out, sh, 0.f, err, 1); break;
+            case OBJETA_HIP_Q5_0: e = launch_general<kQ5>(s, table, ids, wts, nullptr, const_cast<float*>(act), resid, out, sh, 0.f, err, 1); break;
+            case OBJETA_HIP_IQ3_0: e = launch_general<kIQ3>(s, table, ids, wts, nullptr, const_cast<float*>(act), resid, out, sh, 0.f, err, 1); break;
+            default: e = launch_general<kFP4>(s, table, ids, wts, nullptr, const_cast<float*>(act), resid, out, sh, 0.f, err, 1); break;
+        }
+    }
+    if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+    return 0;
+}
+
+int32_t launch_moe_selected(objeta_hip_context* ctx, int32_t format, hipStream_t s,
+                            const objeta_hip_expert_ptrs* table, uint64_t n_table, const uint32_t* ids,
+                            const float* wts, uint64_t n_tokens, uint64_t k, const float* x, const float* resid,
+                            float* out, uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit, float* act) {
+    OBJ_TRY(validate_moe("launch selected-expert MoE", format, n_table, n_tokens, k, hidden, inter, out_dim));
+    if (n_tokens == 0 || out_dim == 0) return 0;
+    OBJ_TRY(launch_moe_gate_up(ctx, format, s, table, n_table, ids, n_tokens, k, x, act, hidden, inter, limit));
+    return launch_moe_down(ctx, format, s, table, n_table, ids, wts, n_tokens, k, act, resid, out, inter, out_dim);
+}
+
+int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
+                        float** out) {
+    void* p = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsMoeAct, static_cast<size_t>(n_tokens * k * inter) * sizeof(float) + 64, &p));
+    *out = static_cast<float*>(p);
+    return 0;
+}
+
+}  // namespace objeta
+
+using namespace objeta;
+
+extern "C" {
+
+int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                       const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                       const uint32_t* d_ids, const float* d_weights, uint64_t n_tokens,
+                                       uint64_t k, const float* d_x, const float* d_residual, float* d_out,
+                                       uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                       float swiglu_limit) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "moe_selected_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    if (n_tokens == 0 || out_dim == 0) return 0;
+    float* act = nullptr;
+    OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k ? k : 1, intermediate ? intermediate : 1, &act));
+    return launch_moe_selected(ctx, format, s, d_table, n_table, d_ids, d_weights, n_tokens, k, d_x, d_residual,
+                               d_out, hidden, intermediate, out_dim, swiglu_limit, act);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_moe_gate_up_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                      const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                      const uint32_t* d_ids, uint64_t n_tokens, uint64_t k, const float* d_x,
+                                      float* d_act, uint64_t hidden, uint64_t intermediate, float swiglu_limit) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "moe_gate_up_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    return launch_moe_gate_up(ctx, format, resolve_stream(ctx, stream), d_table, n_table, d_ids, n_tokens, k, d_x,
+                              d_act, hidden, intermediate, swiglu_limit);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                   const objeta_hip_expert_ptrs* d_table, uint64_t n_table, const uint32_t* d_ids,
+                                   const float* d_weights, uint64_t n_tokens, uint64_t k, const float* d_act,
+                                   const float* d_residual, float* d_out, uint64_t intermediate, uint64_t out_dim) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "moe_down_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    return launch_moe_down(ctx, format, resolve_stream(ctx, stream), d_table, n_table, d_ids, d_weights, n_tokens, k,
+                           d_act, d_residual, d_out, intermediate, out_dim);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                    const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
+                                    const float* d_router_w, const float* d_router_bias, uint64_t k,
+                                    int32_t renormalize, uint64_t n_tokens, const float* d_x,
+                                    const float* d_residual, float* d_out, uint32_t* d_ids_out,
+                                    float* d_weights_out, uint64_t hidden, uint64_t intermediate,
+                                    uint64_t out_dim, float swiglu_limit) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "moe_layer_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    if (n_tokens == 0) return 0;
+    if (!d_ids_out || !d_weights_out) OBJ_FAIL(kInvalidInput, "moe_layer_device", "NULL routing output");
+    OBJ_TRY(objeta_hip_router_topk_device(ctx, s, d_router_w, d_router_bias, d_x, n_tokens, n_experts, hidden, k,
+                                          renormalize, d_ids_out, d_weights_out));
+    if (out_dim == 0) return 0;
+    float* act = nullptr;
+    OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k, intermediate ? intermediate : 1, &act));
+    return launch_moe_selected(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, n_tokens, k, d_x,
+                               d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit, act);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "device error word"));
+    if (!out) OBJ_FAIL(kInvalidInput, "device error word", "out is NULL");
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    for (hipStream_t st : ctx->streams) OBJ_HIP(hipStreamSynchronize(st), "synchronize stream");
+    uint32_t* err = ctx->counters + ctx->counter_words;
+    OBJ_HIP(hipMemcpy(out, err, sizeof(uint32_t), hipMemcpyDeviceToHost), "read device error word");
+    const uint32_t zero = 0;
+    OBJ_HIP(hipMemcpy(err, &zero, sizeof(uint32_t), hipMemcpyHostToDevice), "clear device error word");
+    return 0;
+    OBJ_GUARD_END
+}
+
+}  // extern "C"

@@ -267,8 +267,9 @@ extern "C" int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     hipStream_t s = resolve_stream(ctx, stream);
     const size_t need = static_cast<size_t>(n_tokens) * n_experts * 2 * sizeof(float);
-    OBJ_TRY(ensure_workspace(ctx, s, need));
-    float* wl = static_cast<float*>(ctx->ws.ptr);
+    void* ws = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsRouter, need, &ws));
+    float* wl = static_cast<float*>(ws);
     float* wb = wl + static_cast<size_t>(n_tokens) * n_experts;
     return launch_router(ctx, s, d_w_r, d_bias, d_x, n_tokens, n_experts, hidden, k, renormalize, d_ids,
                          d_weights, wl, wb);

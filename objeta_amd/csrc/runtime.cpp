@@ -53,22 +53,40 @@ hipStream_t resolve_stream(objeta_hip_context* ctx, objeta_hip_stream s) {
     return s ? static_cast<hipStream_t>(s) : ctx->streams[0];
 }
 
-int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, size_t bytes) {
-    if (ctx->ws.bytes >= bytes) return 0;
+int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, int slot, size_t bytes, void** out) {
+    Workspace& ws = ctx->ws[slot];
+    if (ws.bytes >= bytes) {
+        *out = ws.ptr;
+        return 0;
+    }
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     OBJ_HIP(hipStreamIsCapturing(stream, &st), "query stream capture status");
     if (st != hipStreamCaptureStatusNone)
         OBJ_FAIL(kUnsupported, "grow workspace",
                  strf("workspace of %zu bytes needed while capturing (have %zu); run the "
                       "call once outside capture first",
-                      bytes, ctx->ws.bytes));
-    OBJ_HIP(hipDeviceSynchronize(), "synchronize before workspace growth");
-    if (ctx->ws.ptr) OBJ_HIP(hipFree(ctx->ws.ptr), "free workspace");
-    ctx->ws.ptr = nullptr;
-    ctx->ws.bytes = 0;
+                      bytes, ws.bytes));
     size_t grow = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
-    OBJ_HIP(hipMalloc(&ctx->ws.ptr, grow), "allocate workspace");
-    ctx->ws.bytes = grow;
+    void* p = nullptr;
+    OBJ_HIP(hipMalloc(&p, grow), "allocate workspace");
+    if (ws.ptr) ctx->retired_ws.push_back(ws.ptr);
+    ws.ptr = p;
+    ws.bytes = grow;
+    *out = p;
+    return 0;
+}
+
+int32_t ensure_host_stage(objeta_hip_context* ctx, size_t bytes, void** out) {
+    if (ctx->host_stage_bytes < bytes) {
+        OBJ_HIP(hipDeviceSynchronize(), "synchronize before staging growth");
+        if (ctx->host_stage) OBJ_HIP(hipHostFree(ctx->host_stage), "free host staging");
+        ctx->host_stage = nullptr;
+        ctx->host_stage_bytes = 0;
+        size_t grow = bytes < (size_t(1) << 16) ? (size_t(1) << 16) : bytes;
+        OBJ_HIP(hipHostMalloc(&ctx->host_stage, grow, hipHostMallocDefault), "allocate host staging");
+        ctx->host_stage_bytes = grow;
+    }
+    *out = ctx->host_stage;
     return 0;
 }
 
@@ -207,8 +225,9 @@ int32_t objeta_hip_init(const objeta_hip_init_options* opts, objeta_hip_context*
         return fail_cleanup(rc);
     }
     ctx->counter_words = 4096;
-    e = hipMalloc(&ctx->counters, ctx->counter_words * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(ctx->counters, 0, ctx->counter_words * sizeof(uint32_t));
+    // counter_words self-resetting tickets, then the device error word
+    e = hipMalloc(&ctx->counters, (ctx->counter_words + 64) * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(ctx->counters, 0, (ctx->counter_words + 64) * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         int32_t rc = set_error(kDriver, __FILE__, __LINE__, __func__, "allocate device counters", hipGetErrorString(e));
@@ -226,7 +245,10 @@ int32_t objeta_hip_destroy(objeta_hip_context* ctx) {
     (void)hipDeviceSynchronize();
     for (hipStream_t s : ctx->streams) (void)hipStreamDestroy(s);
     if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
-    if (ctx->ws.ptr) (void)hipFree(ctx->ws.ptr);
+    for (auto& w : ctx->ws)
+        if (w.ptr) (void)hipFree(w.ptr);
+    for (void* p : ctx->retired_ws) (void)hipFree(p);
+    if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
     if (ctx->counters) (void)hipFree(ctx->counters);
     (void)hipGetLastError();
     delete ctx;
