@@ -293,6 +293,186 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
  * an expert id outside its table). Synchronises the context's streams. */
 int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out);
 
+/* ------------------------------------------------------------ expert cache */
+/* ExpertTensorKind (moe.rs:37-54). */
+enum {
+    OBJETA_HIP_TENSOR_GATE = 0,
+    OBJETA_HIP_TENSOR_UP = 1,
+    OBJETA_HIP_TENSOR_DOWN = 2,
+    OBJETA_HIP_TENSOR_GATE_WEIGHT = 3,
+    OBJETA_HIP_TENSOR_GATE_SCALE = 4,
+    OBJETA_HIP_TENSOR_UP_WEIGHT = 5,
+    OBJETA_HIP_TENSOR_UP_SCALE = 6,
+    OBJETA_HIP_TENSOR_DOWN_WEIGHT = 7,
+    OBJETA_HIP_TENSOR_DOWN_SCALE = 8,
+    OBJETA_HIP_TENSOR_SHARED_GATE_WEIGHT = 9,
+    OBJETA_HIP_TENSOR_SHARED_GATE_SCALE = 10,
+    OBJETA_HIP_TENSOR_SHARED_UP_WEIGHT = 11,
+    OBJETA_HIP_TENSOR_SHARED_UP_SCALE = 12,
+    OBJETA_HIP_TENSOR_SHARED_DOWN_WEIGHT = 13,
+    OBJETA_HIP_TENSOR_SHARED_DOWN_SCALE = 14
+};
+
+/* ExpertCacheKey (moe.rs:56-62). */
+typedef struct {
+    uint64_t layer_id;
+    uint64_t expert_id;
+    int32_t tensor_kind;  /* OBJETA_HIP_TENSOR_* */
+    int32_t quant_format; /* OBJETA_HIP_Q4_0 .. OBJETA_HIP_FP4_E2M1 */
+} objeta_hip_cache_key;
+
+/* The public fields of CudaExpertCache (moe.rs:70-90). */
+typedef struct {
+    uint64_t capacity_bytes;
+    uint64_t resident_bytes;
+    uint64_t pinned_bytes;
+    uint64_t hit_count;
+    uint64_t miss_count;
+    uint64_t eviction_count;
+    uint64_t cache_insert_attempt_count;
+    uint64_t cache_insert_accept_count;
+    uint64_t cache_insert_bypass_count;
+    uint64_t oversized_tensor_bypass_count;
+    uint64_t oversized_expert_bypass_count;
+    uint64_t self_eviction_risk_count;
+    uint64_t entry_count;           /* tensors resident */
+    uint64_t device_bytes_reserved; /* resident + recycled blocks held for reuse */
+    int32_t bypass_oversized_experts;
+    int32_t reserved;
+} objeta_hip_cache_stats;
+
+/* A single-GPU VRAM expert cache: LRU over tensors, pinned (never evicted) entries,
+ * admission by size. Device memory comes from blocks that are recycled after an
+ * eviction only once every stream of the context has passed the point of the
+ * eviction (event fences, no host waits). Not internally locked (the reference's
+ * &mut CudaExpertCache). With ctx == NULL the cache keeps the accounting only and
+ * owns no device memory (device pointers are NULL): the counters and LRU order
+ * behave identically. */
+typedef struct objeta_hip_expert_cache objeta_hip_expert_cache;
+
+/* CudaExpertCache::new (moe.rs:92-111). */
+int32_t objeta_hip_cache_create(objeta_hip_context* ctx, uint64_t capacity_bytes, objeta_hip_expert_cache** out);
+int32_t objeta_hip_cache_destroy(objeta_hip_expert_cache* cache);
+int32_t objeta_hip_cache_stats_get(const objeta_hip_expert_cache* cache, objeta_hip_cache_stats* out);
+/* The bypass_oversized_experts field (moe.rs:77). */
+int32_t objeta_hip_cache_set_bypass_oversized_experts(objeta_hip_expert_cache* cache, int32_t enable);
+/* get (moe.rs:113-122): on a hit *hit = 1, the entry becomes most recent and its
+ * device address/size are returned; on a miss *hit = 0. d_ptr/nbytes may be NULL. */
+int32_t objeta_hip_cache_get(objeta_hip_expert_cache* cache, const objeta_hip_cache_key* key, int32_t* hit,
+                             const void** d_ptr, uint64_t* nbytes);
+/* insert (moe.rs:124-158) of the host bytes `h_src` (nbytes): the bytes are copied
+ * into cache-owned device memory on the context's copy stream (ordered after
+ * `stream` and before the next use on `stream`). *cached = 0 when the tensor is
+ * larger than the capacity: it is then not kept and *d_ptr is a transient copy
+ * that the caller releases with objeta_hip_cache_release_transient. */
+int32_t objeta_hip_cache_insert(objeta_hip_expert_cache* cache, const objeta_hip_cache_key* key, const void* h_src,
+                                uint64_t nbytes, objeta_hip_stream stream, const void** d_ptr, int32_t* cached);
+/* get, then insert on a miss: the get_or_insert of the reference's README
+ * (README.md:123), which its executor inlines (moe.rs:498-583). */
+int32_t objeta_hip_cache_get_or_insert(objeta_hip_expert_cache* cache, const objeta_hip_cache_key* key,
+                                       const void* h_src, uint64_t nbytes, objeta_hip_stream stream,
+                                       const void** d_ptr, int32_t* hit, int32_t* cached);
+/* insert_pinned (moe.rs:192-210): resident and never evicted. */
+int32_t objeta_hip_cache_insert_pinned(objeta_hip_expert_cache* cache, const objeta_hip_cache_key* key,
+                                       const void* h_src, uint64_t nbytes, objeta_hip_stream stream,
+                                       const void** d_ptr);
+/* pin (moe.rs:182-190), touch (moe.rs:160-165). */
+int32_t objeta_hip_cache_pin(objeta_hip_expert_cache* cache, const objeta_hip_cache_key* key);
+int32_t objeta_hip_cache_touch(objeta_hip_expert_cache* cache, const objeta_hip_cache_key* key);
+/* evict_lru (moe.rs:167-180): *evicted = 1 and the key when an entry left. */
+int32_t objeta_hip_cache_evict_lru(objeta_hip_expert_cache* cache, int32_t* evicted, objeta_hip_cache_key* key_out);
+/* clear (moe.rs:212-218), reset_counters (moe.rs:221-226). */
+int32_t objeta_hip_cache_clear(objeta_hip_expert_cache* cache);
+int32_t objeta_hip_cache_reset_counters(objeta_hip_expert_cache* cache);
+/* Returns a transient copy made by insert/get_or_insert with *cached == 0. */
+int32_t objeta_hip_cache_release_transient(objeta_hip_expert_cache* cache, const void* d_ptr);
+/* The keys in LRU order (least recent first), up to cap of them; *n = count. */
+int32_t objeta_hip_cache_order(const objeta_hip_expert_cache* cache, objeta_hip_cache_key* keys, uint64_t cap,
+                               uint64_t* n);
+
+/* ------------------------------------------------ host-in/host-out executor */
+/* One expert's host tensors: gate/up/down bytes (and, for FP4, the E8M0 scale
+ * arrays) with their lengths. Mirrors ExpertWeights (moe.rs:13-18) and
+ * DeepSeekFp4ExpertWeights (moe.rs:27-35). Pinned host memory
+ * (objeta_hip_alloc_pinned_host) lets cache misses overlap compute. */
+typedef struct {
+    const void* gate;
+    uint64_t gate_len;
+    const void* up;
+    uint64_t up_len;
+    const void* down;
+    uint64_t down_len;
+    const void* gate_scale;
+    uint64_t gate_scale_len;
+    const void* up_scale;
+    uint64_t up_scale_len;
+    const void* down_scale;
+    uint64_t down_scale_len;
+} objeta_hip_host_expert;
+
+/* MoeTelemetry (moe.rs:236-276); bytes_by_tensor_kind flattened. The fused
+ * kernels report their time under gate_up_qgemv_ms (gate + up + SiLU) and
+ * down_qgemv_ms (down + weighted combine); activation_ms and accum_ms are 0. */
+typedef struct {
+    uint64_t selected_expert_count;
+    uint64_t logical_expert_bytes_requested;
+    uint64_t actual_expert_bytes_loaded;
+    uint64_t resident_cache_bytes_reused;
+    uint64_t weight_bytes_loaded;
+    uint64_t weight_bytes_reused;
+    uint64_t scale_bytes_loaded;
+    uint64_t scale_bytes_reused;
+    uint64_t resident_cache_resident_bytes;
+    uint64_t resident_cache_capacity_bytes;
+    uint64_t resident_cache_hit_count;
+    uint64_t resident_cache_miss_count;
+    uint64_t resident_cache_eviction_count;
+    uint64_t resident_cache_insert_attempt_count;
+    uint64_t resident_cache_insert_accept_count;
+    uint64_t resident_cache_insert_bypass_count;
+    uint64_t resident_cache_oversized_tensor_bypass_count;
+    uint64_t resident_cache_oversized_expert_bypass_count;
+    uint64_t resident_cache_self_eviction_risk_count;
+    uint64_t dequantized_scratch_bytes;
+    float h2d_ms;
+    float gate_up_qgemv_ms;
+    float activation_ms;
+    float down_qgemv_ms;
+    float accum_ms;
+    float unaccounted_ms;
+    float total_ms;
+    float shared_expert_ms;
+    uint64_t bytes_by_tensor_kind_gate;
+    uint64_t bytes_by_tensor_kind_up;
+    uint64_t bytes_by_tensor_kind_down;
+    uint64_t bytes_per_expert;
+    uint64_t selected_working_set_bytes;
+    uint64_t routed_fp4_bytes_loaded;
+    uint64_t routed_fp4_bytes_reused;
+    uint64_t shared_fp8_bytes_loaded;
+    uint64_t shared_fp8_bytes_reused;
+    uint64_t total_logical_bytes;
+    uint64_t total_loaded_bytes;
+    uint64_t total_reused_bytes;
+} objeta_hip_moe_telemetry;
+
+/* MoeExecutor::execute_selected_moe_cuda (moe.rs:352-751) for the block formats
+ * (the reference hard-codes Q4_0; Q5_0 and IQ3_0 are accepted too) and
+ * execute_selected_moe_native_fp4_cuda (moe.rs:816-1280) for
+ * OBJETA_HIP_FP4_E2M1 (split layout). Host x in, host out[out_dim] out (zero
+ * based, as the reference). Selection (sel_ids[i], sel_weights[i]) in order;
+ * experts[n_experts]. cache may be NULL. Validation messages, cache keys,
+ * admission and the telemetry byte invariant
+ * logical == loaded + reused (moe.rs:743-748) follow the reference. The weights
+ * of cache misses are copied on the context's copy stream; each expert's kernels
+ * wait only for its own copies. tel may be NULL. */
+int32_t objeta_hip_moe_execute_selected(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                        const objeta_hip_host_expert* experts, uint64_t n_experts,
+                                        const uint64_t* sel_ids, const float* sel_weights, uint64_t n_selected,
+                                        const float* x, uint64_t x_len, uint64_t hidden, uint64_t intermediate,
+                                        uint64_t out_dim, uint64_t layer_id, objeta_hip_expert_cache* cache,
+                                        float* out, objeta_hip_moe_telemetry* tel);
+
 #ifdef __cplusplus
 }
 #endif

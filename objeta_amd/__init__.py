@@ -4,8 +4,10 @@ The compute lives in libobjeta_hip.so (objeta_amd/csrc, include/objeta_hip.h);
 this package is the Python mirror of the reference API used by tests and the
 benchmark.
 """
-from .api import (DeviceBuffer, ExpertTable, HipBackend, HipBackendBuilder, HipError, MoeExecutor,
-                  QGemvShape, QuantBackend, QuantFormat, check, discover_devices)
+from .api import (DeviceBuffer, ExpertCache, ExpertCacheKey, ExpertTable, ExpertTensorKind, HipBackend,
+                  HipBackendBuilder, HipError, MoeExecutor, QGemvShape, QuantBackend, QuantFormat, check,
+                  discover_devices)
 
-__all__ = ["DeviceBuffer", "ExpertTable", "HipBackend", "HipBackendBuilder", "HipError",
-           "MoeExecutor", "QGemvShape", "QuantBackend", "QuantFormat", "check", "discover_devices"]
+__all__ = ["DeviceBuffer", "ExpertCache", "ExpertCacheKey", "ExpertTable", "ExpertTensorKind", "HipBackend",
+           "HipBackendBuilder", "HipError", "MoeExecutor", "QGemvShape", "QuantBackend", "QuantFormat", "check",
+           "discover_devices"]

@@ -47,6 +47,46 @@ class ExpertPtrs(C.Structure):
                 ("down_scale", P)]
 
 
+class CacheKey(C.Structure):
+    _fields_ = [("layer_id", U64), ("expert_id", U64), ("tensor_kind", I32), ("quant_format", I32)]
+
+
+class CacheStats(C.Structure):
+    _fields_ = [(n, U64) for n in (
+        "capacity_bytes", "resident_bytes", "pinned_bytes", "hit_count", "miss_count", "eviction_count",
+        "cache_insert_attempt_count", "cache_insert_accept_count", "cache_insert_bypass_count",
+        "oversized_tensor_bypass_count", "oversized_expert_bypass_count", "self_eviction_risk_count",
+        "entry_count", "device_bytes_reserved")] + [("bypass_oversized_experts", I32), ("reserved", I32)]
+
+
+class HostExpert(C.Structure):
+    _fields_ = [("gate", P), ("gate_len", U64), ("up", P), ("up_len", U64), ("down", P), ("down_len", U64),
+                ("gate_scale", P), ("gate_scale_len", U64), ("up_scale", P), ("up_scale_len", U64),
+                ("down_scale", P), ("down_scale_len", U64)]
+
+
+_TEL_U64_HEAD = ("selected_expert_count", "logical_expert_bytes_requested", "actual_expert_bytes_loaded",
+                 "resident_cache_bytes_reused", "weight_bytes_loaded", "weight_bytes_reused",
+                 "scale_bytes_loaded", "scale_bytes_reused", "resident_cache_resident_bytes",
+                 "resident_cache_capacity_bytes", "resident_cache_hit_count", "resident_cache_miss_count",
+                 "resident_cache_eviction_count", "resident_cache_insert_attempt_count",
+                 "resident_cache_insert_accept_count", "resident_cache_insert_bypass_count",
+                 "resident_cache_oversized_tensor_bypass_count",
+                 "resident_cache_oversized_expert_bypass_count", "resident_cache_self_eviction_risk_count",
+                 "dequantized_scratch_bytes")
+_TEL_F32 = ("h2d_ms", "gate_up_qgemv_ms", "activation_ms", "down_qgemv_ms", "accum_ms", "unaccounted_ms",
+            "total_ms", "shared_expert_ms")
+_TEL_U64_TAIL = ("bytes_by_tensor_kind_gate", "bytes_by_tensor_kind_up", "bytes_by_tensor_kind_down",
+                 "bytes_per_expert", "selected_working_set_bytes", "routed_fp4_bytes_loaded",
+                 "routed_fp4_bytes_reused", "shared_fp8_bytes_loaded", "shared_fp8_bytes_reused",
+                 "total_logical_bytes", "total_loaded_bytes", "total_reused_bytes")
+
+
+class MoeTelemetry(C.Structure):
+    _fields_ = ([(n, U64) for n in _TEL_U64_HEAD] + [(n, F32) for n in _TEL_F32] +
+                [(n, U64) for n in _TEL_U64_TAIL])
+
+
 class QGemvTelemetry(C.Structure):
     _fields_ = [("h2d_ms", F32), ("kernel_ms", F32), ("d2h_ms", F32), ("unaccounted_ms", F32),
                 ("total_ms", F32), ("effective_gbps", F32), ("bytes_read", U64)]
@@ -98,6 +138,23 @@ SIGNATURES = {
     "objeta_hip_device_error": (I32, [P, P]),
     "objeta_hip_moe_gate_up_device": (I32, [P, I32, P, P, U64, P, U64, U64, P, P, U64, U64, F32]),
     "objeta_hip_moe_down_device": (I32, [P, I32, P, P, U64, P, P, U64, U64, P, P, P, U64, U64]),
+    "objeta_hip_cache_create": (I32, [P, U64, P]),
+    "objeta_hip_cache_destroy": (I32, [P]),
+    "objeta_hip_cache_stats_get": (I32, [P, P]),
+    "objeta_hip_cache_set_bypass_oversized_experts": (I32, [P, I32]),
+    "objeta_hip_cache_get": (I32, [P, P, P, P, P]),
+    "objeta_hip_cache_insert": (I32, [P, P, P, U64, P, P, P]),
+    "objeta_hip_cache_get_or_insert": (I32, [P, P, P, U64, P, P, P, P]),
+    "objeta_hip_cache_insert_pinned": (I32, [P, P, P, U64, P, P]),
+    "objeta_hip_cache_pin": (I32, [P, P]),
+    "objeta_hip_cache_touch": (I32, [P, P]),
+    "objeta_hip_cache_evict_lru": (I32, [P, P, P]),
+    "objeta_hip_cache_clear": (I32, [P]),
+    "objeta_hip_cache_reset_counters": (I32, [P]),
+    "objeta_hip_cache_release_transient": (I32, [P, P]),
+    "objeta_hip_cache_order": (I32, [P, P, U64, P]),
+    "objeta_hip_moe_execute_selected": (I32, [P, I32, P, P, U64, P, P, U64, P, U64, U64, U64, U64, U64, P,
+                                              P, P]),
 }
 
 

@@ -15,7 +15,8 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import DeviceInfo, Error, ExpertPtrs, InitOptions, QGemvTelemetry
+from ._lib import (CacheKey, CacheStats, DeviceInfo, Error, ExpertPtrs, HostExpert, InitOptions, MoeTelemetry,
+                   QGemvTelemetry)
 
 KIND_NAMES = ["Driver", "Runtime", "Nvrtc", "Io", "InvalidInput", "Unsupported", "Internal"]
 
@@ -349,3 +350,200 @@ class MoeExecutor:
 
 def _addr_or_none(v):
     return None if v is None else _addr(v)
+
+
+class ExpertTensorKind(enum.IntEnum):
+    """ExpertTensorKind (moe.rs:37-54)."""
+    Gate = 0
+    Up = 1
+    Down = 2
+    GateWeight = 3
+    GateScale = 4
+    UpWeight = 5
+    UpScale = 6
+    DownWeight = 7
+    DownScale = 8
+    SharedGateWeight = 9
+    SharedGateScale = 10
+    SharedUpWeight = 11
+    SharedUpScale = 12
+    SharedDownWeight = 13
+    SharedDownScale = 14
+
+
+@dataclass(frozen=True)
+class ExpertCacheKey:
+    """ExpertCacheKey (moe.rs:56-62)."""
+    layer_id: int
+    expert_id: int
+    tensor_kind: ExpertTensorKind
+    quant_format: QuantFormat
+
+    def c(self) -> CacheKey:
+        return CacheKey(self.layer_id, self.expert_id, int(self.tensor_kind), int(self.quant_format))
+
+
+_CACHE_FIELDS = [n for n, _ in CacheStats._fields_ if n not in ("reserved", "bypass_oversized_experts")]
+
+
+class ExpertCache:
+    """CudaExpertCache (moe.rs:70-226) over the library's cache. Counter fields are
+    read-only attributes with the reference's names; `backend=None` keeps the
+    accounting only (no device memory)."""
+
+    def __init__(self, capacity_bytes: int, backend: HipBackend | None = None):
+        self.backend = backend
+        self.L = _lib.load()
+        h = C.c_void_p()
+        check(self.L.objeta_hip_cache_create(backend.ctx if backend else None, capacity_bytes, C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            check(self.L.objeta_hip_cache_destroy(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def stats(self) -> dict:
+        st = CacheStats()
+        check(self.L.objeta_hip_cache_stats_get(self.h, C.byref(st)))
+        d = {n: getattr(st, n) for n in _CACHE_FIELDS}
+        d["bypass_oversized_experts"] = bool(st.bypass_oversized_experts)
+        return d
+
+    def __getattr__(self, name):
+        if name in _CACHE_FIELDS or name == "bypass_oversized_experts":
+            return self.stats()[name]
+        raise AttributeError(name)
+
+    def __setattr__(self, name, value):
+        if name == "bypass_oversized_experts":
+            check(self.L.objeta_hip_cache_set_bypass_oversized_experts(self.h, 1 if value else 0))
+        else:
+            object.__setattr__(self, name, value)
+
+    def get(self, key: ExpertCacheKey):
+        """get (moe.rs:113-122): device address on a hit, None on a miss."""
+        hit, ptr, n = C.c_int32(), C.c_void_p(), C.c_uint64()
+        k = key.c()
+        check(self.L.objeta_hip_cache_get(self.h, C.byref(k), C.byref(hit), C.byref(ptr), C.byref(n)))
+        return (ptr.value or 0) if hit.value else None
+
+    def insert(self, key: ExpertCacheKey, data: np.ndarray, stream=None):
+        """insert (moe.rs:124-158) of host bytes; returns (device address, cached)."""
+        a = np.ascontiguousarray(data).view(np.uint8).ravel()
+        ptr, cached = C.c_void_p(), C.c_int32()
+        k = key.c()
+        check(self.L.objeta_hip_cache_insert(self.h, C.byref(k), a.ctypes.data_as(C.c_void_p), a.nbytes, stream,
+                                             C.byref(ptr), C.byref(cached)))
+        return ptr.value or 0, bool(cached.value)
+
+    def get_or_insert(self, key: ExpertCacheKey, data: np.ndarray, stream=None):
+        """get, then insert on a miss (README.md:123); returns (address, hit, cached)."""
+        a = np.ascontiguousarray(data).view(np.uint8).ravel()
+        ptr, hit, cached = C.c_void_p(), C.c_int32(), C.c_int32()
+        k = key.c()
+        check(self.L.objeta_hip_cache_get_or_insert(self.h, C.byref(k), a.ctypes.data_as(C.c_void_p), a.nbytes,
+                                                    stream, C.byref(ptr), C.byref(hit), C.byref(cached)))
+        return ptr.value or 0, bool(hit.value), bool(cached.value)
+
+    def insert_pinned(self, key: ExpertCacheKey, data: np.ndarray, stream=None) -> int:
+        a = np.ascontiguousarray(data).view(np.uint8).ravel()
+        ptr = C.c_void_p()
+        k = key.c()
+        check(self.L.objeta_hip_cache_insert_pinned(self.h, C.byref(k), a.ctypes.data_as(C.c_void_p), a.nbytes,
+                                                    stream, C.byref(ptr)))
+        return ptr.value or 0
+
+    def release_transient(self, ptr: int) -> None:
+        check(self.L.objeta_hip_cache_release_transient(self.h, C.c_void_p(ptr)))
+
+    def pin(self, key: ExpertCacheKey) -> None:
+        k = key.c()
+        check(self.L.objeta_hip_cache_pin(self.h, C.byref(k)))
+
+    def touch(self, key: ExpertCacheKey) -> None:
+        k = key.c()
+        check(self.L.objeta_hip_cache_touch(self.h, C.byref(k)))
+
+    def evict_lru(self):
+        ev, k = C.c_int32(), CacheKey()
+        check(self.L.objeta_hip_cache_evict_lru(self.h, C.byref(ev), C.byref(k)))
+        if not ev.value:
+            return None
+        return ExpertCacheKey(k.layer_id, k.expert_id, ExpertTensorKind(k.tensor_kind), QuantFormat(k.quant_format))
+
+    def clear(self) -> None:
+        check(self.L.objeta_hip_cache_clear(self.h))
+
+    def reset_counters(self) -> None:
+        check(self.L.objeta_hip_cache_reset_counters(self.h))
+
+    def order(self) -> list:
+        n = C.c_uint64()
+        check(self.L.objeta_hip_cache_order(self.h, None, 0, C.byref(n)))
+        arr = (CacheKey * max(1, n.value))()
+        check(self.L.objeta_hip_cache_order(self.h, arr, n.value, C.byref(n)))
+        return [(k.layer_id, k.expert_id, k.tensor_kind, k.quant_format) for k in arr[:n.value]]
+
+
+def _telemetry_moe(t: MoeTelemetry) -> dict:
+    d = {k: getattr(t, k) for k, _ in MoeTelemetry._fields_}
+    d["bytes_by_tensor_kind"] = {"gate": d.pop("bytes_by_tensor_kind_gate"), "up": d.pop("bytes_by_tensor_kind_up"),
+                                 "down": d.pop("bytes_by_tensor_kind_down")}
+    return d
+
+
+def _execute(backend: HipBackend, fmt: int, stream, experts, selected, x, hidden, inter, out_dim, layer_id,
+             cache: ExpertCache | None):
+    keep = []
+    arr = (HostExpert * max(1, len(experts)))()
+    for i, e in enumerate(experts):
+        parts = [np.ascontiguousarray(p).view(np.uint8).ravel() for p in e]
+        keep += parts
+        v = []
+        for p in parts:
+            v += [p.ctypes.data, p.nbytes]
+        v += [0] * (12 - len(v))
+        if len(parts) == 6:  # (gate_w, gate_s, up_w, up_s, down_w, down_s)
+            g, gs, u, us, d, ds = parts
+            v = [g.ctypes.data, g.nbytes, u.ctypes.data, u.nbytes, d.ctypes.data, d.nbytes,
+                 gs.ctypes.data, gs.nbytes, us.ctypes.data, us.nbytes, ds.ctypes.data, ds.nbytes]
+        arr[i] = HostExpert(*v)
+    ids = np.array([s[0] for s in selected], np.uint64)
+    ws = np.array([s[1] for s in selected], np.float32)
+    xv = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros(max(out_dim, 1), np.float32)
+    tel = MoeTelemetry()
+    check(backend.L.objeta_hip_moe_execute_selected(
+        backend.ctx, int(fmt), stream, arr, len(experts), ids.ctypes.data_as(C.c_void_p),
+        ws.ctypes.data_as(C.c_void_p), ids.size, xv.ctypes.data_as(C.c_void_p), xv.size, hidden, inter, out_dim,
+        layer_id, cache.h if cache is not None else None, out.ctypes.data_as(C.c_void_p), C.byref(tel)))
+    return out[:out_dim], _telemetry_moe(tel)
+
+
+def _moe_execute_selected(self, quant, stream, experts, selected_experts, x, hidden: int, intermediate: int,
+                          out_dim: int, layer_id: int, cache: ExpertCache | None = None, fmt=QuantFormat.Q4_0):
+    """execute_selected_moe_cuda (moe.rs:352-751): experts = [(w_gate, w_up, w_down)] host
+    bytes; selected_experts = [(expert_id, weight)]. Returns (out, telemetry)."""
+    return _execute(self.backend, int(fmt), stream, experts, selected_experts, x, hidden, intermediate, out_dim,
+                    layer_id, cache)
+
+
+def _moe_execute_native_fp4(self, quant, stream, experts, selected_experts, x, hidden: int, intermediate: int,
+                            out_dim: int, layer_id: int, cache: ExpertCache | None = None):
+    """execute_selected_moe_native_fp4_cuda (moe.rs:816-1280): experts =
+    [(gate_w, gate_s, up_w, up_s, down_w, down_s)] split-FP4 host bytes."""
+    return _execute(self.backend, int(QuantFormat.DeepSeekFp4E2M1), stream, experts, selected_experts, x, hidden,
+                    intermediate, out_dim, layer_id, cache)
+
+
+MoeExecutor.execute_selected_moe = _moe_execute_selected
+MoeExecutor.execute_selected_moe_cuda = _moe_execute_selected
+MoeExecutor.execute_selected_moe_native_fp4 = _moe_execute_native_fp4
+MoeExecutor.execute_selected_moe_native_fp4_cuda = _moe_execute_native_fp4

@@ -1,0 +1,923 @@
+// expert_cache.cpp — single-GPU VRAM expert cache and the host-in/host-out
+// selected-expert MoE executor.
+//
+// Cache semantics follow CudaExpertCache (crates/objeta-cuda/src/moe.rs:70-226):
+// an LRU order over tensors, pinned entries that eviction skips, an insert that
+// bypasses tensors larger than the capacity, and the reference's counters.
+// Differences of mechanism, not of semantics:
+//   * LRU lookups are O(1) (list + iterator map) instead of Vec scans.
+//   * Device memory is recycled, not freed: an evicted tensor's block returns to a
+//     size-keyed free list together with events recorded on every stream of the
+//     context at the moment it was released; a later insert of the same size makes
+//     its copy stream wait for those events, so the block is never overwritten
+//     while a kernel enqueued before the eviction may still read it. The reference
+//     gets the same guarantee from Arc + stream-ordered frees (moe.rs:117,155).
+//   * Blocks referenced by an executor call in flight are not recycled until the
+//     call releases them (the reference's Arc clones held by the executor).
+//   * When only pinned entries remain, insert stops evicting and admits the tensor
+//     over capacity instead of looping forever (moe.rs:145-147).
+//
+// The executor follows execute_selected_moe_cuda (moe.rs:352-751) and
+// execute_selected_moe_native_fp4_cuda (moe.rs:816-1280): same validation,
+// admission, cache keys and byte accounting, but the weight copies of misses go
+// to the context's copy stream from the caller's host memory, and each expert's
+// fused kernels wait only for its own copies, so copies overlap compute. With no
+// misses the call is one fused launch pair for all selected experts.
+#include <algorithm>
+#include <cstring>
+#include <list>
+#include <map>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "host_common.hpp"
+#include "kernels.hpp"
+
+namespace objeta {
+namespace {
+
+struct Key {
+    uint64_t layer, expert;
+    int32_t kind, fmt;
+    bool operator==(const Key& o) const {
+        return layer == o.layer && expert == o.expert && kind == o.kind && fmt == o.fmt;
+    }
+};
+struct KeyHash {
+    size_t operator()(const Key& k) const {
+        uint64_t h = k.layer * 0x9E3779B97F4A7C15ull ^ (k.expert + 0x632BE59BD9B4E019ull);
+        h ^= (static_cast<uint64_t>(static_cast<uint32_t>(k.kind)) << 32) | static_cast<uint32_t>(k.fmt);
+        h ^= h >> 29;
+        return static_cast<size_t>(h * 0xBF58476D1CE4E5B9ull);
+    }
+};
+Key to_key(const objeta_hip_cache_key& k) { return Key{k.layer_id, k.expert_id, k.tensor_kind, k.quant_format}; }
+objeta_hip_cache_key from_key(const Key& k) {
+    objeta_hip_cache_key o{};
+    o.layer_id = k.layer;
+    o.expert_id = k.expert;
+    o.tensor_kind = k.kind;
+    o.quant_format = k.fmt;
+    return o;
+}
+
+struct Block {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    int refs = 0;          // executor references of a call in flight
+    bool in_cache = false;  // owned by a cache entry
+    std::vector<hipEvent_t> fence;
+};
+
+}  // namespace
+}  // namespace objeta
+
+struct objeta_hip_expert_cache {
+    objeta_hip_context* ctx = nullptr;  // NULL: accounting only
+    objeta_hip_cache_stats st{};
+    struct Entry {
+        objeta::Block* blk;
+        size_t size;
+        std::list<objeta::Key>::iterator pos;
+    };
+    std::unordered_map<objeta::Key, Entry, objeta::KeyHash> map;
+    std::list<objeta::Key> order;  // front = least recently used
+    std::unordered_set<objeta::Key, objeta::KeyHash> pinned;
+    std::multimap<size_t, objeta::Block*> free_blocks;  // recycled, fenced
+    std::unordered_map<const void*, objeta::Block*> transients;
+    std::vector<hipEvent_t> event_pool;
+    size_t free_bytes = 0;
+    size_t device_bytes = 0;  // all blocks allocated by this cache
+};
+
+namespace objeta {
+namespace {
+
+using Cache = objeta_hip_expert_cache;
+
+size_t free_list_cap(const Cache* c) {
+    const size_t floor = size_t(64) << 20;
+    return c->st.capacity_bytes > floor ? static_cast<size_t>(c->st.capacity_bytes) : floor;
+}
+
+hipEvent_t take_event(Cache* c) {
+    if (!c->event_pool.empty()) {
+        hipEvent_t e = c->event_pool.back();
+        c->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return e;
+}
+
+// Records, on every stream of the context, the point after which `b` is free.
+void fence_block(Cache* c, Block* b) {
+    for (hipEvent_t e : b->fence) c->event_pool.push_back(e);
+    b->fence.clear();
+    if (!c->ctx) return;
+    auto rec = [&](hipStream_t s) {
+        hipEvent_t e = take_event(c);
+        if (e && hipEventRecord(e, s) == hipSuccess) b->fence.push_back(e);
+        else if (e) c->event_pool.push_back(e);
+    };
+    for (hipStream_t s : c->ctx->streams) rec(s);
+    rec(c->ctx->copy_stream);
+}
+
+void destroy_block(Cache* c, Block* b) {
+    if (c->ctx && b->ptr) {
+        for (hipEvent_t e : b->fence) (void)hipEventSynchronize(e);
+        (void)hipFree(b->ptr);
+        c->device_bytes -= b->bytes;
+    }
+    for (hipEvent_t e : b->fence) c->event_pool.push_back(e);
+    delete b;
+}
+
+// A block left the cache or a call: recycle it once nothing references it.
+void retire_block(Cache* c, Block* b) {
+    if (b->in_cache || b->refs > 0) return;
+    fence_block(c, b);
+    c->free_blocks.emplace(b->bytes, b);
+    c->free_bytes += b->bytes;
+    while (c->free_bytes > free_list_cap(c) && !c->free_blocks.empty()) {
+        auto it = c->free_blocks.begin();  // smallest first
+        Block* v = it->second;
+        c->free_blocks.erase(it);
+        c->free_bytes -= v->bytes;
+        destroy_block(c, v);
+    }
+}
+
+// A block of exactly `bytes` whose previous contents may be overwritten by work
+// enqueued on `s` from now on.
+int32_t acquire_block(Cache* c, size_t bytes, hipStream_t s, Block** out) {
+    auto it = c->free_blocks.find(bytes);
+    if (it != c->free_blocks.end()) {
+        Block* b = it->second;
+        c->free_blocks.erase(it);
+        c->free_bytes -= b->bytes;
+        for (hipEvent_t e : b->fence) OBJ_HIP(hipStreamWaitEvent(s, e, 0), "fence recycled cache block");
+        *out = b;
+        return 0;
+    }
+    Block* b = new Block();
+    b->bytes = bytes;
+    if (c->ctx && bytes) {
+        hipError_t e = hipMalloc(&b->ptr, bytes);
+        if (e != hipSuccess && !c->free_blocks.empty()) {
+            (void)hipGetLastError();
+            while (!c->free_blocks.empty()) {  // give recycled memory back and retry
+                auto v = c->free_blocks.begin();
+                Block* blk = v->second;
+                c->free_blocks.erase(v);
+                c->free_bytes -= blk->bytes;
+                destroy_block(c, blk);
+            }
+            e = hipMalloc(&b->ptr, bytes);
+        }
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            delete b;
+            OBJ_FAIL(kDriver, strf("allocate cache block of %zu bytes", bytes), hipGetErrorString(e));
+        }
+        c->device_bytes += bytes;
+    }
+    *out = b;
+    return 0;
+}
+
+// Copies host bytes into a block on the copy stream, ordered after `s`.
+int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t s) {
+    if (!c->ctx || n == 0) return 0;
+    if (!h_src) OBJ_FAIL(kInvalidInput, "copy tensor into the cache", "NULL host pointer");
+    hipStream_t cs = c->ctx->copy_stream;
+    hipEvent_t e = take_event(c);
+    if (!e) OBJ_FAIL(kDriver, "copy tensor into the cache", "event creation failed");
+    hipError_t r = hipEventRecord(e, s);
+    if (r == hipSuccess) r = hipStreamWaitEvent(cs, e, 0);
+    c->event_pool.push_back(e);
+    if (r == hipSuccess) r = hipMemcpyAsync(b->ptr, h_src, n, hipMemcpyHostToDevice, cs);
+    if (r != hipSuccess) {
+        (void)hipGetLastError();
+        OBJ_FAIL(kDriver, "copy tensor into the cache", hipGetErrorString(r));
+    }
+    return 0;
+}
+
+// Makes `s` wait for everything enqueued so far on the copy stream.
+int32_t join_copies(Cache* c, hipStream_t s) {
+    if (!c || !c->ctx) return 0;
+    hipEvent_t e = take_event(c);
+    if (!e) OBJ_FAIL(kDriver, "join cache copies", "event creation failed");
+    hipError_t r = hipEventRecord(e, c->ctx->copy_stream);
+    if (r == hipSuccess) r = hipStreamWaitEvent(s, e, 0);
+    c->event_pool.push_back(e);
+    if (r != hipSuccess) {
+        (void)hipGetLastError();
+        OBJ_FAIL(kDriver, "join cache copies", hipGetErrorString(r));
+    }
+    return 0;
+}
+
+void touch(Cache* c, const Key& k) {  // moe.rs:160-165
+    auto it = c->map.find(k);
+    if (it == c->map.end()) return;
+    c->order.splice(c->order.end(), c->order, it->second.pos);
+}
+
+bool evict_lru(Cache* c, Key* out) {  // moe.rs:167-180
+    for (auto it = c->order.begin(); it != c->order.end(); ++it) {
+        if (c->pinned.count(*it)) continue;
+        const Key k = *it;
+        c->order.erase(it);
+        auto m = c->map.find(k);
+        Block* b = m->second.blk;
+        c->st.resident_bytes -= m->second.size;
+        c->st.eviction_count += 1;
+        c->map.erase(m);
+        b->in_cache = false;
+        retire_block(c, b);
+        if (out) *out = k;
+        return true;
+    }
+    return false;
+}
+
+void remove_existing(Cache* c, const Key& k) {
+    auto m = c->map.find(k);
+    if (m == c->map.end()) return;
+    c->st.resident_bytes -= m->second.size;
+    c->order.erase(m->second.pos);
+    Block* b = m->second.blk;
+    c->map.erase(m);
+    b->in_cache = false;
+    retire_block(c, b);
+}
+
+void make_room(Cache* c, size_t size) {
+    while (c->st.resident_bytes + size > c->st.capacity_bytes && !c->order.empty())
+        if (!evict_lru(c, nullptr)) break;
+}
+
+Block* lookup(Cache* c, const Key& k) {  // get (moe.rs:113-122)
+    auto it = c->map.find(k);
+    if (it == c->map.end()) {
+        c->st.miss_count += 1;
+        return nullptr;
+    }
+    c->st.hit_count += 1;
+    c->order.splice(c->order.end(), c->order, it->second.pos);
+    return it->second.blk;
+}
+
+// insert (moe.rs:124-158) of a filled block. Returns false (block untouched and
+// still owned by the caller) when the tensor is larger than the capacity.
+bool insert_block(Cache* c, const Key& k, Block* b, size_t size) {
+    c->st.cache_insert_attempt_count += 1;
+    if (size > c->st.capacity_bytes) {
+        c->st.oversized_tensor_bypass_count += 1;
+        c->st.cache_insert_bypass_count += 1;
+        return false;
+    }
+    c->st.cache_insert_accept_count += 1;
+    remove_existing(c, k);
+    make_room(c, size);
+    c->order.push_back(k);
+    b->in_cache = true;
+    c->map.emplace(k, Cache::Entry{b, size, std::prev(c->order.end())});
+    c->st.resident_bytes += size;
+    return true;
+}
+
+// A filled block for host bytes: recycled or new, copy enqueued after `s`.
+int32_t stage_tensor(Cache* c, const void* h_src, size_t n, hipStream_t s, Block** out) {
+    Block* b = nullptr;
+    OBJ_TRY(acquire_block(c, n, c->ctx ? c->ctx->copy_stream : nullptr, &b));
+    int32_t rc = fill_block(c, b, h_src, n, s);
+    if (rc) {
+        retire_block(c, b);
+        return rc;
+    }
+    *out = b;
+    return 0;
+}
+
+int32_t check_cache(const objeta_hip_expert_cache* c, const char* action) {
+    if (!c) OBJ_FAIL(kInvalidInput, action, "cache is NULL");
+    return 0;
+}
+
+// Frees every device block and event of `c` (the context is going away).
+void release_device(Cache* c) {
+    if (!c->ctx) return;
+    std::vector<Block*> all;
+    for (auto& kv : c->map) all.push_back(kv.second.blk);
+    for (auto& kv : c->free_blocks) all.push_back(kv.second);
+    for (auto& kv : c->transients) all.push_back(kv.second);
+    for (Block* b : all) destroy_block(c, b);
+    c->map.clear();
+    c->order.clear();
+    c->pinned.clear();
+    c->free_blocks.clear();
+    c->transients.clear();
+    c->free_bytes = 0;
+    c->st.resident_bytes = 0;
+    c->st.pinned_bytes = 0;
+    for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
+    c->event_pool.clear();
+    c->ctx = nullptr;
+}
+
+}  // namespace
+
+void detach_caches(objeta_hip_context* ctx) {
+    for (void* p : ctx->caches) release_device(static_cast<Cache*>(p));
+    ctx->caches.clear();
+}
+
+}  // namespace objeta
+
+using namespace objeta;
+
+extern "C" {
+
+int32_t objeta_hip_cache_create(objeta_hip_context* ctx, uint64_t capacity_bytes, objeta_hip_expert_cache** out) {
+    OBJ_GUARD_BEGIN
+    if (!out) OBJ_FAIL(kInvalidInput, "create expert cache", "out is NULL");
+    auto* c = new objeta_hip_expert_cache();
+    c->ctx = ctx;
+    c->st.capacity_bytes = capacity_bytes;
+    if (ctx) ctx->caches.push_back(c);
+    *out = c;
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_destroy(objeta_hip_expert_cache* c) {
+    OBJ_GUARD_BEGIN
+    if (!c) return 0;
+    if (c->ctx) {
+        objeta_hip_context* ctx = c->ctx;
+        (void)hipSetDevice(ctx->device);
+        for (hipStream_t s : ctx->streams) (void)hipStreamSynchronize(s);
+        (void)hipStreamSynchronize(ctx->copy_stream);
+        auto& v = ctx->caches;
+        v.erase(std::remove(v.begin(), v.end(), static_cast<void*>(c)), v.end());
+        release_device(c);
+    } else {
+        std::vector<Block*> all;
+        for (auto& kv : c->map) all.push_back(kv.second.blk);
+        for (auto& kv : c->free_blocks) all.push_back(kv.second);
+        for (auto& kv : c->transients) all.push_back(kv.second);
+        for (Block* b : all) destroy_block(c, b);
+    }
+    delete c;
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_stats_get(const objeta_hip_expert_cache* c, objeta_hip_cache_stats* out) {
+    OBJ_TRY(check_cache(c, "cache stats"));
+    if (!out) OBJ_FAIL(kInvalidInput, "cache stats", "out is NULL");
+    *out = c->st;
+    out->entry_count = c->map.size();
+    out->device_bytes_reserved = c->device_bytes;
+    return 0;
+}
+
+int32_t objeta_hip_cache_set_bypass_oversized_experts(objeta_hip_expert_cache* c, int32_t enable) {
+    OBJ_TRY(check_cache(c, "set bypass_oversized_experts"));
+    c->st.bypass_oversized_experts = enable ? 1 : 0;
+    return 0;
+}
+
+int32_t objeta_hip_cache_get(objeta_hip_expert_cache* c, const objeta_hip_cache_key* key, int32_t* hit,
+                             const void** d_ptr, uint64_t* nbytes) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache get"));
+    if (!key || !hit) OBJ_FAIL(kInvalidInput, "cache get", "NULL argument");
+    Block* b = lookup(c, to_key(*key));
+    *hit = b ? 1 : 0;
+    if (d_ptr) *d_ptr = b ? b->ptr : nullptr;
+    if (nbytes) *nbytes = b ? c->map.find(to_key(*key))->second.size : 0;
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_insert(objeta_hip_expert_cache* c, const objeta_hip_cache_key* key, const void* h_src,
+                                uint64_t nbytes, objeta_hip_stream stream, const void** d_ptr, int32_t* cached) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache insert"));
+    if (!key || !d_ptr || !cached) OBJ_FAIL(kInvalidInput, "cache insert", "NULL argument");
+    hipStream_t s = nullptr;
+    if (c->ctx) {
+        OBJ_HIP(hipSetDevice(c->ctx->device), "hipSetDevice");
+        s = resolve_stream(c->ctx, stream);
+    }
+    Block* b = nullptr;
+    OBJ_TRY(stage_tensor(c, h_src, nbytes, s, &b));
+    if (c->ctx) OBJ_TRY(join_copies(c, s));
+    const bool ok = insert_block(c, to_key(*key), b, nbytes);
+    if (!ok && b->ptr) c->transients[b->ptr] = b;
+    else if (!ok) retire_block(c, b);
+    *cached = ok ? 1 : 0;
+    *d_ptr = b->ptr;
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_get_or_insert(objeta_hip_expert_cache* c, const objeta_hip_cache_key* key,
+                                       const void* h_src, uint64_t nbytes, objeta_hip_stream stream,
+                                       const void** d_ptr, int32_t* hit, int32_t* cached) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache get_or_insert"));
+    if (!key || !d_ptr || !hit || !cached) OBJ_FAIL(kInvalidInput, "cache get_or_insert", "NULL argument");
+    Block* b = lookup(c, to_key(*key));
+    if (b) {
+        *hit = 1;
+        *cached = 1;
+        *d_ptr = b->ptr;
+        return 0;
+    }
+    *hit = 0;
+    return objeta_hip_cache_insert(c, key, h_src, nbytes, stream, d_ptr, cached);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_insert_pinned(objeta_hip_expert_cache* c, const objeta_hip_cache_key* key,
+                                       const void* h_src, uint64_t nbytes, objeta_hip_stream stream,
+                                       const void** d_ptr) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache insert_pinned"));
+    if (!key || !d_ptr) OBJ_FAIL(kInvalidInput, "cache insert_pinned", "NULL argument");
+    hipStream_t s = nullptr;
+    if (c->ctx) {
+        OBJ_HIP(hipSetDevice(c->ctx->device), "hipSetDevice");
+        s = resolve_stream(c->ctx, stream);
+    }
+    const Key k = to_key(*key);
+    make_room(c, nbytes);  // moe.rs:195-199
+    Block* b = nullptr;
+    OBJ_TRY(stage_tensor(c, h_src, nbytes, s, &b));
+    if (c->ctx) OBJ_TRY(join_copies(c, s));
+    remove_existing(c, k);
+    c->order.push_back(k);
+    b->in_cache = true;
+    c->map.emplace(k, Cache::Entry{b, nbytes, std::prev(c->order.end())});
+    c->st.resident_bytes += nbytes;
+    c->st.pinned_bytes += nbytes;
+    c->pinned.insert(k);
+    *d_ptr = b->ptr;
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_pin(objeta_hip_expert_cache* c, const objeta_hip_cache_key* key) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache pin"));
+    if (!key) OBJ_FAIL(kInvalidInput, "cache pin", "key is NULL");
+    const Key k = to_key(*key);
+    auto it = c->map.find(k);
+    if (it != c->map.end() && !c->pinned.count(k)) {
+        c->pinned.insert(k);
+        c->st.pinned_bytes += it->second.size;
+    }
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_touch(objeta_hip_expert_cache* c, const objeta_hip_cache_key* key) {
+    OBJ_TRY(check_cache(c, "cache touch"));
+    if (!key) OBJ_FAIL(kInvalidInput, "cache touch", "key is NULL");
+    touch(c, to_key(*key));
+    return 0;
+}
+
+int32_t objeta_hip_cache_evict_lru(objeta_hip_expert_cache* c, int32_t* evicted, objeta_hip_cache_key* key_out) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache evict_lru"));
+    if (!evicted) OBJ_FAIL(kInvalidInput, "cache evict_lru", "NULL argument");
+    Key k{};
+    *evicted = evict_lru(c, &k) ? 1 : 0;
+    if (*evicted && key_out) *key_out = from_key(k);
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_clear(objeta_hip_expert_cache* c) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache clear"));
+    std::vector<Block*> blocks;
+    for (auto& kv : c->map) blocks.push_back(kv.second.blk);
+    c->map.clear();
+    c->order.clear();
+    c->pinned.clear();
+    c->st.resident_bytes = 0;
+    c->st.pinned_bytes = 0;
+    for (Block* b : blocks) {
+        b->in_cache = false;
+        retire_block(c, b);
+    }
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_reset_counters(objeta_hip_expert_cache* c) {
+    OBJ_TRY(check_cache(c, "cache reset_counters"));
+    c->st.hit_count = c->st.miss_count = c->st.eviction_count = 0;
+    c->st.cache_insert_attempt_count = c->st.cache_insert_accept_count = c->st.cache_insert_bypass_count = 0;
+    c->st.oversized_tensor_bypass_count = c->st.oversized_expert_bypass_count = 0;
+    c->st.self_eviction_risk_count = 0;
+    return 0;
+}
+
+int32_t objeta_hip_cache_release_transient(objeta_hip_expert_cache* c, const void* d_ptr) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "release transient tensor"));
+    auto it = c->transients.find(d_ptr);
+    if (it == c->transients.end()) OBJ_FAIL(kInvalidInput, "release transient tensor", "unknown device pointer");
+    Block* b = it->second;
+    c->transients.erase(it);
+    retire_block(c, b);
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_order(const objeta_hip_expert_cache* c, objeta_hip_cache_key* keys, uint64_t cap,
+                               uint64_t* n) {
+    OBJ_TRY(check_cache(c, "cache order"));
+    if (!n) OBJ_FAIL(kInvalidInput, "cache order", "n is NULL");
+    uint64_t i = 0;
+    for (const Key& k : c->order) {
+        if (keys && i < cap) keys[i] = from_key(k);
+        ++i;
+    }
+    *n = i;
+    return 0;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ executor
+namespace objeta {
+namespace {
+
+struct TensorRef {
+    const void* h;
+    uint64_t len;
+    int32_t kind;
+    bool scale;
+};
+
+const char* tensor_label(int32_t kind) {
+    switch (kind) {
+        case OBJETA_HIP_TENSOR_GATE: return "w_gate";
+        case OBJETA_HIP_TENSOR_UP: return "w_up";
+        case OBJETA_HIP_TENSOR_DOWN: return "w_down";
+        case OBJETA_HIP_TENSOR_GATE_WEIGHT: return "gate_weight";
+        case OBJETA_HIP_TENSOR_GATE_SCALE: return "gate_scale";
+        case OBJETA_HIP_TENSOR_UP_WEIGHT: return "up_weight";
+        case OBJETA_HIP_TENSOR_UP_SCALE: return "up_scale";
+        case OBJETA_HIP_TENSOR_DOWN_WEIGHT: return "down_weight";
+        default: return "down_scale";
+    }
+}
+
+// Per-context pool for transient (uncached) tensor copies; destroyed with the context.
+Cache* transient_pool(objeta_hip_context* ctx) {
+    if (!ctx->transient_pool) {
+        Cache* c = new Cache();
+        c->ctx = ctx;
+        c->st.capacity_bytes = 0;
+        ctx->transient_pool = c;
+    }
+    return static_cast<Cache*>(ctx->transient_pool);
+}
+
+float elapsed(hipEvent_t a, hipEvent_t b) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, a, b) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0.f;
+    }
+    return ms;
+}
+
+}  // namespace
+}  // namespace objeta
+
+extern "C" int32_t objeta_hip_moe_execute_selected(
+    objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream, const objeta_hip_host_expert* experts,
+    uint64_t n_experts, const uint64_t* sel_ids, const float* sel_weights, uint64_t n_selected, const float* x,
+    uint64_t x_len, uint64_t hidden, uint64_t intermediate, uint64_t out_dim, uint64_t layer_id,
+    objeta_hip_expert_cache* cache, float* out, objeta_hip_moe_telemetry* tel) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "execute_selected_moe"));
+    const bool fp4 = format == OBJETA_HIP_FP4_E2M1;
+    if (format < OBJETA_HIP_Q4_0 || format > OBJETA_HIP_FP4_E2M1)
+        OBJ_FAIL(kUnsupported, "validate MoE format", strf("unsupported MoE format %d", format));
+    if (cache && cache->ctx && cache->ctx != ctx)
+        OBJ_FAIL(kInvalidInput, "validate expert cache", "cache belongs to another context");
+    // ---- validation (moe.rs:366-422, 830-925)
+    if (x_len != hidden)
+        OBJ_FAIL(kInvalidInput,
+                 fp4 ? "validate execute_selected_moe_native_fp4_cuda input x size"
+                     : "validate execute_selected_moe_cuda input x size",
+                 strf("x len %llu != hidden %llu", (unsigned long long)x_len, (unsigned long long)hidden));
+    if (n_selected && (!sel_ids || !sel_weights)) OBJ_FAIL(kInvalidInput, "validate selection", "NULL selection");
+    if ((hidden && !x) || (out_dim && !out)) OBJ_FAIL(kInvalidInput, "validate buffers", "NULL host pointer");
+    const int32_t bb = objeta_hip_block_bytes(format);
+    const uint64_t gu_w = fp4 ? intermediate * (hidden / 2) : intermediate * (hidden / 32) * bb;
+    const uint64_t gu_s = fp4 ? intermediate * (hidden / 32) : 0;
+    const uint64_t dn_w = fp4 ? out_dim * (intermediate / 2) : out_dim * (intermediate / 32) * bb;
+    const uint64_t dn_s = fp4 ? out_dim * (intermediate / 32) : 0;
+    auto tensors_of = [&](const objeta_hip_host_expert& e, TensorRef* t) -> int {
+        if (!fp4) {
+            t[0] = {e.gate, e.gate_len, OBJETA_HIP_TENSOR_GATE, false};
+            t[1] = {e.up, e.up_len, OBJETA_HIP_TENSOR_UP, false};
+            t[2] = {e.down, e.down_len, OBJETA_HIP_TENSOR_DOWN, false};
+            return 3;
+        }
+        t[0] = {e.gate, e.gate_len, OBJETA_HIP_TENSOR_GATE_WEIGHT, false};
+        t[1] = {e.gate_scale, e.gate_scale_len, OBJETA_HIP_TENSOR_GATE_SCALE, true};
+        t[2] = {e.up, e.up_len, OBJETA_HIP_TENSOR_UP_WEIGHT, false};
+        t[3] = {e.up_scale, e.up_scale_len, OBJETA_HIP_TENSOR_UP_SCALE, true};
+        t[4] = {e.down, e.down_len, OBJETA_HIP_TENSOR_DOWN_WEIGHT, false};
+        t[5] = {e.down_scale, e.down_scale_len, OBJETA_HIP_TENSOR_DOWN_SCALE, true};
+        return 6;
+    };
+    for (uint64_t i = 0; i < n_selected; ++i) {
+        const uint64_t e = sel_ids[i];
+        if (e >= n_experts)
+            OBJ_FAIL(kInvalidInput, "validate expert index",
+                     strf("expert index %llu out of bounds (len=%llu)", (unsigned long long)e,
+                          (unsigned long long)n_experts));
+        TensorRef t[6];
+        const int nt = tensors_of(experts[e], t);
+        for (int j = 0; j < nt; ++j) {
+            const uint64_t want = (j < 2 * (nt / 3)) ? (t[j].scale ? gu_s : gu_w) : (t[j].scale ? dn_s : dn_w);
+            if (t[j].len != want)
+                OBJ_FAIL(kInvalidInput, strf("validate expert %s size", tensor_label(t[j].kind)),
+                         strf("%s len %llu != expected %llu", tensor_label(t[j].kind), (unsigned long long)t[j].len,
+                              (unsigned long long)want));
+        }
+    }
+    if (n_selected > 32) OBJ_FAIL(kInvalidInput, "validate selection", "at most 32 selected experts per call");
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    const uint64_t k = n_selected;
+
+    // ---- telemetry events
+    hipEvent_t ev[8] = {};
+    for (auto& e : ev) OBJ_HIP(hipEventCreate(&e), "create telemetry event");
+    struct EvGuard {
+        hipEvent_t* e;
+        ~EvGuard() {
+            for (int i = 0; i < 8; ++i)
+                if (e[i]) (void)hipEventDestroy(e[i]);
+        }
+    } evg{ev};
+    enum { T0, X0, X1, GU0, GU1, DN1, D2H0, T1 };
+    OBJ_HIP(hipEventRecord(ev[T0], s), "record event");
+
+    // ---- device scratch: [x | out | weights | table] and host staging
+    const size_t x_b = (hidden * 4 + 255) & ~size_t(255);
+    const size_t o_b = (out_dim * 4 + 255) & ~size_t(255);
+    const size_t w_b = 256;
+    const size_t t_b = (k ? k : 1) * sizeof(objeta_hip_expert_ptrs);
+    void* dws = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsMoeTable, x_b + o_b + w_b + t_b, &dws));
+    void* hst = nullptr;
+    OBJ_TRY(ensure_host_stage(ctx, x_b + w_b + t_b + o_b, &hst));
+    char* d0 = static_cast<char*>(dws);
+    float* d_x = reinterpret_cast<float*>(d0);
+    float* d_out = reinterpret_cast<float*>(d0 + x_b);
+    float* d_w = reinterpret_cast<float*>(d0 + x_b + o_b);
+    objeta_hip_expert_ptrs* d_tab = reinterpret_cast<objeta_hip_expert_ptrs*>(d0 + x_b + o_b + w_b);
+    char* h0 = static_cast<char*>(hst);
+    std::memcpy(h0, x, hidden * 4);
+    if (k) std::memcpy(h0 + x_b + o_b, sel_weights, k * 4);
+    objeta_hip_expert_ptrs* h_tab = reinterpret_cast<objeta_hip_expert_ptrs*>(h0 + x_b + o_b + w_b);
+    float* h_out = reinterpret_cast<float*>(h0 + x_b);
+    OBJ_HIP(hipEventRecord(ev[X0], s), "record event");
+    OBJ_HIP(hipMemcpyAsync(d_x, h0, hidden * 4, hipMemcpyHostToDevice, s), "moe_x_h2d");
+    OBJ_HIP(hipEventRecord(ev[X1], s), "record event");
+
+    // ---- weights: cache admission and copies (moe.rs:458-583, 1000-1100)
+    Cache* pool = transient_pool(ctx);
+    std::vector<std::pair<Cache*, Block*>> held;  // (home, block) references of this call
+    std::vector<hipEvent_t> ready(k, nullptr);
+    hipEvent_t c0 = nullptr, c1 = nullptr;  // copy stream span of this call's weight copies
+    OBJ_HIP(hipEventCreate(&c0), "create telemetry event");
+    struct CopyEvGuard {
+        hipEvent_t& a;
+        hipEvent_t& b;
+        ~CopyEvGuard() {
+            if (a) (void)hipEventDestroy(a);
+            if (b) (void)hipEventDestroy(b);
+        }
+    } cg{c0, c1};
+    OBJ_HIP(hipEventCreate(&c1), "create telemetry event");
+    OBJ_HIP(hipEventRecord(c0, ctx->copy_stream), "record event");
+    uint64_t w_loaded = 0, w_reused = 0, s_loaded = 0, s_reused = 0, logical = 0;
+    uint64_t by_kind[3] = {0, 0, 0};
+    std::vector<uint64_t> uniq(sel_ids, sel_ids + k);
+    std::sort(uniq.begin(), uniq.end());
+    uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
+    const uint64_t single_expert_bytes = 2 * (gu_w + gu_s) + dn_w + dn_s;
+    bool any_copy = false;
+    int32_t rc = 0;
+    auto release_all = [&]() {
+        for (auto& hb : held) {
+            hb.second->refs -= 1;
+            retire_block(hb.first, hb.second);
+        }
+        held.clear();
+    };
+    for (uint64_t j = 0; j < k && rc == 0; ++j) {
+        const uint64_t e = sel_ids[j];
+        TensorRef t[6];
+        const int nt = tensors_of(experts[e], t);
+        uint64_t eb = 0;
+        for (int q = 0; q < nt; ++q) eb += t[q].len;
+        logical += eb;
+        by_kind[0] += t[0].len + (fp4 ? t[1].len : 0);
+        by_kind[1] += fp4 ? t[2].len + t[3].len : t[1].len;
+        by_kind[2] += fp4 ? t[4].len + t[5].len : t[2].len;
+        bool bypass = false;
+        if (cache && eb > cache->st.capacity_bytes) {
+            if (cache->st.bypass_oversized_experts) {
+                bypass = true;
+                cache->st.oversized_expert_bypass_count += 1;
+            } else {
+                cache->st.self_eviction_risk_count += 1;
+            }
+        }
+        const void* dptr[6] = {};
+        bool copied = false;
+        for (int q = 0; q < nt && rc == 0; ++q) {
+            const Key key{layer_id, e, t[q].kind, format};
+            Block* b = nullptr;
+            bool hit = false;
+            if (bypass) {
+                cache->st.cache_insert_attempt_count += 1;
+                cache->st.cache_insert_bypass_count += 1;
+            } else if (cache) {
+                b = lookup(cache, key);
+                hit = b != nullptr;
+            }
+            Cache* home = cache && !bypass ? cache : pool;
+            if (!hit) {
+                rc = stage_tensor(home, t[q].h, t[q].len, s, &b);
+                if (rc) break;
+                copied = true;
+                if (cache && !bypass) (void)insert_block(cache, key, b, t[q].len);
+            }
+            b->refs += 1;
+            held.push_back({home, b});
+            dptr[q] = b->ptr;
+            if (hit) (t[q].scale ? s_reused : w_reused) += t[q].len;
+            else (t[q].scale ? s_loaded : w_loaded) += t[q].len;
+        }
+        if (rc) break;
+        if (copied) {
+            any_copy = true;
+            hipEvent_t r = nullptr;
+            if (hipEventCreateWithFlags(&r, hipEventDisableTiming) != hipSuccess ||
+                hipEventRecord(r, ctx->copy_stream) != hipSuccess) {
+                (void)hipGetLastError();
+                rc = set_error(kDriver, __FILE__, __LINE__, __func__, "record copy event", "event failure");
+                if (r) (void)hipEventDestroy(r);
+                break;
+            }
+            ready[j] = r;
+        }
+        objeta_hip_expert_ptrs& p = h_tab[j];
+        if (fp4) p = {dptr[0], dptr[2], dptr[4], dptr[1], dptr[3], dptr[5]};
+        else p = {dptr[0], dptr[1], dptr[2], nullptr, nullptr, nullptr};
+    }
+    auto destroy_ready = [&]() {
+        for (hipEvent_t r : ready)
+            if (r) (void)hipEventDestroy(r);
+    };
+    if (rc) {
+        (void)hipStreamSynchronize(ctx->copy_stream);
+        release_all();
+        destroy_ready();
+        return rc;
+    }
+    OBJ_HIP(hipEventRecord(c1, ctx->copy_stream), "record event");
+
+    // ---- compute
+    do {
+        if (k) {
+            hipError_t e = hipMemcpyAsync(d_w, h0 + x_b + o_b, w_b + t_b, hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                rc = set_error(kDriver, __FILE__, __LINE__, __func__, "moe_table_h2d", hipGetErrorString(e));
+                break;
+            }
+        }
+        float* act = nullptr;
+        if ((rc = moe_act_scratch(ctx, s, 1, k ? k : 1, intermediate ? intermediate : 1, &act))) break;
+        (void)hipEventRecord(ev[GU0], s);
+        if (k == 0) {
+            if ((rc = launch_zero(s, d_out, out_dim * 4))) break;
+            (void)hipEventRecord(ev[GU1], s);
+        } else if (!any_copy) {
+            if ((rc = launch_moe_gate_up(ctx, format, s, d_tab, k, nullptr, 1, k, d_x, act, hidden, intermediate, 0.f)))
+                break;
+            (void)hipEventRecord(ev[GU1], s);
+            if ((rc = launch_moe_down(ctx, format, s, d_tab, k, nullptr, d_w, 1, k, act, nullptr, d_out, intermediate,
+                                      out_dim)))
+                break;
+        } else {
+            // expert by expert, each waiting only for its own copies
+            for (uint64_t j = 0; j < k && rc == 0; ++j) {
+                if (ready[j]) {
+                    hipError_t e = hipStreamWaitEvent(s, ready[j], 0);
+                    if (e != hipSuccess) {
+                        (void)hipGetLastError();
+                        rc = set_error(kDriver, __FILE__, __LINE__, __func__, "wait expert copies", hipGetErrorString(e));
+                        break;
+                    }
+                }
+                rc = launch_moe_gate_up(ctx, format, s, d_tab + j, 1, nullptr, 1, 1, d_x, act, hidden, intermediate, 0.f);
+                if (!rc)
+                    rc = launch_moe_down(ctx, format, s, d_tab + j, 1, nullptr, d_w + j, 1, 1, act, j ? d_out : nullptr,
+                                         d_out, intermediate, out_dim);
+            }
+            (void)hipEventRecord(ev[GU1], s);
+        }
+        if (rc) break;
+        (void)hipEventRecord(ev[DN1], s);
+        (void)hipEventRecord(ev[D2H0], s);
+        hipError_t e = hipMemcpyAsync(h_out, d_out, out_dim * 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipEventRecord(ev[T1], s);
+        if (e == hipSuccess) e = hipEventSynchronize(ev[T1]);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            rc = set_error(kDriver, __FILE__, __LINE__, __func__, "moe_d2h", hipGetErrorString(e));
+        }
+    } while (false);
+    if (rc) {
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamSynchronize(ctx->copy_stream);
+        release_all();
+        destroy_ready();
+        return rc;
+    }
+    std::memcpy(out, h_out, out_dim * 4);
+    release_all();
+    destroy_ready();
+
+    // ---- telemetry (moe.rs:664-748)
+    const uint64_t loaded = w_loaded + s_loaded, reused = w_reused + s_reused;
+    if (logical != loaded + reused)
+        OBJ_FAIL(kInternal, "MoE byte invariant", "logical_expert_bytes_requested != loaded + reused");
+    if (tel) {
+        objeta_hip_moe_telemetry t{};
+        t.selected_expert_count = k;
+        t.logical_expert_bytes_requested = logical;
+        t.actual_expert_bytes_loaded = loaded;
+        t.resident_cache_bytes_reused = reused;
+        t.weight_bytes_loaded = w_loaded;
+        t.weight_bytes_reused = w_reused;
+        t.scale_bytes_loaded = s_loaded;
+        t.scale_bytes_reused = s_reused;
+        if (cache) {
+            t.resident_cache_resident_bytes = cache->st.resident_bytes;
+            t.resident_cache_capacity_bytes = cache->st.capacity_bytes;
+            t.resident_cache_hit_count = cache->st.hit_count;
+            t.resident_cache_miss_count = cache->st.miss_count;
+            t.resident_cache_eviction_count = cache->st.eviction_count;
+            t.resident_cache_insert_attempt_count = cache->st.cache_insert_attempt_count;
+            t.resident_cache_insert_accept_count = cache->st.cache_insert_accept_count;
+            t.resident_cache_insert_bypass_count = cache->st.cache_insert_bypass_count;
+            t.resident_cache_oversized_tensor_bypass_count = cache->st.oversized_tensor_bypass_count;
+            t.resident_cache_oversized_expert_bypass_count = cache->st.oversized_expert_bypass_count;
+            t.resident_cache_self_eviction_risk_count = cache->st.self_eviction_risk_count;
+        }
+        t.h2d_ms = elapsed(ev[X0], ev[X1]) + (any_copy ? elapsed(c0, c1) : 0.f);
+        t.gate_up_qgemv_ms = elapsed(ev[GU0], ev[GU1]);
+        t.down_qgemv_ms = elapsed(ev[GU1], ev[DN1]);
+        const float d2h = elapsed(ev[D2H0], ev[T1]);
+        t.total_ms = elapsed(ev[T0], ev[T1]);
+        const float un = t.total_ms - t.h2d_ms - t.gate_up_qgemv_ms - t.down_qgemv_ms - d2h;
+        t.unaccounted_ms = un > 0.f ? un : 0.f;
+        t.bytes_by_tensor_kind_gate = by_kind[0];
+        t.bytes_by_tensor_kind_up = by_kind[1];
+        t.bytes_by_tensor_kind_down = by_kind[2];
+        t.bytes_per_expert = single_expert_bytes;
+        t.selected_working_set_bytes = uniq.size() * single_expert_bytes;
+        *tel = t;
+    }
+    return 0;
+    OBJ_GUARD_END
+}

@@ -83,6 +83,8 @@ struct objeta_hip_context {
     objeta::Workspace ws[objeta::kWsSlots];  // scratch for multi-kernel entry points
     std::vector<void*> retired_ws;           // replaced regions, freed at destroy
     void* host_stage = nullptr;              // pinned host staging (expert tables)
+    void* transient_pool = nullptr;          // objeta_hip_expert_cache for uncached copies
+    std::vector<void*> caches;               // live caches created on this context
     size_t host_stage_bytes = 0;
     uint32_t* counters = nullptr;       // zero-initialised device counters (self-resetting),
                                         // followed by the device error word
@@ -98,6 +100,9 @@ hipStream_t resolve_stream(objeta_hip_context* ctx, objeta_hip_stream s);
 // Makes sure workspace region `slot` holds at least `bytes` and returns it in *out;
 // fails (Unsupported) if it would have to grow while `stream` is capturing.
 int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, int slot, size_t bytes, void** out);
+// Releases the device memory of every cache still alive on `ctx` (the caches stay
+// valid as accounting-only objects until destroyed).
+void detach_caches(objeta_hip_context* ctx);
 // Pinned host staging of at least `bytes` (grown outside capture only).
 int32_t ensure_host_stage(objeta_hip_context* ctx, size_t bytes, void** out);
 

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/objeta_hip.h"
+
 struct objeta_hip_context;
 
 namespace objeta {
@@ -16,5 +18,16 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
                          const float* d_x, float* d_y, uint64_t rows, uint64_t cols, uint64_t batch);
 
 int32_t launch_zero(hipStream_t s, void* d, uint64_t bytes);
+
+int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                           uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
+                           float* act, uint64_t hidden, uint64_t inter, float limit);
+
+int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                        uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
+                        const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim);
+
+int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
+                        float** out);
 
 }  // namespace objeta

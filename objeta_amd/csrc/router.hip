@@ -26,6 +26,7 @@ constexpr int kRThreads = 256;
 constexpr int kRWaves = kRThreads / 64;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
+constexpr int kChunkBatch = 8;  // 256-element chunks loaded per batch (8 float4 per lane)
 
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
@@ -33,7 +34,7 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     return v;
 }
 
-// Inclusive scan over the wave (Hillis-Steele; exact enough in double).
+// Inclusive scan over the wave (Hillis-Steele, in double).
 __device__ __forceinline__ double wave_scan_d(double v, int lane) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -41,6 +42,81 @@ __device__ __forceinline__ double wave_scan_d(double v, int lane) {
         if (lane >= off) v += o;
     }
     return v;
+}
+
+// The exact sum S of the rounded products fl(row[h] * x[h]) (accumulated in
+// double) and sum_h |S_h| over the sequential prefix sums S_h = sum_{h' <= h},
+// the quantity that bounds the reference's sequential fp32 rounding error.
+// Vector form: the row is read as 256-element chunks, lane l holding elements
+// 4l..4l+3 of each chunk (coalesced float4 loads, 8 chunks in flight); the prefix
+// of an element is (chunks before) + (lanes before, a wave scan) + (its lane's own).
+__device__ __forceinline__ void exact_logit_vec(const float* __restrict__ row, const float* __restrict__ xt,
+                                                uint32_t hidden, uint32_t lane, double& total, double& abs_prefix) {
+    const uint32_t n4 = hidden >> 2;
+    const uint32_t nchunks = (hidden + 255) >> 8;
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    const float4* x4 = reinterpret_cast<const float4*>(xt);
+    double base = 0.0, absacc = 0.0;
+    for (uint32_t c0 = 0; c0 < nchunks; c0 += kChunkBatch) {
+        float4 w[kChunkBatch], v[kChunkBatch];
+#pragma unroll
+        for (int g = 0; g < kChunkBatch; ++g) {
+            const uint32_t i = (c0 + g) * 64 + lane;
+            const uint32_t ic = i < n4 ? i : n4 - 1;
+            w[g] = r4[ic];
+            v[g] = x4[ic];
+        }
+        // the batch's scans are independent: run them side by side
+        double p[kChunkBatch][4], local[kChunkBatch], incl[kChunkBatch];
+#pragma unroll
+        for (int g = 0; g < kChunkBatch; ++g) {
+            const bool ok = (c0 + g) * 64 + lane < n4;
+            p[g][0] = ok ? static_cast<double>(__fmul_rn(w[g].x, v[g].x)) : 0.0;
+            p[g][1] = ok ? static_cast<double>(__fmul_rn(w[g].y, v[g].y)) : 0.0;
+            p[g][2] = ok ? static_cast<double>(__fmul_rn(w[g].z, v[g].z)) : 0.0;
+            p[g][3] = ok ? static_cast<double>(__fmul_rn(w[g].w, v[g].w)) : 0.0;
+            local[g] = ((p[g][0] + p[g][1]) + p[g][2]) + p[g][3];
+            incl[g] = local[g];
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+            for (int g = 0; g < kChunkBatch; ++g) {
+                const double o = __shfl_up(incl[g], off, 64);
+                if (static_cast<int>(lane) >= off) incl[g] += o;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kChunkBatch; ++g) {
+            const bool ok = (c0 + g) * 64 + lane < n4;
+            const double s0 = base + (incl[g] - local[g]) + p[g][0];
+            const double s1 = s0 + p[g][1], s2 = s1 + p[g][2], s3 = s2 + p[g][3];
+            if (ok) absacc += fabs(s0) + fabs(s1) + fabs(s2) + fabs(s3);
+            base += __shfl(incl[g], 63, 64);
+        }
+    }
+    total = base;
+    abs_prefix = wave_sum_d(absacc);
+}
+
+// Scalar form for any hidden and alignment: lane l owns the contiguous range
+// [l*chunk, (l+1)*chunk) of the sequential order.
+__device__ __forceinline__ void exact_logit_scalar(const float* __restrict__ row, const float* __restrict__ xt,
+                                                   uint32_t hidden, uint32_t lane, double& total,
+                                                   double& abs_prefix) {
+    const uint32_t chunk = (hidden + 63) / 64;
+    const uint32_t c0 = lane * chunk < hidden ? lane * chunk : hidden;
+    const uint32_t c1 = c0 + chunk < hidden ? c0 + chunk : hidden;
+    double local = 0.0;
+    for (uint32_t h = c0; h < c1; ++h) local += static_cast<double>(__fmul_rn(row[h], xt[h]));
+    const double incl = wave_scan_d(local, static_cast<int>(lane));
+    double run = incl - local, absacc = 0.0;
+    for (uint32_t h = c0; h < c1; ++h) {
+        run += static_cast<double>(__fmul_rn(row[h], xt[h]));
+        absacc += fabs(run);
+    }
+    total = __shfl(incl, 63, 64);
+    abs_prefix = wave_sum_d(absacc);
 }
 
 // Ranks n values (descending, lower index first on ties) and writes the ids of
@@ -78,6 +154,7 @@ __device__ float block_sum(float v, float* red) {
 }
 
 // grid = (ceil(E / 4), T). Wave w of block b handles expert b*4 + w of token y.
+template <bool VEC>
 __global__ __launch_bounds__(kRThreads) void router_kernel(
     const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
     uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
@@ -90,22 +167,9 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
 
     if (e < n_experts) {
         const float* row = w_r + static_cast<size_t>(e) * hidden;
-        // Lane owns the contiguous chunk [c0, c1) of the sequential order.
-        const uint32_t chunk = (hidden + 63) / 64;
-        const uint32_t c0 = lane * chunk < hidden ? lane * chunk : hidden;
-        const uint32_t c1 = c0 + chunk < hidden ? c0 + chunk : hidden;
-        double local = 0.0;
-        for (uint32_t h = c0; h < c1; ++h) local += static_cast<double>(__fmul_rn(row[h], xt[h]));
-        const double incl = wave_scan_d(local, lane);
-        const double base = incl - local;
-        double abs_prefix = 0.0;
-        double run = base;
-        for (uint32_t h = c0; h < c1; ++h) {
-            run += static_cast<double>(__fmul_rn(row[h], xt[h]));
-            abs_prefix += fabs(run);
-        }
-        abs_prefix = wave_sum_d(abs_prefix);
-        const double total = __shfl(incl, 63, 64);
+        double total, abs_prefix;
+        if constexpr (VEC) exact_logit_vec(row, xt, hidden, lane, total, abs_prefix);
+        else exact_logit_scalar(row, xt, hidden, lane, total, abs_prefix);
         if (lane == 0) {
             const double b = bias ? static_cast<double>(bias[e]) : 0.0;
             const float lhat = static_cast<float>(total + b);
@@ -205,8 +269,7 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
         __syncthreads();
     } else {
         float part = 0.0f;
-        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads)
-            part += static_cast<float>(exp(static_cast<double>(s_val[j] - mx)));
+        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) part += expf(s_val[j] - mx);
         const float tot = block_sum(part, s_red);
         if (threadIdx.x == 0) s_sum_exp = tot;
         __syncthreads();
@@ -218,7 +281,8 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
         float p[kMaxTopK];
         float sel_sum = 0.0f;
         for (uint32_t r = 0; r < k; ++r) {
-            const float ev = static_cast<float>(exp(static_cast<double>(__fsub_rn(s_val[s_sel[r]], mx))));
+            const float ev = s_uncertain ? static_cast<float>(exp(static_cast<double>(__fsub_rn(s_val[s_sel[r]], mx))))
+                                         : expf(__fsub_rn(s_val[s_sel[r]], mx));
             p[r] = __fdiv_rn(ev, sum_exp);
             sel_sum = __fadd_rn(sel_sum, p[r]);
         }
@@ -246,9 +310,15 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
     if (n_tokens > ctx->counter_words) OBJ_FAIL(kInvalidInput, action, strf("n_tokens > %zu", ctx->counter_words));
     if (!w_r || !x || !ids || !weights) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     const dim3 grid(static_cast<uint32_t>((n_experts + kRWaves - 1) / kRWaves), static_cast<uint32_t>(n_tokens));
-    hipLaunchKernelGGL(router_kernel, grid, dim3(kRThreads), 0, s, w_r, bias, x, static_cast<uint32_t>(n_experts),
-                       static_cast<uint32_t>(hidden), static_cast<uint32_t>(k), renormalize, ids, weights, ws_logit,
-                       ws_bound, ctx->counters);
+    const bool vec = hidden % 4 == 0 && reinterpret_cast<uintptr_t>(w_r) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (vec)
+        hipLaunchKernelGGL(router_kernel<true>, grid, dim3(kRThreads), 0, s, w_r, bias, x,
+                           static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden), static_cast<uint32_t>(k),
+                           renormalize, ids, weights, ws_logit, ws_bound, ctx->counters);
+    else
+        hipLaunchKernelGGL(router_kernel<false>, grid, dim3(kRThreads), 0, s, w_r, bias, x,
+                           static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden), static_cast<uint32_t>(k),
+                           renormalize, ids, weights, ws_logit, ws_bound, ctx->counters);
     OBJ_HIP(hipGetLastError(), action);
     return 0;
 }

@@ -243,6 +243,9 @@ int32_t objeta_hip_destroy(objeta_hip_context* ctx) {
     if (!ctx) return 0;
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
+    if (ctx->transient_pool) (void)objeta_hip_cache_destroy(static_cast<objeta_hip_expert_cache*>(ctx->transient_pool));
+    ctx->transient_pool = nullptr;
+    objeta::detach_caches(ctx);
     for (hipStream_t s : ctx->streams) (void)hipStreamDestroy(s);
     if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
     for (auto& w : ctx->ws)
