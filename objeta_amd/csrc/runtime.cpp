@@ -69,6 +69,7 @@ int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, int slot, 
     size_t grow = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
     void* p = nullptr;
     OBJ_HIP(hipMalloc(&p, grow), "allocate workspace");
+    OBJ_HIP(hipMemset(p, 0, grow), "clear workspace");
     if (ws.ptr) ctx->retired_ws.push_back(ws.ptr);
     ws.ptr = p;
     ws.bytes = grow;
