@@ -7,14 +7,17 @@ blocks), router W_r ~N(0, 0.02) with logits biased by ln Zipf(s=1.1) over a
 per-layer rank permutation, hidden ~N(0, 1), batch 1 decode. Each layer computes
     h <- h + sum_j w_j * down_j(silu(gate_j h) * up_j h)
 over the router's softmax -> top-8 -> renormalised selection. Every expert of every
-layer is resident in HBM (16.3 GB); one step is one token through all 48 layers,
-replayed from a hipGraph (router, fused gate/up + SiLU, down + combine per layer).
+layer is resident in HBM (16.3 GB); one step is one token through all 48 layers in
+one launch of the persistent decode-stack kernel (router, top-8, fused gate/up +
+SiLU, down + combine for every layer, handed between workgroups on the device).
+The same stack run as three kernels per layer from a hipGraph is reported beside it.
 
 Reported: MoE layer us/token (stack time / 48), the stack's us/token, achieved HBM
 GB/s on expert-weight bytes (8 experts x 2,654,208 B per layer) and its fraction of
-MI355X's 8 TB/s, a roofline record for the dominant kernel (fused gate/up) timed
-with HIP events on its own stream, and the CPU baseline: the oracle's single-thread
-restatement of the reference CPU path (cpu_router + selected_moe_cpu) on one token.
+MI355X's 8 TB/s, a roofline record for the dominant kernel (the decode-stack
+kernel, one launch per token) timed with HIP events on its stream, and the CPU
+baseline: the oracle's single-thread restatement of the reference CPU path
+(cpu_router + selected_moe_cpu) on a few tokens.
 
 Synthetic data generated on the device with the counter-based generator shared
 with the oracle (no checkpoints).
@@ -121,7 +124,7 @@ def main() -> int:
                                    "(the multi-GPU sharding is described in DESIGN.md)"}))
         return 2
 
-    from objeta_amd import HipBackend, MoeExecutor, check
+    from objeta_amd import HipBackend, MoeExecutor, MoeStack, check
     from objeta_amd._lib import load
 
     H, E, K, I, L = 2048, 128, 8, 768, args.layers
@@ -149,7 +152,35 @@ def main() -> int:
             moe.layer_device(stack.fmt, stack.tables[l], stack.router_w[l], stack.router_b[l], K, 1, src, src,
                              h.addr(), ids.addr(4 * l * K), wts.addr(4 * l * K), H, I, H, stream=stream)
 
-    # size the workspaces outside capture, then capture one graph per pool token
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    check(lib.objeta_hip_event_create(ctx, C.byref(ev0)))
+    check(lib.objeta_hip_event_create(ctx, C.byref(ev1)))
+    ms = C.c_float()
+
+    # ---- headline: the persistent decode-stack kernel, one launch per token ----
+    layers = [(stack.tables[l], stack.router_w[l], stack.router_b[l], ids.addr(4 * l * K), wts.addr(4 * l * K))
+              for l in range(L)]
+    plan = MoeStack(be, stack.fmt, layers, E, K, H, I)
+    for i in range(args.warmup):
+        plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream)
+    be.synchronize(stream)
+    check(lib.objeta_hip_event_record(ctx, ev0, stream))
+    for i in range(args.steps):
+        plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream)
+    check(lib.objeta_hip_event_record(ctx, ev1, stream))
+    check(lib.objeta_hip_event_elapsed_ms(ctx, ev0, ev1, C.byref(ms)))
+    be.synchronize(stream)
+    stack_us = ms.value * 1000.0 / args.steps
+    layer_us = stack_us / L
+    expert_bytes_token = L * K * stack.expert_bytes
+    router_bytes_token = L * (4 * E * H)
+    gbps = expert_bytes_token / (stack_us * 1e-6) / 1e9
+    if moe.device_error() != 0:
+        raise RuntimeError("device error word set during the timed run")
+    kernel_bytes = expert_bytes_token + router_bytes_token + 4 * H * 2
+    kernel_gbps = kernel_bytes / (stack_us * 1e-6) / 1e9
+
+    # ---- the same stack as three kernels per layer, replayed from a hipGraph ----
     enqueue_token(0)
     be.synchronize(stream)
     graphs = []
@@ -159,55 +190,19 @@ def main() -> int:
         g = C.c_void_p()
         check(lib.objeta_hip_graph_end_capture(ctx, stream, C.byref(g)))
         graphs.append(g)
-
-    ev0, ev1 = C.c_void_p(), C.c_void_p()
-    check(lib.objeta_hip_event_create(ctx, C.byref(ev0)))
-    check(lib.objeta_hip_event_create(ctx, C.byref(ev1)))
-    for i in range(args.warmup):
+    gsteps = max(10, args.steps // 4)
+    for i in range(min(args.warmup, 5)):
         check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream))
     be.synchronize(stream)
     check(lib.objeta_hip_event_record(ctx, ev0, stream))
-    for i in range(args.steps):
+    for i in range(gsteps):
         check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream))
     check(lib.objeta_hip_event_record(ctx, ev1, stream))
-    ms = C.c_float()
     check(lib.objeta_hip_event_elapsed_ms(ctx, ev0, ev1, C.byref(ms)))
     be.synchronize(stream)
-    stack_us = ms.value * 1000.0 / args.steps
-    layer_us = stack_us / L
-    expert_bytes_token = L * K * stack.expert_bytes
-    gbps = expert_bytes_token / (stack_us * 1e-6) / 1e9
+    graph_layer_us = ms.value * 1000.0 / gsteps / L
     if moe.device_error() != 0:
-        raise RuntimeError("device error word set during the timed run")
-
-    # ---- dominant kernel: fused gate/up, timed alone on the same stream ----
-    act = be.alloc(4 * K * I + 64)
-    gate_up_iters = max(4, min(args.steps, 50))
-
-    def gate_up(l: int):
-        check(lib.objeta_hip_moe_gate_up_device(ctx, stack.fmt, stream, stack.tables[l].addr(), E,
-                                                ids.addr(4 * l * K), 1, K, h.addr(), act.addr(), H, I,
-                                                C.c_float(0.0)))
-    evs = []
-    for _ in range(2 * L):
-        e = C.c_void_p()
-        check(lib.objeta_hip_event_create(ctx, C.byref(e)))
-        evs.append(e)
-    gate_up(0)
-    be.synchronize(stream)
-    tot = 0.0
-    for it in range(gate_up_iters):
-        for l in range(L):
-            check(lib.objeta_hip_event_record(ctx, evs[2 * l], stream))
-            gate_up(l)
-            check(lib.objeta_hip_event_record(ctx, evs[2 * l + 1], stream))
-        be.synchronize(stream)
-        for l in range(L):
-            check(lib.objeta_hip_event_elapsed_ms(ctx, evs[2 * l], evs[2 * l + 1], C.byref(ms)))
-            tot += ms.value
-    gu_us = tot * 1000.0 / (gate_up_iters * L)
-    gu_bytes = K * 2 * stack.gu_bytes + 4 * H + 4 * K * I
-    gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
+        raise RuntimeError("device error word set during the graph run")
 
     # ---- CPU baseline: oracle restatement, one thread, same layers ----
     cpu = None
@@ -219,7 +214,7 @@ def main() -> int:
         max_rel = 0.0
         for p in range(args.cpu_tokens):
             # GPU result and routing for this token
-            check(lib.objeta_hip_graph_launch(ctx, graphs[p], stream))
+            plan.run(xs.addr(4 * p * H), h.addr(), stream=stream)
             be.synchronize(stream)
             gpu_h = h.download(np.float32, H)
             gpu_ids = ids.download(np.uint32, L * K).reshape(L, K)
@@ -270,14 +265,17 @@ def main() -> int:
         "expert_bytes_per_token": expert_bytes_token,
         "expert_hbm_gbps": round(gbps, 1),
         "expert_hbm_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-        "roofline": {"kernel": "moe_gate_up_kernel (fused gate+up GEMV, SiLU*mul)", "bound": "hbm",
-                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "avg_launch_us": round(gu_us, 3), "algorithmic_bytes_per_launch": gu_bytes},
+        "roofline": {"kernel": "moe_stack_kernel (persistent decode stack, 48 layers per launch)", "bound": "hbm",
+                     "achieved": round(kernel_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "avg_launch_us": round(stack_us, 3), "algorithmic_bytes_per_launch": kernel_bytes},
+        "per_layer_graph_us_per_token_layer": round(graph_layer_us, 3),
+        "stack_grid_workgroups": plan.info()["grid"],
         "cpu_baseline": cpu,
         "device": {"name": dev["name"], "arch": dev["arch"], "compute_units": dev["compute_units"]},
     }
     print(json.dumps(rec), flush=True)
+    plan.close()
     be.close()
     return 0
 

@@ -1,0 +1,437 @@
+// router_math.hpp — the router's arithmetic, shared by the router kernel and the
+// persistent decode-stack kernel.
+//
+// Reference semantics: cpu_router (crates/objeta-cuda/src/bin/
+// deepseek_single_layer_moe.rs:687-743) takes each logit as a sequential fp32 sum
+// of rounded products, a softmax over all experts, and a stable descending sort
+// (ties keep the lower expert id); the k selected probabilities are renormalised
+// (crates/objeta-qwen36-executor/src/moe_dispatch.rs:403-435). The device takes the
+// exact sum S of the same rounded products (in double) with a rigorous bound on
+// |S - sequential fp32 sum| (Higham: u * sum_k |S_k| / (1 - n u) over the
+// sequential prefix sums S_k); decisions closer than the bounds are recomputed in
+// the reference's order by the caller.
+#pragma once
+
+#include "device_common.hpp"
+
+namespace objeta {
+namespace rmath {
+
+constexpr int kPadX = 68;  // floats per 64-activation slot of the padded LDS layout
+
+constexpr int kRThreads = 256;
+constexpr int kRWaves = kRThreads / 64;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopK = 32;
+constexpr int kChunkBatch = 8;  // 256-element chunks loaded per batch (8 float4 per lane)
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Inclusive scan over the wave (Hillis-Steele, in double).
+__device__ __forceinline__ double wave_scan_d(double v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const double o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+// The exact sum S of the rounded products fl(row[h] * x[h]) (accumulated in
+// double) and sum_h |S_h| over the sequential prefix sums S_h = sum_{h' <= h},
+// the quantity that bounds the reference's sequential fp32 rounding error.
+// Vector form: the row is read as 256-element chunks, lane l holding elements
+// 4l..4l+3 of each chunk (coalesced float4 loads, 8 chunks in flight); the prefix
+// of an element is (chunks before) + (lanes before, a wave scan) + (its lane's own).
+__device__ __forceinline__ void exact_logit_vec(const float* __restrict__ row, const float* __restrict__ xt,
+                                                uint32_t hidden, uint32_t lane, double& total, double& abs_prefix) {
+    const uint32_t n4 = hidden >> 2;
+    const uint32_t nchunks = (hidden + 255) >> 8;
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    const float4* x4 = reinterpret_cast<const float4*>(xt);
+    double base = 0.0, absacc = 0.0;
+    for (uint32_t c0 = 0; c0 < nchunks; c0 += kChunkBatch) {
+        float4 w[kChunkBatch], v[kChunkBatch];
+#pragma unroll
+        for (int g = 0; g < kChunkBatch; ++g) {
+            const uint32_t i = (c0 + g) * 64 + lane;
+            const uint32_t ic = i < n4 ? i : n4 - 1;
+            w[g] = r4[ic];
+            v[g] = x4[ic];
+        }
+        // the batch's scans are independent: run them side by side
+        double p[kChunkBatch][4], local[kChunkBatch], incl[kChunkBatch];
+#pragma unroll
+        for (int g = 0; g < kChunkBatch; ++g) {
+            const bool ok = (c0 + g) * 64 + lane < n4;
+            p[g][0] = ok ? static_cast<double>(__fmul_rn(w[g].x, v[g].x)) : 0.0;
+            p[g][1] = ok ? static_cast<double>(__fmul_rn(w[g].y, v[g].y)) : 0.0;
+            p[g][2] = ok ? static_cast<double>(__fmul_rn(w[g].z, v[g].z)) : 0.0;
+            p[g][3] = ok ? static_cast<double>(__fmul_rn(w[g].w, v[g].w)) : 0.0;
+            local[g] = ((p[g][0] + p[g][1]) + p[g][2]) + p[g][3];
+            incl[g] = local[g];
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+            for (int g = 0; g < kChunkBatch; ++g) {
+                const double o = __shfl_up(incl[g], off, 64);
+                if (static_cast<int>(lane) >= off) incl[g] += o;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kChunkBatch; ++g) {
+            const bool ok = (c0 + g) * 64 + lane < n4;
+            const double s0 = base + (incl[g] - local[g]) + p[g][0];
+            const double s1 = s0 + p[g][1], s2 = s1 + p[g][2], s3 = s2 + p[g][3];
+            if (ok) absacc += fabs(s0) + fabs(s1) + fabs(s2) + fabs(s3);
+            base += __shfl(incl[g], 63, 64);
+        }
+    }
+    total = base;
+    abs_prefix = wave_sum_d(absacc);
+}
+
+// Scalar form for any hidden and alignment: lane l owns the contiguous range
+// [l*chunk, (l+1)*chunk) of the sequential order.
+__device__ __forceinline__ void exact_logit_scalar(const float* __restrict__ row, const float* __restrict__ xt,
+                                                   uint32_t hidden, uint32_t lane, double& total,
+                                                   double& abs_prefix) {
+    const uint32_t chunk = (hidden + 63) / 64;
+    const uint32_t c0 = lane * chunk < hidden ? lane * chunk : hidden;
+    const uint32_t c1 = c0 + chunk < hidden ? c0 + chunk : hidden;
+    double local = 0.0;
+    for (uint32_t h = c0; h < c1; ++h) local += static_cast<double>(__fmul_rn(row[h], xt[h]));
+    const double incl = wave_scan_d(local, static_cast<int>(lane));
+    double run = incl - local, absacc = 0.0;
+    for (uint32_t h = c0; h < c1; ++h) {
+        run += static_cast<double>(__fmul_rn(row[h], xt[h]));
+        absacc += fabs(run);
+    }
+    total = __shfl(incl, 63, 64);
+    abs_prefix = wave_sum_d(absacc);
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int w = 1; w < kRWaves; ++w) m = fmaxf(m, red[w]);
+    __syncthreads();
+    return m;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+    for (int w = 1; w < kRWaves; ++w) s += red[w];
+    __syncthreads();
+    return s;
+}
+
+// Order key of (value, index): a larger key means a larger value, or an equal
+// value at a lower index, which is the order of the reference's stable descending
+// sort. -0.0 is folded into +0.0 (they compare equal as floats).
+__device__ __forceinline__ uint64_t order_key(float v, uint32_t index) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v + 0.0f);
+    u ^= (u >> 31) ? 0xFFFFFFFFu : 0x80000000u;
+    return (static_cast<uint64_t>(u) << 32) | (0xFFFFFFFFu - index);
+}
+
+// Rank of every value among n by key (keys padded with 0 to a multiple of 8). The
+// ids of ranks < want go to sel[]. Each value's comparisons are split over up to 8
+// threads (as many as 256 threads allow) whose partial counts meet in part[].
+__device__ __forceinline__ void rank_select(const uint64_t* keys, int n, int want, int* rank, int* sel, int* part) {
+    const int n8 = (n + 7) >> 3;
+    int parts = 1;
+    while (parts < 8 && parts * 2 * n <= kRThreads) parts *= 2;
+    const int per = (n8 + parts - 1) / parts;  // 8-key groups per part
+    for (int w = threadIdx.x; w < n * parts; w += kRThreads) {
+        const int e = w % n, p = w / n;
+        const uint64_t me = keys[e];
+        int r = 0;
+        const int g1 = (p + 1) * per < n8 ? (p + 1) * per : n8;
+        for (int g = p * per; g < g1; ++g) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r += keys[8 * g + i] > me;
+        }
+        if (parts == 1) {
+            rank[e] = r;
+            if (r < want) sel[r] = e;
+        } else {
+            part[p * n + e] = r;
+        }
+    }
+    if (parts > 1) {
+        __syncthreads();
+        for (int e = threadIdx.x; e < n; e += kRThreads) {
+            int r = 0;
+            for (int p = 0; p < parts; ++p) r += part[p * n + e];
+            rank[e] = r;
+            if (r < want) sel[r] = e;
+        }
+    }
+}
+
+// A 64-bit word {value bits, epoch}: one atomic store publishes both, so a reader
+// that sees the current epoch also sees the value written with it.
+__device__ __forceinline__ uint64_t tag(float v, uint32_t epoch) {
+    return (static_cast<uint64_t>(epoch) << 32) | __builtin_bit_cast(uint32_t, v);
+}
+
+constexpr uint32_t kSpinLimit = 1u << 20;  // bounded waits (about a second), then the error word
+
+// grid = (ceil(E / 4), T). Wave w of block b handles expert b*4 + w of token y and
+// publishes {logit, epoch} and {bound, epoch}. Workgroup 0 of each token then
+// waits for all experts' words of the current epoch (counters[t] + 1), selects, and
+// advances counters[t]. No fences: the words are read and written with agent-scope
+// atomics, and the epoch in each word makes stale words detectable.
+
+// ------------------------------------------------------------ logits and bounds
+// Rounds the exact sum to the logit the device reports and bounds its distance to
+// the reference's sequential fp32 logit (+ bias), for one expert.
+__device__ __forceinline__ void finish_logit(double total, double abs_prefix, const float* bias, uint32_t e,
+                                             uint32_t hidden, float& lhat, float& bnd) {
+    const double b = bias ? static_cast<double>(bias[e]) : 0.0;
+    lhat = static_cast<float>(total + b);
+    const double u = 5.9604644775390625e-08;  // 2^-24
+    const double n = static_cast<double>(hidden);
+    double bound = u * abs_prefix / (1.0 - n * u);
+    bound += u * (fabs(total + b) + fabs(static_cast<double>(lhat))) * 1.0001;
+    bound += 1e-12 * abs_prefix + 1e-30;
+    bnd = static_cast<float>(bound * 1.0001);
+}
+
+// exact_logit_vec for a row whose 256-element chunks are already in registers
+// (w[c] = elements 256c + 4 lane .. +3) and an activation vector staged in LDS in
+// the padded pair layout (68 floats per 64). nchunks <= NB.
+template <int NB>
+__device__ __forceinline__ void exact_logit_regs(const float4 (&w)[NB], const float* __restrict__ x_lds,
+                                                 uint32_t hidden, uint32_t lane, double& total, double& abs_prefix) {
+    const uint32_t n4 = hidden >> 2;
+    const uint32_t nchunks = (hidden + 255) >> 8;
+    double p[NB][4], local[NB], incl[NB];
+#pragma unroll
+    for (int g = 0; g < NB; ++g) {
+        const bool ok = static_cast<uint32_t>(g) < nchunks && g * 64 + lane < n4;
+        const uint32_t idx = static_cast<uint32_t>(g) * 256 + 4 * lane;
+        const float4 v = ok ? *reinterpret_cast<const float4*>(x_lds + (idx >> 6) * kPadX + (idx & 63))
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        p[g][0] = ok ? static_cast<double>(__fmul_rn(w[g].x, v.x)) : 0.0;
+        p[g][1] = ok ? static_cast<double>(__fmul_rn(w[g].y, v.y)) : 0.0;
+        p[g][2] = ok ? static_cast<double>(__fmul_rn(w[g].z, v.z)) : 0.0;
+        p[g][3] = ok ? static_cast<double>(__fmul_rn(w[g].w, v.w)) : 0.0;
+        local[g] = ((p[g][0] + p[g][1]) + p[g][2]) + p[g][3];
+        incl[g] = local[g];
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < NB; ++g) {
+            const double o = __shfl_up(incl[g], off, 64);
+            if (static_cast<int>(lane) >= off) incl[g] += o;
+        }
+    }
+    double base = 0.0, absacc = 0.0;
+#pragma unroll
+    for (int g = 0; g < NB; ++g) {
+        const bool ok = static_cast<uint32_t>(g) < nchunks && g * 64 + lane < n4;
+        const double s0 = base + (incl[g] - local[g]) + p[g][0];
+        const double s1 = s0 + p[g][1], s2 = s1 + p[g][2], s3 = s2 + p[g][3];
+        if (ok) absacc += fabs(s0) + fabs(s1) + fabs(s2) + fabs(s3);
+        base += __shfl(incl[g], 63, 64);
+    }
+    total = base;
+    abs_prefix = wave_sum_d(absacc);
+}
+
+
+// exact_logit_regs with the products recomputed in the second pass instead of
+// kept: two arrays of NB doubles live instead of six, for kernels that hold other
+// state in registers.
+template <int NB>
+__device__ __forceinline__ void exact_logit_regs_lean(const float4 (&w)[NB], const float* __restrict__ x_lds,
+                                                      uint32_t hidden, uint32_t lane, double& total,
+                                                      double& abs_prefix) {
+    const uint32_t n4 = hidden >> 2;
+    const uint32_t nchunks = (hidden + 255) >> 8;
+    double local[NB], incl[NB];
+    auto xat = [&](int g) {
+        const uint32_t idx = static_cast<uint32_t>(g) * 256 + 4 * lane;
+        return *reinterpret_cast<const float4*>(x_lds + (idx >> 6) * kPadX + (idx & 63));
+    };
+#pragma unroll
+    for (int g = 0; g < NB; ++g) {
+        const bool ok = static_cast<uint32_t>(g) < nchunks && g * 64 + lane < n4;
+        double l = 0.0;
+        if (ok) {
+            const float4 v = xat(g);
+            l = ((static_cast<double>(__fmul_rn(w[g].x, v.x)) + static_cast<double>(__fmul_rn(w[g].y, v.y))) +
+                 static_cast<double>(__fmul_rn(w[g].z, v.z))) +
+                static_cast<double>(__fmul_rn(w[g].w, v.w));
+        }
+        local[g] = l;
+        incl[g] = l;
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < NB; ++g) {
+            const double o = __shfl_up(incl[g], off, 64);
+            if (static_cast<int>(lane) >= off) incl[g] += o;
+        }
+    }
+    double base = 0.0, absacc = 0.0;
+#pragma unroll
+    for (int g = 0; g < NB; ++g) {
+        const bool ok = static_cast<uint32_t>(g) < nchunks && g * 64 + lane < n4;
+        if (ok) {
+            const float4 v = xat(g);
+            const double s0 = base + (incl[g] - local[g]) + static_cast<double>(__fmul_rn(w[g].x, v.x));
+            const double s1 = s0 + static_cast<double>(__fmul_rn(w[g].y, v.y));
+            const double s2 = s1 + static_cast<double>(__fmul_rn(w[g].z, v.z));
+            const double s3 = s2 + static_cast<double>(__fmul_rn(w[g].w, v.w));
+            absacc += fabs(s0) + fabs(s1) + fabs(s2) + fabs(s3);
+        }
+        base += __shfl(incl[g], 63, 64);
+    }
+    total = base;
+    abs_prefix = wave_sum_d(absacc);
+}
+
+// -------------------------------------------------------------------- selection
+template <int MAXE>
+struct SelectLds {
+    float val[MAXE];
+    float bnd[MAXE];
+    int rank[MAXE];
+    int part[kRThreads];
+    __align__(16) uint64_t key[MAXE + 8];
+    int sel[kMaxTopK + 1];
+    float red[kRWaves];
+    float e[kMaxTopK];
+    int flag;
+};
+
+// With s.val / s.bnd holding all n logits and bounds (visible to the block):
+// ranks the experts and checks that every decision the top-k depends on is
+// separated beyond the bounds plus a margin that keeps the softmax probabilities
+// distinct after rounding. When certain (returns true), s.sel[0..k) holds the ids
+// and s.e[0..k) exp(l - max) (renormalize) or the probabilities. Block-wide; 256
+// threads.
+template <int MAXE>
+__device__ bool select_certain(SelectLds<MAXE>& s, uint32_t n, uint32_t k, int renormalize) {
+    if (threadIdx.x == 0) s.flag = 0;
+    for (uint32_t j = threadIdx.x; j < ((n + 7) & ~7u); j += kRThreads) s.key[j] = j < n ? order_key(s.val[j], j) : 0ull;
+    __syncthreads();
+    const uint32_t want = k + 1 <= n ? k + 1 : n;
+    rank_select(s.key, static_cast<int>(n), static_cast<int>(want), s.rank, s.sel, s.part);
+    __syncthreads();
+    const float mx = s.val[s.sel[0]];
+    {
+        const float lk = s.val[s.sel[k - 1]];
+        const float kmin_lo = lk - s.bnd[s.sel[k - 1]];
+        int unsure = 0;
+        for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
+            if (s.rank[j] >= static_cast<int>(k)) {
+                const float margin = 9.5367431640625e-07f * (1.0f + fabsf(s.val[j] - mx) + fabsf(lk - mx));
+                if (!(s.val[j] + s.bnd[j] + margin < kmin_lo)) unsure = 1;
+            }
+        }
+        if (threadIdx.x + 1 < k) {
+            const int a = s.sel[threadIdx.x], b = s.sel[threadIdx.x + 1];
+            const float margin = 9.5367431640625e-07f * (1.0f + fabsf(s.val[a] - mx) + fabsf(s.val[b] - mx));
+            if (!(s.val[a] - s.bnd[a] > s.val[b] + s.bnd[b] + margin)) unsure = 1;
+        }
+        // The margins assume normal probabilities: once exp(l_k - max) / sum can be
+        // subnormal or zero, distinct logits can give equal probabilities, which the
+        // reference's stable sort orders by index.
+        if (threadIdx.x == 0 && !(lk - s.bnd[s.sel[k - 1]] - mx > -80.0f)) unsure = 1;
+        if (unsure) s.flag = 1;
+    }
+    __syncthreads();
+    if (s.flag) return false;
+    float z = 1.0f;
+    if (!renormalize) {
+        float part = 0.0f;
+        for (uint32_t j = threadIdx.x; j < n; j += kRThreads) part += expf(s.val[j] - mx);
+        z = block_sum(part, s.red);
+    }
+    if (threadIdx.x < k) {
+        const float ev = expf(__fsub_rn(s.val[s.sel[threadIdx.x]], mx));
+        s.e[threadIdx.x] = renormalize ? ev : __fdiv_rn(ev, z);
+    }
+    __syncthreads();
+    return true;
+}
+
+// The reference's order throughout (cpu_router): logits[e] = sum_h fl(W[e,h] * x[h])
+// accumulated left to right in fp32 (+ bias); probs = exp(l - max) / sum with the
+// sum taken in expert order; stable descending sort of the probs. exp is evaluated
+// in double and rounded once, which agrees with glibc's expf on all but ~0.03% of
+// arguments (only a probability tie could expose that). Fills s.sel and s.e (the
+// probabilities). xat(h) returns x[h]. Block-wide; 256 threads.
+template <int MAXE, class XAt>
+__device__ void select_sequential(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
+                                  XAt xat, uint32_t n, uint32_t hidden, uint32_t k) {
+    __shared__ float s_sum_exp;
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
+        // every product and every add rounds on its own, as in the reference
+#pragma clang fp contract(off)
+        const float* row = w_r + static_cast<size_t>(j) * hidden;
+        float sacc = 0.0f;
+        for (uint32_t h = 0; h < hidden; ++h) {
+            const float p = row[h] * xat(h);
+            sacc = sacc + p;
+        }
+        if (bias) sacc = sacc + bias[j];
+        s.val[j] = sacc;
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) mx = fmaxf(mx, s.val[j]);
+    mx = block_max(mx, s.red);
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads)
+        s.bnd[j] = static_cast<float>(exp(static_cast<double>(__fsub_rn(s.val[j], mx))));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < n; ++j) sum = __fadd_rn(sum, s.bnd[j]);
+        s_sum_exp = sum;
+    }
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) s.bnd[j] = __fdiv_rn(s.bnd[j], s_sum_exp);
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < ((n + 7) & ~7u); j += kRThreads) s.key[j] = j < n ? order_key(s.bnd[j], j) : 0ull;
+    __syncthreads();
+    const uint32_t want = k + 1 <= n ? k + 1 : n;
+    rank_select(s.key, static_cast<int>(n), static_cast<int>(want), s.rank, s.sel, s.part);
+    __syncthreads();
+    if (threadIdx.x < k) s.e[threadIdx.x] = s.bnd[s.sel[threadIdx.x]];
+    __syncthreads();
+}
+
+// The k selected weights in selection order: renormalised (p / sum of the selected
+// p, summed in selection order) or as they are. Threads 0..63 write.
+template <int MAXE>
+__device__ __forceinline__ void write_selection(const SelectLds<MAXE>& s, uint32_t k, int renormalize,
+                                                uint32_t* __restrict__ ids, float* __restrict__ weights) {
+    if (threadIdx.x < 64) {
+        float sel_sum = 0.0f;
+        for (uint32_t r = 0; r < k; ++r) sel_sum = __fadd_rn(sel_sum, s.e[r]);
+        for (uint32_t r = threadIdx.x; r < k; r += 64) {
+            ids[r] = static_cast<uint32_t>(s.sel[r]);
+            weights[r] = renormalize ? __fdiv_rn(s.e[r], sel_sum) : s.e[r];
+        }
+    }
+}
+
+}  // namespace rmath
+}  // namespace objeta

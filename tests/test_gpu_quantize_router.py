@@ -126,3 +126,21 @@ def test_router_validation(backend):
     with pytest.raises(HipError) as e:
         _router(backend, np.zeros(8 * 64, np.float32), np.zeros(64, np.float32), None, 8, 64, 9, 1)
     assert e.value.kind == "InvalidInput" and "top_k" in e.value.source_message
+
+
+def test_router_underflowing_probabilities_order_by_index(backend):
+    """Logits spread by hundreds: most softmax probabilities are exactly zero and the
+    reference's stable sort orders those experts by index, not by logit."""
+    ne, hidden, k = 64, 256, 8
+    w = orc.gauss(ne * hidden, 21, 0.02).reshape(ne, hidden).copy()
+    w *= np.float32(150.0)
+    tokens = 6
+    x = orc.gauss(tokens * hidden, 22, 3.0)
+    ids, ws = _router(backend, w.ravel(), x, None, ne, hidden, k, tokens)
+    zero_tail = 0
+    for t in range(tokens):
+        rid, rw, _, probs = orc.router(w.ravel(), x[t * hidden:(t + 1) * hidden], ne, hidden, k)
+        zero_tail += int(np.sum(probs[rid] == 0.0))
+        assert list(ids[t]) == list(rid), f"token {t}"
+        assert np.allclose(ws[t], rw, rtol=2e-5, atol=1e-6)
+    assert zero_tail > 0  # the index-ordered zero-probability case is exercised
