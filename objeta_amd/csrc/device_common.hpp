@@ -36,23 +36,35 @@ __device__ __forceinline__ uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t by
     return __builtin_amdgcn_alignbyte(hi, lo, bytes);
 }
 
+// A pointer to device memory as a global-address-space pointer. Weight pointers
+// read from a device table are otherwise generic, and generic (flat) loads are
+// also counted by the LDS counter: every LDS wait would then wait for all weight
+// loads in flight, which serialises prefetching with LDS work.
+template <class T>
+using gptr = const __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ gptr<T> as_global(const T* p) {
+    return (gptr<T>)(p);
+}
+
 // Loads N dwords starting at a 4-byte aligned address. Weight bytes are read
 // exactly once per launch, so the loads are non-temporal (they bypass cache
 // retention and leave L2/MALL to the activations).
 template <int N>
 __device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint32_t (&d)[N]) {
+    const gptr<uint32_t> g = as_global(p);
     int i = 0;
 #pragma unroll
     for (; i + 4 <= N; i += 4) {
-        u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + i));
+        u32x4 v = __builtin_nontemporal_load((gptr<u32x4>)(g + i));
         d[i] = v.x; d[i + 1] = v.y; d[i + 2] = v.z; d[i + 3] = v.w;
     }
     if constexpr (N % 4 >= 2) {
-        u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p + i));
+        u32x2 v = __builtin_nontemporal_load((gptr<u32x2>)(g + i));
         d[i] = v.x; d[i + 1] = v.y;
         i += 2;
     }
-    if constexpr (N % 2 == 1) d[i] = __builtin_nontemporal_load(p + i);
+    if constexpr (N % 2 == 1) d[i] = __builtin_nontemporal_load(g + i);
 }
 
 // ---------------------------------------------------------------- Q4_0
@@ -197,9 +209,12 @@ __device__ __forceinline__ void block_dot_reference_form(const uint32_t (&n)[4],
 // Dot product of a pair of consecutive blocks (64 weights, 4-byte aligned pair
 // start `pair`, already loaded into d) with NT activation vectors xs[t][0..63]
 // (LDS or global), adding to acc.
+// xs_slow: the same activations for the reference-form path (indexed at run time,
+// so it must be addressable memory even when xs points at registers).
 template <int F, int NT>
 __device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw],
-                                         const float* const (&xs)[NT], float (&acc)[NT]) {
+                                         const float* const (&xs)[NT], float (&acc)[NT],
+                                         const float* const (&xs_slow)[NT]) {
     {
         const float s0 = f16_to_f32(d[0] & 0xFFFFu);
         const float s1 = F == kQ4 ? f16_to_f32(d[4] >> 16)
@@ -217,8 +232,8 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw],
                 n1[0] = d[4]; n1[1] = d[5]; n1[2] = d[6];
                 n0[3] = n1[3] = 0;
             }
-            block_dot_reference_form<F, NT>(n0, m0, s0, xs, 0, acc);
-            block_dot_reference_form<F, NT>(n1, m1, s1, xs, 32, acc);
+            block_dot_reference_form<F, NT>(n0, m0, s0, xs_slow, 0, acc);
+            block_dot_reference_form<F, NT>(n1, m1, s1, xs_slow, 32, acc);
             return;
         }
     }
@@ -291,6 +306,12 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw],
             for (int t = 0; t < NT; ++t) acc[t] = __builtin_fmaf(s, a[t], acc[t]);
         }
     }
+}
+
+template <int F, int NT>
+__device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw],
+                                         const float* const (&xs)[NT], float (&acc)[NT]) {
+    pair_dot<F, NT>(d, xs, acc, xs);
 }
 
 // ------------------------------------------------------------- FP4 E2M1

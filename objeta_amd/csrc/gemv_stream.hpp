@@ -38,6 +38,11 @@ struct QRows {
                                         float (&acc)[NT]) const {
         pair_dot<F, NT>(d, xs, acc);
     }
+    template <int NT>
+    __device__ __forceinline__ void dot(const uint32_t (&d)[kDw], const float* const (&xs)[NT],
+                                        float (&acc)[NT], const float* const (&xs_slow)[NT]) const {
+        pair_dot<F, NT>(d, xs, acc, xs_slow);
+    }
 };
 
 // Rows of a DeepSeek split FP4 matrix: nibbles [rows][cols/2], E8M0 [rows][cols/32].
@@ -52,11 +57,16 @@ struct Fp4Rows {
         load_dwords<8>(reinterpret_cast<const uint32_t*>(w + static_cast<size_t>(r) * wrow + p * 32u), n);
 #pragma unroll
         for (int i = 0; i < 8; ++i) d[i] = n[i];
-        d[8] = *reinterpret_cast<const uint16_t*>(s + static_cast<size_t>(r) * srow + p * 2u);
+        d[8] = *as_global(reinterpret_cast<const uint16_t*>(s + static_cast<size_t>(r) * srow + p * 2u));
     }
     template <int NT>
     __device__ __forceinline__ void dot(const uint32_t (&d)[kDw], const float* const (&xs)[NT],
                                         float (&acc)[NT]) const {
+        dot<NT>(d, xs, acc, xs);
+    }
+    template <int NT>
+    __device__ __forceinline__ void dot(const uint32_t (&d)[kDw], const float* const (&xs)[NT],
+                                        float (&acc)[NT], const float* const (&xs_slow)[NT]) const {
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
             const float scale = e8m0_to_f32((d[8] >> (8 * blk)) & 0xFFu);
@@ -82,7 +92,7 @@ struct Fp4Rows {
                     const uint32_t c = (d[blk * 4 + i / 8] >> (4 * (i & 7))) & 15u;
                     const float wv = f16_to_f32(((c & 7u) << 9) | ((c & 8u) << 12)) * 16384.0f * scale;
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) acc[t] = __builtin_fmaf(wv, xs[t][blk * 32 + i], acc[t]);
+                    for (int t = 0; t < NT; ++t) acc[t] = __builtin_fmaf(wv, xs_slow[t][blk * 32 + i], acc[t]);
                 }
             }
         }

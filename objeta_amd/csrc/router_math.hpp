@@ -306,6 +306,53 @@ __device__ __forceinline__ void exact_logit_regs_lean(const float4 (&w)[NB], con
     abs_prefix = wave_sum_d(absacc);
 }
 
+// The exact sum and a bound on sum_h |S_h| for a row held lane-contiguously: lane
+// l owns elements [l*4*n4, (l+1)*4*n4) as w[0..n4) (float4s) against x staged in
+// LDS in the padded pair layout (4*n4 divides 64). The lane's range is cut into 4
+// sub-blocks of NB/4 float4s, each running its own prefix sums s_i and sum |s_i|
+// (four independent dependency chains); one wave scan gives every sub-block's
+// offset T, and sum_i |T + s_i| <= n_b |T| + sum_i |s_i| bounds its share of
+// sum_h |S_h|. The bound is at most twice the exact one and needs no scans per
+// element.
+template <int NB>
+__device__ __forceinline__ void exact_logit_lanes(const float4 (&w)[NB], const float* __restrict__ x_lds,
+                                                  uint32_t n4, uint32_t lane, double& total, double& abs_bound) {
+    static_assert(NB % 4 == 0, "four sub-blocks per lane");
+    constexpr int kSub = NB / 4;  // float4 per sub-block
+    double s[4] = {0.0, 0.0, 0.0, 0.0}, a[4] = {0.0, 0.0, 0.0, 0.0};
+    const uint32_t base = lane * n4 * 4;
+#pragma unroll
+    for (int g = 0; g < NB; ++g) {
+        const int sb = g / kSub;
+        if (static_cast<uint32_t>(g) < n4) {
+            const uint32_t h = base + 4u * static_cast<uint32_t>(g);
+            const float4 v = *reinterpret_cast<const float4*>(x_lds + (h >> 6) * kPadX + (h & 63));
+            s[sb] += static_cast<double>(__fmul_rn(w[g].x, v.x));
+            a[sb] += fabs(s[sb]);
+            s[sb] += static_cast<double>(__fmul_rn(w[g].y, v.y));
+            a[sb] += fabs(s[sb]);
+            s[sb] += static_cast<double>(__fmul_rn(w[g].z, v.z));
+            a[sb] += fabs(s[sb]);
+            s[sb] += static_cast<double>(__fmul_rn(w[g].w, v.w));
+            a[sb] += fabs(s[sb]);
+        }
+    }
+    const double lane_sum = ((s[0] + s[1]) + s[2]) + s[3];
+    const double incl = wave_scan_d(lane_sum, static_cast<int>(lane));
+    double t = __shfl_up(incl, 1, 64);
+    if (lane == 0) t = 0.0;
+    double b = 0.0;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+        const int lo = sb * kSub;
+        const int cnt = static_cast<int>(n4) - lo < 0 ? 0 : (static_cast<int>(n4) - lo > kSub ? kSub : static_cast<int>(n4) - lo);
+        b += static_cast<double>(4 * cnt) * fabs(t) + a[sb];
+        t += s[sb];
+    }
+    total = __shfl(incl, 63, 64);
+    abs_bound = wave_sum_d(b);
+}
+
 // -------------------------------------------------------------------- selection
 template <int MAXE>
 struct SelectLds {
@@ -426,9 +473,13 @@ __device__ __forceinline__ void write_selection(const SelectLds<MAXE>& s, uint32
     if (threadIdx.x < 64) {
         float sel_sum = 0.0f;
         for (uint32_t r = 0; r < k; ++r) sel_sum = __fadd_rn(sel_sum, s.e[r]);
+        // global (not generic) stores: a generic store could alias LDS, and every
+        // later LDS read would then wait for it to complete
+        auto* gi = (__attribute__((address_space(1))) uint32_t*)(ids);
+        auto* gw = (__attribute__((address_space(1))) float*)(weights);
         for (uint32_t r = threadIdx.x; r < k; r += 64) {
-            ids[r] = static_cast<uint32_t>(s.sel[r]);
-            weights[r] = renormalize ? __fdiv_rn(s.e[r], sel_sum) : s.e[r];
+            gi[r] = static_cast<uint32_t>(s.sel[r]);
+            gw[r] = renormalize ? __fdiv_rn(s.e[r], sel_sum) : s.e[r];
         }
     }
 }

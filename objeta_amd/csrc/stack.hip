@@ -43,10 +43,10 @@ using namespace dev;
 using namespace rmath;
 
 constexpr int kSMaxE = 256;      // experts per layer
-constexpr int kSMaxK = 8;        // selection slots (two per wave in the down phase)
-constexpr uint32_t kSMaxH = 2048;  // router rows held in registers: 8 chunks of 256
-constexpr int kRouterNB = 8;
-constexpr int kJW = 2;           // down: selection slots per wave
+constexpr int kSMaxK = 8;        // selection slots
+constexpr uint32_t kSMaxH = 2048;  // router rows held in registers: H/64 floats per lane
+constexpr int kRouterNB = 8;     // float4 per lane of a router row
+constexpr int kTabWords = 6;     // expert-table words per thread (kSMaxE * 6 / 256)
 constexpr uint32_t kWaitLimit = 1u << 18;  // polls per gather (a fraction of a second)
 
 struct StackLayerDev {
@@ -57,6 +57,11 @@ struct StackLayerDev {
     float* weights_out;
 };
 
+// Work split of the GEMV workgroups (all of them run the same code):
+//   gate/up  wave w owns rw = gs_h * UG consecutive rows of the flattened
+//            (slot, row) space, lpr_h = H/64 lanes per row (one pair per lane);
+//   down     workgroup b owns output rows [b*rd, (b+1)*rd) for every slot; its
+//            4 * gs_i (row, slot) combinations take lpr_i = I/(64*CHI) lanes each.
 struct StackParams {
     const StackLayerDev* layers;
     uint32_t L, E, K, H, I;
@@ -70,9 +75,9 @@ struct StackParams {
     uint64_t* sbuf;  // [L][2K]  selection of the sequential path
     uint32_t epoch0;
     uint32_t* err;
-    uint32_t lpr_h, lpr_i;  // lanes per row of H-wide and I-wide rows
-    uint32_t n_gu_chunks;   // (K*I) / (gs_h * UG)
-    uint32_t n_dn_blocks;   // ceil(H / (gs_i * UD))
+    uint32_t n_router;    // router workgroups (first in the grid)
+    uint32_t lpr_h, rw, n_gu_waves;
+    uint32_t lpr_i, rd;
 };
 
 __device__ __forceinline__ uint64_t load_word(const uint64_t* p) {
@@ -97,52 +102,71 @@ __device__ void wait_sample(const uint64_t* __restrict__ p, uint32_t n, uint32_t
             if (!done) done = static_cast<uint32_t>(load_word(p + ic) >> 32) == epoch;
             if (__all(done)) break;
             if (spin == 1 && (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4u)) break;
-            if (spin < 8) __builtin_amdgcn_s_sleep(2);
-            else __builtin_amdgcn_s_sleep(8);
+            if (spin < 16) __builtin_amdgcn_s_sleep(1);
+            else __builtin_amdgcn_s_sleep(4);
         }
     }
     __syncthreads();
 }
 
 // Block-wide gather of n words that must carry `epoch`; sink(i, value) is called
-// once per word when it is seen current. Threads remember which of their (at most
-// 32) positions are still pending, so later rounds re-read only those.
-template <class Sink>
+// once per word when it is seen current. Each thread issues its loads in batches of
+// kGatherBatch before it waits for any of them (one memory latency per batch, not
+// per word), and remembers which of its words are still pending so that later
+// rounds re-check only those. Segments of 32 words per thread keep the pending set
+// in one 32-bit mask.
+//
+// SHARED: the first round uses ordinary (L2-cached) loads. Hundreds of workgroups
+// gather the same vector, and the 32 CUs of an XCD then share one L2 copy instead
+// of each fetching every word across the fabric. A line cached before its
+// producer wrote it shows an older epoch; those words are re-read with agent-scope
+// loads, which bypass the caches.
+constexpr int kGatherBatch = 16;
+template <bool SHARED, class Sink>
 __device__ void gather(const uint64_t* __restrict__ p, uint32_t n, uint32_t epoch, uint32_t* err, int* s_flag,
                        Sink sink) {
     wait_sample(p, n, epoch, err);
-    const uint32_t per = (n + kThreads - 1) / kThreads;
-    uint32_t mask = per >= 32 ? 0xFFFFFFFFu : ((1u << per) - 1u);
-    for (uint32_t spin = 0;; ++spin) {
-        // after one timed-out wait every later wait gives up at once, so the grid drains
-        if (spin == 1 && (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4u)) return;
-        uint32_t m = mask;
-        while (m) {
-            const uint32_t q = __builtin_ctz(m);
-            m &= m - 1;
-            const uint32_t i = threadIdx.x + q * kThreads;
-            if (i >= n) {
-                mask &= ~(1u << q);
-                continue;
+    constexpr uint32_t kSeg = 32u * kThreads;
+    for (uint32_t s0 = 0; s0 < n; s0 += kSeg) {
+        const uint32_t ns = n - s0 < kSeg ? n - s0 : kSeg;
+        const uint32_t per = (ns + kThreads - 1) / kThreads;  // <= 32
+        uint32_t mask = 0;
+        for (uint32_t q = 0; q < per; ++q)
+            if (threadIdx.x + q * kThreads < ns) mask |= 1u << q;
+        for (uint32_t spin = 0;; ++spin) {
+            // after one timed-out wait every later wait gives up at once, so the grid drains
+            if (spin == 1 && (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4u)) return;
+            for (uint32_t q0 = 0; q0 < per; q0 += kGatherBatch) {
+                if (((mask >> q0) & ((1u << kGatherBatch) - 1u)) == 0) continue;
+                uint64_t w[kGatherBatch];
+#pragma unroll
+                for (int j = 0; j < kGatherBatch; ++j) {
+                    const uint32_t i = threadIdx.x + (q0 + static_cast<uint32_t>(j)) * kThreads;
+                    const uint64_t* wp = p + s0 + (i < ns ? i : ns - 1);
+                    w[j] = (SHARED && spin == 0) ? *as_global(wp) : load_word(wp);
+                }
+#pragma unroll
+                for (int j = 0; j < kGatherBatch; ++j) {
+                    const uint32_t q = q0 + static_cast<uint32_t>(j);
+                    if (q < 32 && ((mask >> q) & 1u) && static_cast<uint32_t>(w[j] >> 32) == epoch) {
+                        sink(s0 + threadIdx.x + q * kThreads, word_value(w[j]));
+                        mask &= ~(1u << q);
+                    }
+                }
             }
-            const uint64_t w = load_word(p + i);
-            if (static_cast<uint32_t>(w >> 32) == epoch) {
-                sink(i, word_value(w));
-                mask &= ~(1u << q);
+            if (threadIdx.x == 0) *s_flag = 0;
+            __syncthreads();
+            if (mask) *s_flag = 1;
+            __syncthreads();
+            const int pending = *s_flag;
+            __syncthreads();
+            if (!pending) break;
+            if (spin >= kWaitLimit) {
+                if (threadIdx.x == 0) atomicOr(err, 4u);
+                return;
             }
+            __builtin_amdgcn_s_sleep(8);
         }
-        if (threadIdx.x == 0) *s_flag = 0;
-        __syncthreads();
-        if (mask) *s_flag = 1;
-        __syncthreads();
-        const int pending = *s_flag;
-        __syncthreads();
-        if (!pending) return;
-        if (spin >= kWaitLimit) {
-            if (threadIdx.x == 0) atomicOr(err, 4u);
-            return;
-        }
-        __builtin_amdgcn_s_sleep(8);
     }
 }
 
@@ -176,43 +200,52 @@ struct StackLds {
     int uncertain;
 };
 
-// Router workgroups (the first ceil(E/4)): wave gw owns expert gw. It keeps its
-// router row in registers, loaded one layer ahead, and per layer waits for h_l,
-// publishes {logit}, {bound} and loads the next layer's row.
+// h_l into LDS: layer 0 copies the caller's x, later layers gather the h words
+// the previous layer published.
+__device__ __forceinline__ void load_h(const StackParams& a, StackLds& S, float* xs, uint32_t l, uint32_t epoch) {
+    const uint32_t H = a.H;
+    if (l == 0) {
+        for (uint32_t i = threadIdx.x; i < (H >> 2); i += kThreads) {
+            const uint32_t c = i << 2;
+            *reinterpret_cast<float4*>(xs + (c >> 6) * kPad + (c & 63)) = reinterpret_cast<const float4*>(a.x_in)[i];
+        }
+        __syncthreads();
+    } else {
+        gather<true>(a.hbuf + static_cast<size_t>(l - 1) * H, H, epoch - 1, a.err, &S.flag,
+               [&](uint32_t i, float v) { xs[(i >> 6) * kPad + (i & 63)] = v; });
+    }
+}
+
+// Router workgroups (the first n_router): wave gw owns expert gw. Its router row
+// sits in registers lane-contiguously (lane l: elements [l*H/64, (l+1)*H/64)),
+// loaded one layer ahead; per layer it waits for h_l and publishes {logit},
+// {bound}.
 __device__ void router_role(const StackParams& a, StackLds& S, float* xs) {
     const uint32_t H = a.H, E = a.E;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const bool active = gw < E;
+    const uint32_t n4 = H >> 8;  // float4 per lane
     float4 wr[kRouterNB];
     auto load_router = [&](uint32_t l) {
-        const float4* r4 = reinterpret_cast<const float4*>(a.layers[l].w_r + static_cast<size_t>(gw) * H);
-        const uint32_t n4 = H >> 2;
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const gptr<f32x4> r4 = as_global(reinterpret_cast<const f32x4*>(a.layers[l].w_r + static_cast<size_t>(gw) * H));
 #pragma unroll
         for (int g = 0; g < kRouterNB; ++g) {
-            const uint32_t i = g * 64 + lane;
-            wr[g] = r4[i < n4 ? i : n4 - 1];
+            const f32x4 v = r4[lane * n4 + (static_cast<uint32_t>(g) < n4 ? static_cast<uint32_t>(g) : n4 - 1)];
+            wr[g] = make_float4(v.x, v.y, v.z, v.w);
         }
     };
     if (active) load_router(0);
     for (uint32_t l = 0; l < a.L; ++l) {
         const uint32_t epoch = a.epoch0 + l;
-        if (l == 0) {
-            for (uint32_t i = threadIdx.x; i < (H >> 2); i += kThreads) {
-                const uint32_t c = i << 2;
-                *reinterpret_cast<float4*>(xs + (c >> 6) * kPad + (c & 63)) = reinterpret_cast<const float4*>(a.x_in)[i];
-            }
-            __syncthreads();
-        } else {
-            gather(a.hbuf + static_cast<size_t>(l - 1) * H, H, epoch - 1, a.err, &S.flag,
-                   [&](uint32_t i, float v) { xs[(i >> 6) * kPad + (i & 63)] = v; });
-        }
+        load_h(a, S, xs, l, epoch);
         if (active) {
-            double total, abs_prefix;
-            exact_logit_regs_lean<kRouterNB>(wr, xs, H, lane, total, abs_prefix);
+            double total, abs_bound;
+            exact_logit_lanes<kRouterNB>(wr, xs, n4, lane, total, abs_bound);
             if (lane == 0) {
                 float lhat, bnd;
-                finish_logit(total, abs_prefix, a.layers[l].bias, gw, H, lhat, bnd);
+                finish_logit(total, abs_bound, a.layers[l].bias, gw, H, lhat, bnd);
                 uint64_t* lw = a.lbuf + static_cast<size_t>(l) * 2 * E;
                 store_word(lw + gw, lhat, epoch);
                 store_word(lw + E + gw, bnd, epoch);
@@ -223,39 +256,69 @@ __device__ void router_role(const StackParams& a, StackLds& S, float* xs) {
     }
 }
 
-// GEMV workgroups. R: row accessor; CHH / CHI: pair chunks per lane for H-wide /
-// I-wide rows; UG: rows per gate/up slot; UD: rows per down slot.
-template <class R, int CHH, int CHI, int UG, int UD>
-__device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* as, float* red, uint32_t gb) {
+// Sums of N values over aligned groups of lpr lanes (a power of two): an xor
+// butterfly, the N values interleaved step by step so that their shuffles overlap.
+// Every lane of a group ends with the group's sums.
+template <int N>
+__device__ __forceinline__ void reduce_groups(float (&v)[N], uint32_t lpr) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        if (static_cast<uint32_t>(off) < lpr) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], off, 64);
+        }
+    }
+}
+
+// GEMV workgroups. R: row accessor; UG: gate/up row groups per wave; CHI: pairs
+// per lane of a down row.
+template <class R, int UG, int CHI>
+__device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* as, float* red,
+                          objeta_hip_expert_ptrs* tab, uint32_t gb) {
     const uint32_t H = a.H, I = a.I, K = a.K, E = a.E;
     const uint32_t pairs_i = I >> 6;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t gwv = gb * kWaves + wave;  // GEMV wave index
-    const uint32_t gs_h = 64 / a.lpr_h, slot_h = lane / a.lpr_h, lp_h = lane - slot_h * a.lpr_h;
-    const uint32_t gs_i = 64 / a.lpr_i, slot_i = lane / a.lpr_i, lp_i = lane - slot_i * a.lpr_i;
-    const uint32_t rows_dn = gs_i * UD;
-    const uint32_t rows_gu = gs_h * UG;
-    const bool has_gu = gwv < a.n_gu_chunks;
-    const bool has_dn = gb < a.n_dn_blocks;
+    const uint32_t lpr_h = a.lpr_h, gs_h = 64 / lpr_h, slot_h = lane / lpr_h, lp_h = lane - slot_h * lpr_h;
+    const uint32_t lpr_i = a.lpr_i, gs_i = 64 / lpr_i, slot_i = lane / lpr_i, lp_i = lane - slot_i * lpr_i;
+    const uint32_t rd = a.rd;
+    const bool has_gu = gwv < a.n_gu_waves;
+    // waves past the last gate/up chunk re-load the last one and publish nothing
+    const uint32_t f0 = (has_gu ? gwv : a.n_gu_waves - 1) * a.rw;  // chunks never straddle slots
+    const uint32_t gj = f0 / I, gi0 = f0 - gj * I;
+    // this lane group's down (row, slot) combination; spare combinations repeat the last
+    const uint32_t combo = wave * gs_i + slot_i;
+    const bool has_dn = combo < rd * K;
+    const uint32_t cc = has_dn ? combo : rd * K - 1;
+    const uint32_t dj = cc % K, drr = cc / K;
+    const uint32_t r_dn = gb * rd + drr;
+    const uint32_t r_dn_c = r_dn < H ? r_dn : H - 1;
     const bool publisher = gb == 0;  // publishes the sequential-path selection and the ids
+    const uint32_t n_tab = E * (sizeof(objeta_hip_expert_ptrs) / 8);
+    uint64_t* tab_w = reinterpret_cast<uint64_t*>(tab);
 
     for (uint32_t l = 0; l < a.L; ++l) {
         const uint32_t epoch = a.epoch0 + l;
         const StackLayerDev& ly = a.layers[l];
-        // ---- h_l into LDS
-        if (l == 0) {
-            for (uint32_t i = threadIdx.x; i < (H >> 2); i += kThreads) {
-                const uint32_t c = i << 2;
-                *reinterpret_cast<float4*>(xs + (c >> 6) * kPad + (c & 63)) = reinterpret_cast<const float4*>(a.x_in)[i];
+        // ---- this layer's expert table: loads issued now, landed by the h wait
+        uint64_t tw[kTabWords];
+        {
+            const gptr<uint64_t> src = as_global(reinterpret_cast<const uint64_t*>(ly.table));
+#pragma unroll
+            for (int q = 0; q < kTabWords; ++q) {
+                const uint32_t i = threadIdx.x + static_cast<uint32_t>(q) * kThreads;
+                tw[q] = src[i < n_tab ? i : n_tab - 1];
             }
-            __syncthreads();
-        } else {
-            gather(a.hbuf + static_cast<size_t>(l - 1) * H, H, epoch - 1, a.err, &S.flag,
-                   [&](uint32_t i, float v) { xs[(i >> 6) * kPad + (i & 63)] = v; });
+        }
+        load_h(a, S, xs, l, epoch);
+#pragma unroll
+        for (int q = 0; q < kTabWords; ++q) {
+            const uint32_t i = threadIdx.x + static_cast<uint32_t>(q) * kThreads;
+            if (i < n_tab) tab_w[i] = tw[q];
         }
         // ---- selection (every GEMV workgroup, same result)
         const uint64_t* lw = a.lbuf + static_cast<size_t>(l) * 2 * E;
-        gather(lw, 2 * E, epoch, a.err, &S.flag, [&](uint32_t i, float v) {
+        gather<false>(lw, 2 * E, epoch, a.err, &S.flag, [&](uint32_t i, float v) {
             if (i < E) S.sel.val[i] = v;
             else S.sel.bnd[i - E] = v;
         });
@@ -271,7 +334,7 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
                     store_word(sw + K + threadIdx.x, S.sel.e[threadIdx.x], epoch);
                 }
             } else {
-                gather(sw, 2 * K, epoch, a.err, &S.flag, [&](uint32_t i, float v) {
+                gather<false>(sw, 2 * K, epoch, a.err, &S.flag, [&](uint32_t i, float v) {
                     if (i < K) {
                         const uint32_t id = __builtin_bit_cast(uint32_t, v);
                         S.sel.sel[i] = static_cast<int>(id < E ? id : 0u);
@@ -287,138 +350,127 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
             for (uint32_t r = 0; r < K; ++r) sel_sum = __fadd_rn(sel_sum, S.sel.e[r]);
             for (uint32_t r = 0; r < K; ++r) S.wsel[r] = a.renormalize ? __fdiv_rn(S.sel.e[r], sel_sum) : S.sel.e[r];
         }
-        if (publisher && ly.ids_out) write_selection(S.sel, K, a.renormalize, ly.ids_out, ly.weights_out);
-        __syncthreads();
 
-        // ---- issue this wave's loads: its gate/up rows, its workgroup's down rows
-        uint32_t dg[UG][CHH][R::kDw], du[UG][CHH][R::kDw];
-        uint32_t gj = 0, gi0 = 0;
-        R gm{}, um{};
-        if (has_gu) {
-            const uint32_t f0 = gwv * rows_gu;  // flattened (slot, row); chunks never straddle slots
-            gj = f0 / I;
-            gi0 = f0 - gj * I;
-            const uint32_t e = static_cast<uint32_t>(S.sel.sel[gj]);
-            const objeta_hip_expert_ptrs P = ly.table[e < E ? e : E - 1];
-            gm = RowsFor<R>::make(P.gate, P.gate_scale, H);
-            um = RowsFor<R>::make(P.up, P.up_scale, H);
+        // ---- every weight load of the layer, issued back to back
+        uint32_t eg = static_cast<uint32_t>(S.sel.sel[gj]);
+        eg = eg < E ? eg : E - 1;
+        uint32_t ed = static_cast<uint32_t>(S.sel.sel[dj]);
+        ed = ed < E ? ed : E - 1;
+        const R gm = RowsFor<R>::make(tab[eg].gate, tab[eg].gate_scale, H);
+        const R um = RowsFor<R>::make(tab[eg].up, tab[eg].up_scale, H);
+        const R dm = RowsFor<R>::make(tab[ed].down, tab[ed].down_scale, I);
+        uint32_t dg[UG][R::kDw], du[UG][R::kDw], dd[CHI][R::kDw];
 #pragma unroll
-            for (int u = 0; u < UG; ++u) {
-                const uint32_t r = gi0 + static_cast<uint32_t>(u) * gs_h + (slot_h < gs_h ? slot_h : 0);
-#pragma unroll
-                for (int c = 0; c < CHH; ++c) {
-                    const uint32_t p = lp_h + static_cast<uint32_t>(c) * a.lpr_h;
-                    gm.load(r, p, dg[u][c]);
-                    um.load(r, p, du[u][c]);
-                }
-            }
+        for (int u = 0; u < UG; ++u) {
+            const uint32_t r = gi0 + static_cast<uint32_t>(u) * gs_h + slot_h;
+            gm.load(r, lp_h, dg[u]);
+            um.load(r, lp_h, du[u]);
         }
-        uint32_t dd[kJW][UD][CHI][R::kDw];
-        R dm[kJW];
-        const uint32_t row0_dn = gb * rows_dn;
-        if (has_dn) {
 #pragma unroll
-            for (int jj = 0; jj < kJW; ++jj) {
-                const uint32_t j = wave * kJW + jj;
-                const uint32_t jc = j < K ? j : K - 1;
-                const uint32_t e = static_cast<uint32_t>(S.sel.sel[jc]);
-                const objeta_hip_expert_ptrs P = ly.table[e < E ? e : E - 1];
-                dm[jj] = RowsFor<R>::make(P.down, P.down_scale, I);
-#pragma unroll
-                for (int u = 0; u < UD; ++u) {
-                    const uint32_t r = row0_dn + static_cast<uint32_t>(u) * gs_i + slot_i;
-                    const uint32_t rc = r < H ? r : H - 1;
-#pragma unroll
-                    for (int c = 0; c < CHI; ++c) dm[jj].load(rc, lp_i + static_cast<uint32_t>(c) * a.lpr_i, dd[jj][u][c]);
-                }
-            }
-        }
+        for (int c = 0; c < CHI; ++c) dm.load(r_dn_c, lp_i + static_cast<uint32_t>(c) * lpr_i, dd[c]);
+        // No barrier until the activation gather: a workgroup barrier also waits for
+        // every load in flight, and the down rows are not needed before then. (wsel,
+        // written by thread 0 above, is read after the gather's barriers.)
+        __builtin_amdgcn_sched_barrier(0);
 
-        // ---- gate/up compute, activation words
+        // ---- gate/up: silu(gate) * up, published as activation words. The lane's
+        // 64 activations are read from LDS once (16 reads in flight) and serve every
+        // gate and up row of the wave from registers.
         uint64_t* aw = a.abuf + static_cast<size_t>(l) * K * I;
-        if (has_gu) {
+        {
+            const float* xl = xs + lp_h * kPad;
+            float4 xr4[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) xr4[q] = *reinterpret_cast<const float4*>(xl + 4 * q);
+            const float* xsp[1] = {reinterpret_cast<const float*>(xr4)};
+            const float* xsl[1] = {xl};
+            float gv[2 * UG];
 #pragma unroll
             for (int u = 0; u < UG; ++u) {
                 float ag[1] = {0.f}, au[1] = {0.f};
+                gm.template dot<1>(dg[u], xsp, ag, xsl);
+                um.template dot<1>(du[u], xsp, au, xsl);
+                gv[2 * u] = ag[0];
+                gv[2 * u + 1] = au[0];
+            }
+            reduce_groups<2 * UG>(gv, lpr_h);
+            if (has_gu && lp_h == 0) {
 #pragma unroll
-                for (int c = 0; c < CHH; ++c) {
-                    const float* xsp[1] = {xs + (lp_h + static_cast<uint32_t>(c) * a.lpr_h) * kPad};
-                    gm.template dot<1>(dg[u][c], xsp, ag);
-                    um.template dot<1>(du[u][c], xsp, au);
-                }
-                const float g = row_reduce(ag[0], lp_h, a.lpr_h);
-                const float v = row_reduce(au[0], lp_h, a.lpr_h);
-                if (slot_h < gs_h && lp_h == 0) {
+                for (int u = 0; u < UG; ++u) {
                     const uint32_t r = gi0 + static_cast<uint32_t>(u) * gs_h + slot_h;
-                    store_word(aw + static_cast<size_t>(gj) * I + r, silu_mul_s(g, v, a.limit), epoch);
+                    store_word(aw + static_cast<size_t>(gj) * I + r, silu_mul_s(gv[2 * u], gv[2 * u + 1], a.limit), epoch);
                 }
             }
         }
+        if (publisher && ly.ids_out) write_selection(S.sel, K, a.renormalize, ly.ids_out, ly.weights_out);
 
-        // ---- down + combine
-        if (has_dn) {
-            gather(aw, K * I, epoch, a.err, &S.flag, [&](uint32_t i, float v) {
-                const uint32_t j = i / I, c = i - j * I;
-                as[(j * pairs_i + (c >> 6)) * kPad + (c & 63)] = v;
-            });
+        // ---- down: gather every activation, finish the row sums from registers
+        gather<true>(aw, K * I, epoch, a.err, &S.flag, [&](uint32_t i, float v) {
+            const uint32_t j = i / I, c = i - j * I;
+            as[(j * pairs_i + (c >> 6)) * kPad + (c & 63)] = v;
+        });
+        {
+            float acc[1] = {0.f};
 #pragma unroll
-            for (int jj = 0; jj < kJW; ++jj) {
-                const uint32_t j = wave * kJW + jj;
-                const uint32_t jc = j < K ? j : K - 1;
+            for (int c = 0; c < CHI; ++c) {
+                const float* al = as + (dj * pairs_i + lp_i + static_cast<uint32_t>(c) * lpr_i) * kPad;
+                float4 ar4[16];
 #pragma unroll
-                for (int u = 0; u < UD; ++u) {
-                    float acc[1] = {0.f};
-#pragma unroll
-                    for (int c = 0; c < CHI; ++c) {
-                        const float* xsp[1] = {as + (jc * pairs_i + lp_i + static_cast<uint32_t>(c) * a.lpr_i) * kPad};
-                        dm[jj].template dot<1>(dd[jj][u][c], xsp, acc);
-                    }
-                    const float v = row_reduce(acc[0], lp_i, a.lpr_i);
-                    if (slot_i < gs_i && lp_i == 0 && j < K) red[j * rows_dn + static_cast<uint32_t>(u) * gs_i + slot_i] = v;
-                }
+                for (int q = 0; q < 16; ++q) ar4[q] = *reinterpret_cast<const float4*>(al + 4 * q);
+                const float* xsp[1] = {reinterpret_cast<const float*>(ar4)};
+                const float* xsl[1] = {al};
+                dm.template dot<1>(dd[c], xsp, acc, xsl);
             }
-            __syncthreads();
-            if (threadIdx.x < rows_dn) {
-                const uint32_t r = row0_dn + threadIdx.x;
-                if (r < H) {
-                    float acc = xs[(r >> 6) * kPad + (r & 63)];
-                    for (uint32_t j = 0; j < K; ++j) acc = __builtin_fmaf(S.wsel[j], red[j * rows_dn + threadIdx.x], acc);
-                    if (l + 1 < a.L) store_word(a.hbuf + static_cast<size_t>(l) * H + r, acc, epoch);
-                    else a.h_out[r] = acc;
-                }
+            reduce_groups<1>(acc, lpr_i);
+            if (has_dn && lp_i == 0) red[dj * rd + drr] = acc[0];
+        }
+        __syncthreads();
+        // ---- combine into the residual in slot order; publish h_{l+1}
+        if (threadIdx.x < rd) {
+            const uint32_t r = gb * rd + threadIdx.x;
+            if (r < H) {
+                float acc = xs[(r >> 6) * kPad + (r & 63)];
+                for (uint32_t j = 0; j < K; ++j) acc = __builtin_fmaf(S.wsel[j], red[j * rd + threadIdx.x], acc);
+                if (l + 1 < a.L) store_word(a.hbuf + static_cast<size_t>(l) * H + r, acc, epoch);
+                else a.h_out[r] = acc;
             }
         }
         __syncthreads();
     }
 }
 
-template <class R, int CHH, int CHI, int UG, int UD>
-__global__ __launch_bounds__(kThreads) void moe_stack_kernel(StackParams a) {
+template <class R, int UG, int CHI>
+__global__ __launch_bounds__(kThreads, 2) void moe_stack_kernel(StackParams a) {
     extern __shared__ float dyn[];
     __shared__ StackLds S;
     const uint32_t pairs_h = a.H >> 6, pairs_i = a.I >> 6;
-    float* xs = dyn;                       // h_l, padded: pairs_h * kPad
-    float* as = dyn + pairs_h * kPad + 4;  // activations, padded: K * pairs_i * kPad
-    float* red = as + a.K * pairs_i * kPad;  // down row sums: K * gs_i * UD
-    const uint32_t n_router = (a.E + kWaves - 1) / kWaves;
-    if (blockIdx.x < n_router) router_role(a, S, xs);
-    else gemv_role<R, CHH, CHI, UG, UD>(a, S, xs, as, red, blockIdx.x - n_router);
+    float* xs = dyn;                                      // h_l, padded: pairs_h * kPad
+    float* as = dyn + pairs_h * kPad;                     // activations, padded: K * pairs_i * kPad
+    float* red = as + a.K * pairs_i * kPad;               // down row sums: K * rd
+    const uint32_t red_n = (a.K * a.rd + 3u) & ~3u;
+    auto* tab = reinterpret_cast<objeta_hip_expert_ptrs*>(red + red_n);  // E entries (16-byte aligned)
+    if (blockIdx.x < a.n_router) router_role(a, S, xs);
+    else gemv_role<R, UG, CHI>(a, S, xs, as, red, tab, blockIdx.x - a.n_router);
 }
 
-template <class R, int CHH, int CHI>
-void* stack_kernel_ptr(int ug, int ud) {
-    if (ug == 2 && ud == 2) return reinterpret_cast<void*>(&moe_stack_kernel<R, CHH, CHI, 2, 2>);
-    if (ug == 2) return reinterpret_cast<void*>(&moe_stack_kernel<R, CHH, CHI, 2, 1>);
-    if (ud == 2) return reinterpret_cast<void*>(&moe_stack_kernel<R, CHH, CHI, 1, 2>);
-    return reinterpret_cast<void*>(&moe_stack_kernel<R, CHH, CHI, 1, 1>);
+template <class R, int UG>
+void* stack_kernel_ug(int chi) {
+    switch (chi) {
+        case 1: return reinterpret_cast<void*>(&moe_stack_kernel<R, UG, 1>);
+        case 2: return reinterpret_cast<void*>(&moe_stack_kernel<R, UG, 2>);
+        case 3: return reinterpret_cast<void*>(&moe_stack_kernel<R, UG, 3>);
+        default: return reinterpret_cast<void*>(&moe_stack_kernel<R, UG, 4>);
+    }
 }
 
 template <class R>
-void* stack_kernel_for(uint32_t chh, uint32_t chi, int ug, int ud) {
-    if (chh == 1 && chi == 1) return stack_kernel_ptr<R, 1, 1>(ug, ud);
-    if (chh == 1) return stack_kernel_ptr<R, 1, 2>(ug, ud);
-    if (chi == 1) return stack_kernel_ptr<R, 2, 1>(ug, ud);
-    return stack_kernel_ptr<R, 2, 2>(ug, ud);
+void* stack_kernel_for(int ug, int chi) {
+    switch (ug) {
+        case 1: return stack_kernel_ug<R, 1>(chi);
+        case 2: return stack_kernel_ug<R, 2>(chi);
+        case 3: return stack_kernel_ug<R, 3>(chi);
+        default: return stack_kernel_ug<R, 4>(chi);
+    }
 }
 
 }  // namespace
@@ -467,35 +519,60 @@ int32_t objeta_hip_moe_stack_create(objeta_hip_context* ctx, int32_t format, con
     }
     const uint32_t H = static_cast<uint32_t>(hidden), I = static_cast<uint32_t>(intermediate);
     const uint32_t K = static_cast<uint32_t>(k), E = static_cast<uint32_t>(n_experts), L = static_cast<uint32_t>(n_layers);
-    const uint32_t lpr_h = pick_lpr(H >> 6), lpr_i = pick_lpr(I >> 6);
-    if (!lpr_h || !lpr_i || (H >> 6) / lpr_h > 2 || (I >> 6) / lpr_i > 2)
-        OBJ_FAIL(kUnsupported, action, "no lane layout for these widths");
-    const uint32_t chh = (H >> 6) / lpr_h, chi = (I >> 6) / lpr_i;
-    const uint32_t gs_h = 64 / lpr_h, gs_i = 64 / lpr_i;
-    int ug = (I % (2 * gs_h) == 0) ? 2 : 1;
-    if (I % (gs_h * ug) != 0) OBJ_FAIL(kUnsupported, action, "intermediate not a multiple of the gate/up rows per wave");
-    const int ud = 2;
+    // gate/up: one pair per lane, H/64 lanes per row (a power of two)
+    const uint32_t pairs_h = H >> 6, pairs_i = I >> 6;
+    if (pairs_h & (pairs_h - 1)) OBJ_FAIL(kUnsupported, action, "hidden/64 must be a power of two");
+    const uint32_t lpr_h = pairs_h, gs_h = 64 / lpr_h;
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    // down: CHI pairs per lane, lpr_i = I/(64*CHI) lanes per (row, slot) (a power of
+    // two); 4*gs_i combinations per workgroup give rd = 4*gs_i/K rows. Among the
+    // layouts whose gate/up rows also fit the same workgroups (UG <= 4, chunks that
+    // do not straddle slots), take the one with the most workgroups up to one per CU.
+    int best_chi = 0, best_ug = 0;
+    uint32_t best_g = 0, best_rd = 0, best_lpr_i = 0, best_rw = 0;
+    for (int chi = 1; chi <= 4; ++chi) {
+        if (pairs_i % chi) continue;
+        const uint32_t lpr_i = pairs_i / chi;
+        if (lpr_i == 0 || lpr_i > 64 || (lpr_i & (lpr_i - 1))) continue;
+        const uint32_t gs_i = 64 / lpr_i;
+        const uint32_t rd = (4 * gs_i / K) > 0 ? 4 * gs_i / K : 1;
+        if (rd * K > 4 * gs_i) continue;
+        const uint32_t g = (H + rd - 1) / rd;
+        for (int ug = 1; ug <= 4; ++ug) {
+            const uint32_t rw = gs_h * ug;
+            if (I % rw) continue;
+            if (K * I / rw > 4 * g) continue;
+            const bool better = best_g == 0 || (g <= cus && (best_g > cus || g > best_g));
+            if (better) {
+                best_chi = chi;
+                best_ug = ug;
+                best_g = g;
+                best_rd = rd;
+                best_lpr_i = lpr_i;
+                best_rw = rw;
+            }
+            break;
+        }
+    }
+    if (!best_g) OBJ_FAIL(kUnsupported, action, "no lane layout for these widths");
     void* kern = nullptr;
     switch (format) {
-        case OBJETA_HIP_Q4_0: kern = stack_kernel_for<QRows<kQ4>>(chh, chi, ug, ud); break;
-        case OBJETA_HIP_Q5_0: kern = stack_kernel_for<QRows<kQ5>>(chh, chi, ug, ud); break;
-        case OBJETA_HIP_IQ3_0: kern = stack_kernel_for<QRows<kIQ3>>(chh, chi, ug, ud); break;
-        default: kern = stack_kernel_for<Fp4Rows>(chh, chi, ug, ud); break;
+        case OBJETA_HIP_Q4_0: kern = stack_kernel_for<QRows<kQ4>>(best_ug, best_chi); break;
+        case OBJETA_HIP_Q5_0: kern = stack_kernel_for<QRows<kQ5>>(best_ug, best_chi); break;
+        case OBJETA_HIP_IQ3_0: kern = stack_kernel_for<QRows<kIQ3>>(best_ug, best_chi); break;
+        default: kern = stack_kernel_for<Fp4Rows>(best_ug, best_chi); break;
     }
-    const uint32_t n_gu_chunks = K * I / (gs_h * ug);
-    const uint32_t rows_dn = gs_i * ud;
-    const uint32_t n_dn_blocks = (H + rows_dn - 1) / rows_dn;
-    const size_t lds = (static_cast<size_t>(H >> 6) * kPad + 4 + static_cast<size_t>(K) * (I >> 6) * kPad +
-                        static_cast<size_t>(K) * rows_dn) * sizeof(float);
+    const uint32_t red_n = (K * best_rd + 3u) & ~3u;
+    const size_t lds = (static_cast<size_t>(pairs_h) * kPad + static_cast<size_t>(K) * pairs_i * kPad + red_n) *
+                           sizeof(float) +
+                       static_cast<size_t>(E) * sizeof(objeta_hip_expert_ptrs);
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     int per_cu = 0;
     OBJ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), kThreads, lds),
             "query stack kernel occupancy");
-    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
     const uint32_t capacity = static_cast<uint32_t>(per_cu) * cus;
-    uint32_t need = (n_gu_chunks + kWaves - 1) / kWaves;  // GEMV workgroups
-    need = need > n_dn_blocks ? need : n_dn_blocks;
-    need += (E + kWaves - 1) / kWaves;  // router workgroups
+    const uint32_t n_router = (E + kWaves - 1) / kWaves;
+    const uint32_t need = best_g + n_router;
     if (per_cu < 1 || need > capacity)
         OBJ_FAIL(kUnsupported, action,
                  strf("needs %u co-resident workgroups, the device holds %u (LDS %zu B)", need, capacity, lds));
@@ -537,10 +614,12 @@ int32_t objeta_hip_moe_stack_create(objeta_hip_context* ctx, int32_t format, con
     p.abuf = reinterpret_cast<uint64_t*>(base + desc_b + h_b + l_b);
     p.sbuf = reinterpret_cast<uint64_t*>(base + desc_b + h_b + l_b + a_b);
     p.err = ctx->counters + ctx->counter_words;
+    p.n_router = n_router;
     p.lpr_h = lpr_h;
-    p.lpr_i = lpr_i;
-    p.n_gu_chunks = n_gu_chunks;
-    p.n_dn_blocks = n_dn_blocks;
+    p.rw = best_rw;
+    p.n_gu_waves = K * I / best_rw;
+    p.lpr_i = best_lpr_i;
+    p.rd = best_rd;
     *out = st;
     return 0;
     OBJ_GUARD_END
