@@ -118,6 +118,8 @@ def main() -> int:
     ap.add_argument("--tokens-pool", type=int, default=16, help="distinct input tokens cycled over steps")
     ap.add_argument("--cpu-tokens", type=int, default=4, help="tokens in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=20251201)
+    ap.add_argument("--path", choices=("auto", "stack", "graph"), default="auto",
+                    help="auto: time both and report the faster as the headline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus > 1 is not supported "
@@ -157,52 +159,78 @@ def main() -> int:
     check(lib.objeta_hip_event_create(ctx, C.byref(ev1)))
     ms = C.c_float()
 
-    # ---- headline: the persistent decode-stack kernel, one launch per token ----
+    expert_bytes_token = L * K * stack.expert_bytes
+    router_bytes_token = L * (4 * E * H)
+
+    def timed(launch, steps):
+        check(lib.objeta_hip_event_record(ctx, ev0, stream))
+        for i in range(steps):
+            launch(i)
+        check(lib.objeta_hip_event_record(ctx, ev1, stream))
+        check(lib.objeta_hip_event_elapsed_ms(ctx, ev0, ev1, C.byref(ms)))
+        be.synchronize(stream)
+        if moe.device_error() != 0:
+            raise RuntimeError("device error word set during a timed run")
+        return ms.value * 1000.0 / steps
+
+    # ---- the persistent decode-stack kernel, one launch per token ----
     layers = [(stack.tables[l], stack.router_w[l], stack.router_b[l], ids.addr(4 * l * K), wts.addr(4 * l * K))
               for l in range(L)]
     plan = MoeStack(be, stack.fmt, layers, E, K, H, I)
-    for i in range(args.warmup):
-        plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream)
-    be.synchronize(stream)
-    check(lib.objeta_hip_event_record(ctx, ev0, stream))
-    for i in range(args.steps):
-        plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream)
-    check(lib.objeta_hip_event_record(ctx, ev1, stream))
-    check(lib.objeta_hip_event_elapsed_ms(ctx, ev0, ev1, C.byref(ms)))
-    be.synchronize(stream)
-    stack_us = ms.value * 1000.0 / args.steps
-    layer_us = stack_us / L
-    expert_bytes_token = L * K * stack.expert_bytes
-    router_bytes_token = L * (4 * E * H)
-    gbps = expert_bytes_token / (stack_us * 1e-6) / 1e9
-    if moe.device_error() != 0:
-        raise RuntimeError("device error word set during the timed run")
-    kernel_bytes = expert_bytes_token + router_bytes_token + 4 * H * 2
-    kernel_gbps = kernel_bytes / (stack_us * 1e-6) / 1e9
+    stack_us = None
+    if args.path in ("auto", "stack"):
+        for i in range(args.warmup):
+            plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream)
+        be.synchronize(stream)
+        stack_us = timed(lambda i: plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream), args.steps)
 
-    # ---- the same stack as three kernels per layer, replayed from a hipGraph ----
-    enqueue_token(0)
-    be.synchronize(stream)
-    graphs = []
-    for p in range(P):
-        check(lib.objeta_hip_graph_begin_capture(ctx, stream))
-        enqueue_token(p)
-        g = C.c_void_p()
-        check(lib.objeta_hip_graph_end_capture(ctx, stream, C.byref(g)))
-        graphs.append(g)
-    gsteps = max(10, args.steps // 4)
-    for i in range(min(args.warmup, 5)):
-        check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream))
-    be.synchronize(stream)
-    check(lib.objeta_hip_event_record(ctx, ev0, stream))
-    for i in range(gsteps):
-        check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream))
-    check(lib.objeta_hip_event_record(ctx, ev1, stream))
-    check(lib.objeta_hip_event_elapsed_ms(ctx, ev0, ev1, C.byref(ms)))
-    be.synchronize(stream)
-    graph_layer_us = ms.value * 1000.0 / gsteps / L
-    if moe.device_error() != 0:
-        raise RuntimeError("device error word set during the graph run")
+    # ---- three kernels per layer (router, gate/up + SiLU, down + combine), replayed from a hipGraph ----
+    graph_us = None
+    gu_us = None
+    if args.path in ("auto", "graph"):
+        enqueue_token(0)
+        be.synchronize(stream)
+        graphs = []
+        for p in range(P):
+            check(lib.objeta_hip_graph_begin_capture(ctx, stream))
+            enqueue_token(p)
+            g = C.c_void_p()
+            check(lib.objeta_hip_graph_end_capture(ctx, stream, C.byref(g)))
+            graphs.append(g)
+        for i in range(args.warmup):
+            check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream))
+        be.synchronize(stream)
+        gsteps = args.steps if args.path == "graph" else max(10, args.steps // 2)
+        graph_us = timed(lambda i: check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream)), gsteps)
+        # the graph's largest kernel on its own: gate/up + SiLU of one layer's 8 selected experts
+        act = be.alloc(4 * K * I)
+        lids = ids.addr(4 * 0 * K)
+
+        def gate_up(i):
+            moe.gate_up_device(stack.fmt, stack.tables[i % L], lids, 1, K, xs.addr(4 * (i % P) * H), act.addr(),
+                               H, I, stream=stream)
+        for i in range(args.warmup):
+            gate_up(i)
+        be.synchronize(stream)
+        gu_us = timed(gate_up, args.steps)
+
+    use_stack = graph_us is None or (stack_us is not None and stack_us <= graph_us)
+    token_us = stack_us if use_stack else graph_us
+    layer_us = token_us / L
+    gbps = expert_bytes_token / (token_us * 1e-6) / 1e9
+    if use_stack:
+        kernel_bytes = expert_bytes_token + router_bytes_token + 4 * H * 2
+        roof = {"kernel": f"moe_stack_kernel (persistent decode stack, {L} layers per launch)", "bound": "hbm",
+                "achieved": round(kernel_bytes / (stack_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(kernel_bytes / (stack_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                "avg_launch_us": round(stack_us, 3), "algorithmic_bytes_per_launch": kernel_bytes}
+    else:
+        # 8 experts' gate and up matrices + x in + activations out
+        kernel_bytes = K * 2 * stack.gu_bytes + 4 * H + 4 * K * I
+        roof = {"kernel": "moe_gate_up_kernel (fused gate/up + SiLU, 8 selected experts, one layer)", "bound": "hbm",
+                "achieved": round(kernel_bytes / (gu_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(kernel_bytes / (gu_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                "avg_launch_us": round(gu_us, 3), "algorithmic_bytes_per_launch": kernel_bytes}
 
     # ---- CPU baseline: oracle restatement, one thread, same layers ----
     cpu = None
@@ -252,7 +280,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(stack_us / 1000.0, 4),
+        "ms_per_step": round(token_us / 1000.0, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -261,15 +289,15 @@ def main() -> int:
         "config": {"workload": "qwen3_a3b_moe_stack", "layers": L, "hidden": H, "experts": E, "top_k": K,
                    "moe_intermediate": I, "batch": 1, "format": "Q4_0", "residency": "all experts in HBM",
                    "tokens_pool": P},
-        "stack_us_per_token": round(stack_us, 2),
+        "path": "persistent decode stack" if use_stack else "three kernels per layer from a hipGraph",
+        "us_per_token": round(token_us, 2),
         "expert_bytes_per_token": expert_bytes_token,
         "expert_hbm_gbps": round(gbps, 1),
         "expert_hbm_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-        "roofline": {"kernel": "moe_stack_kernel (persistent decode stack, 48 layers per launch)", "bound": "hbm",
-                     "achieved": round(kernel_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "avg_launch_us": round(stack_us, 3), "algorithmic_bytes_per_launch": kernel_bytes},
-        "per_layer_graph_us_per_token_layer": round(graph_layer_us, 3),
+        "roofline": roof,
+        "stack_us_per_token_layer": round(stack_us / L, 3) if stack_us is not None else None,
+        "graph_us_per_token_layer": round(graph_us / L, 3) if graph_us is not None else None,
+        "gate_up_kernel_us": round(gu_us, 3) if gu_us is not None else None,
         "stack_grid_workgroups": plan.info()["grid"],
         "cpu_baseline": cpu,
         "device": {"name": dev["name"], "arch": dev["arch"], "compute_units": dev["compute_units"]},

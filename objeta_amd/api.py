@@ -332,6 +332,20 @@ class MoeExecutor:
             _addr(d_weights), n_tokens, k, _addr(d_x), _addr_or_none(d_residual), _addr(d_out), hidden,
             inter, out_dim, swiglu_limit))
 
+    def gate_up_device(self, fmt, table: ExpertTable, d_ids, n_tokens: int, k: int, d_x, d_act,
+                       hidden: int, inter: int, swiglu_limit: float = 0.0, stream=None) -> None:
+        """The fused gate/up + SiLU phase alone: act[t*k + j] = silu(gate_e x_t) * up_e x_t."""
+        check(self.L.objeta_hip_moe_gate_up_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr_or_none(d_ids), n_tokens, k,
+            _addr(d_x), _addr(d_act), hidden, inter, swiglu_limit))
+
+    def down_device(self, fmt, table: ExpertTable, d_ids, d_weights, n_tokens: int, k: int, d_act,
+                    d_residual, d_out, inter: int, out_dim: int, stream=None) -> None:
+        """The down + weighted-combine phase alone: out = residual + sum_j w_j down_e act_j."""
+        check(self.L.objeta_hip_moe_down_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr_or_none(d_ids), _addr(d_weights),
+            n_tokens, k, _addr(d_act), _addr_or_none(d_residual), _addr(d_out), inter, out_dim))
+
     def layer_device(self, fmt, table: ExpertTable, d_router_w, d_router_bias, k: int, n_tokens: int,
                      d_x, d_residual, d_out, d_ids_out, d_weights_out, hidden: int, inter: int,
                      out_dim: int, renormalize: bool = True, swiglu_limit: float = 0.0,

@@ -114,14 +114,28 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     stage_x<1>(lds, x + static_cast<size_t>(t) * hidden, hidden, pairs);
     __syncthreads();
 
+    // with one pair per lane, the lane's 64 activations are read from LDS once and
+    // serve the gate and up rows of every row slot from registers
+    float4 xr4[CH == 1 ? 16 : 1];
+    if constexpr (CH == 1) {
+        const float* xl = lds + lp * kPad;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) xr4[q] = *reinterpret_cast<const float4*>(xl + 4 * q);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         float ag[1] = {0.f}, au[1] = {0.f};
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const float* xs[1] = {lds + (lp + static_cast<uint32_t>(c) * lpr) * kPad};
-            gm.template dot<1>(dg[u][c], xs, ag);
-            um.template dot<1>(du[u][c], xs, au);
+            const float* xl[1] = {lds + (lp + static_cast<uint32_t>(c) * lpr) * kPad};
+            if constexpr (CH == 1) {
+                const float* xr[1] = {reinterpret_cast<const float*>(xr4)};
+                gm.template dot<1>(dg[u][c], xr, ag, xl);
+                um.template dot<1>(du[u][c], xr, au, xl);
+            } else {
+                gm.template dot<1>(dg[u][c], xl, ag);
+                um.template dot<1>(du[u][c], xl, au);
+            }
         }
         const float g = row_reduce(ag[0], lp, lpr);
         const float v = row_reduce(au[0], lp, lpr);
@@ -182,15 +196,27 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
         const uint32_t j = wave * JW + jj;
+        float acc[U][1];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u][0] = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const float* xl[1] = {xst + (jj * pairs + lp + static_cast<uint32_t>(c) * lpr) * kPad};
+            if constexpr (U > 1) {
+                // the chunk's 64 activations, read from LDS once for all U rows
+                float4 xr4[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) xr4[q] = *reinterpret_cast<const float4*>(xl[0] + 4 * q);
+                const float* xr[1] = {reinterpret_cast<const float*>(xr4)};
+#pragma unroll
+                for (int u = 0; u < U; ++u) m[jj].template dot<1>(d[jj][u][c], xr, acc[u], xl);
+            } else {
+                m[jj].template dot<1>(d[jj][0][c], xl, acc[0]);
+            }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float acc[1] = {0.f};
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const float* xs[1] = {xst + (jj * pairs + lp + static_cast<uint32_t>(c) * lpr) * kPad};
-                m[jj].template dot<1>(d[jj][u][c], xs, acc);
-            }
-            const float v = row_reduce(acc[0], lp, lpr);
+            const float v = row_reduce(acc[u][0], lp, lpr);
             if (slot < gs && lp == 0 && j < k)
                 red[j * rows_blk + static_cast<uint32_t>(u) * gs + slot] = ok[jj] ? v : __builtin_nanf("");
         }

@@ -25,7 +25,48 @@ namespace objeta {
 namespace {
 
 using namespace rmath;
+using dev::gptr;
+using dev::as_global;
 
+// Workgroup 0 of token t: gathers the words of this epoch, selects, writes the
+// ids and weights and advances counters[t].
+template <class XAt>
+__device__ void router_select(const float* __restrict__ w_r, const float* __restrict__ bias,
+                              const float* __restrict__ xt, XAt xat, uint32_t n_experts, uint32_t hidden, uint32_t k,
+                              int renormalize, uint32_t* __restrict__ ids, float* __restrict__ weights,
+                              const uint64_t* ws_logit, const uint64_t* ws_bound, uint32_t epoch,
+                              uint32_t* __restrict__ counter, uint32_t* __restrict__ err, float* scratch,
+                              uint32_t scratch_floats) {
+    __shared__ SelectLds<kMaxExperts> s;
+    __shared__ int s_pending;
+    for (uint32_t spin = 0;; ++spin) {
+        if (threadIdx.x == 0) s_pending = 0;
+        __syncthreads();
+        int pending = 0;
+        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) {
+            const uint64_t a = __hip_atomic_load(&ws_logit[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t b = __hip_atomic_load(&ws_bound[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (static_cast<uint32_t>(a >> 32) != epoch || static_cast<uint32_t>(b >> 32) != epoch) pending = 1;
+            s.val[j] = __builtin_bit_cast(float, static_cast<uint32_t>(a));
+            s.bnd[j] = __builtin_bit_cast(float, static_cast<uint32_t>(b));
+        }
+        if (pending) s_pending = 1;
+        __syncthreads();
+        if (!s_pending) break;
+        if (spin >= kSpinLimit) {  // a producer never published: flag it and stop waiting
+            if (threadIdx.x == 0) atomicOr(err, 2u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (!select_certain(s, n_experts, k, renormalize) &&
+        !select_refine(s, w_r, bias, xat, n_experts, hidden, k, renormalize, scratch, scratch_floats))
+        select_sequential(s, w_r, bias, xat, n_experts, hidden, k);
+    write_selection(s, k, renormalize, ids, weights);
+    if (threadIdx.x == 0) __hip_atomic_store(counter, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// General form: each wave reads its expert's row and x from global memory.
 template <bool VEC>
 __global__ __launch_bounds__(kRThreads) void router_kernel(
     const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
@@ -55,34 +96,66 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
         }
     }
     if (blockIdx.x != 0) return;
+    __shared__ float scratch[kRWaves * 256];
+    router_select(w_r, bias, xt, [xt](uint32_t h) { return xt[h]; }, n_experts, hidden, k, renormalize,
+                  ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit, ws_bound, epoch,
+                  &counters[t], err, scratch, kRWaves * 256);
+}
 
-    // ---- workgroup 0 of token t: gather the words of this epoch, select
-    __shared__ SelectLds<kMaxExperts> s;
-    __shared__ int s_pending;
-    for (uint32_t spin = 0;; ++spin) {
-        if (threadIdx.x == 0) s_pending = 0;
-        __syncthreads();
-        int pending = 0;
-        for (uint32_t j = threadIdx.x; j < n_experts; j += kRThreads) {
-            const uint64_t a = __hip_atomic_load(&ws_logit[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint64_t b = __hip_atomic_load(&ws_bound[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (static_cast<uint32_t>(a >> 32) != epoch || static_cast<uint32_t>(b >> 32) != epoch) pending = 1;
-            s.val[j] = __builtin_bit_cast(float, static_cast<uint32_t>(a));
-            s.bnd[j] = __builtin_bit_cast(float, static_cast<uint32_t>(b));
+// hidden % 256 == 0, hidden <= 256 * NB: the row sits lane-contiguously in
+// registers (lane l: elements [l*hidden/64, (l+1)*hidden/64)) and x is staged in
+// LDS, so a logit is one pass of lane-local prefix sums (exact_logit_lanes)
+// instead of a wave scan per 256 elements.
+constexpr uint32_t kRefineScratch = kRWaves * 2048;  // floats of row chunks for select_refine
+
+template <int NB>
+__global__ __launch_bounds__(kRThreads) void router_lanes_kernel(
+    const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
+    uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
+    float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
+    uint32_t* __restrict__ err) {
+    extern __shared__ float xs[];  // x in the padded pair layout: (hidden / 64) * kPadX floats
+    const uint32_t t = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t e = blockIdx.x * kRWaves + (threadIdx.x >> 6);
+    const float* xt = x + static_cast<size_t>(t) * hidden;
+    uint64_t* ws_logit = ws + static_cast<size_t>(t) * 2 * kMaxExperts;
+    uint64_t* ws_bound = ws_logit + kMaxExperts;
+    const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    const uint32_t n4 = hidden >> 8;  // float4 per lane
+    const uint32_t ec = e < n_experts ? e : n_experts - 1;
+    float4 wr[NB];
+    {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const gptr<f32x4> r4 = as_global(reinterpret_cast<const f32x4*>(w_r + static_cast<size_t>(ec) * hidden));
+#pragma unroll
+        for (int g = 0; g < NB; ++g) {
+            const f32x4 v = r4[lane * n4 + (static_cast<uint32_t>(g) < n4 ? static_cast<uint32_t>(g) : n4 - 1)];
+            wr[g] = make_float4(v.x, v.y, v.z, v.w);
         }
-        if (pending) s_pending = 1;
-        __syncthreads();
-        if (!s_pending) break;
-        if (spin >= kSpinLimit) {  // a producer never published: flag it and stop waiting
-            if (threadIdx.x == 0) atomicOr(err, 2u);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
     }
-    if (!select_certain(s, n_experts, k, renormalize))
-        select_sequential(s, w_r, bias, [xt](uint32_t h) { return xt[h]; }, n_experts, hidden, k);
-    write_selection(s, k, renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k);
-    if (threadIdx.x == 0) __hip_atomic_store(&counters[t], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t i = threadIdx.x; i < (hidden >> 2); i += kRThreads) {
+        const uint32_t c = i << 2;
+        *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = reinterpret_cast<const float4*>(xt)[i];
+    }
+    __syncthreads();
+    if (e < n_experts) {
+        double total, abs_bound;
+        exact_logit_lanes<NB>(wr, xs, n4, lane, total, abs_bound);
+        if (lane == 0) {
+            float lhat, bnd;
+            finish_logit(total, abs_bound, bias, e, hidden, lhat, bnd);
+            __hip_atomic_store(&ws_logit[e], tag(lhat, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ws_bound[e], tag(bnd, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (blockIdx.x != 0) return;
+    // x stays in LDS for the refinement; the row chunks go behind it
+    const uint32_t x_floats = (hidden / 64) * kPadX;
+    const float* xl = xs;
+    router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,
+                  renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit,
+                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch);
 }
 
 }  // namespace
@@ -103,7 +176,18 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
     const dim3 grid(static_cast<uint32_t>((n_experts + kRWaves - 1) / kRWaves), static_cast<uint32_t>(n_tokens));
     const bool vec = hidden % 4 == 0 && reinterpret_cast<uintptr_t>(w_r) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     uint32_t* err = ctx->counters + ctx->counter_words;
-    if (vec)
+    const bool lanes = vec && hidden % 256 == 0 && hidden <= 256u * 32u;
+    if (lanes) {
+        const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
+        if (hidden <= 256u * 8u)
+            hipLaunchKernelGGL(router_lanes_kernel<8>, grid, dim3(kRThreads), lds, s, w_r, bias, x,
+                               static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+        else
+            hipLaunchKernelGGL(router_lanes_kernel<32>, grid, dim3(kRThreads), lds, s, w_r, bias, x,
+                               static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+    } else if (vec)
         hipLaunchKernelGGL(router_kernel<true>, grid, dim3(kRThreads), 0, s, w_r, bias, x,
                            static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden), static_cast<uint32_t>(k),
                            renormalize, ids, weights, ws, ctx->counters, err);

@@ -365,6 +365,9 @@ struct SelectLds {
     float red[kRWaves];
     float e[kMaxTopK];
     int flag;
+    int need[MAXE];
+    int nlist[64];
+    int ncount;
 };
 
 // With s.val / s.bnd holding all n logits and bounds (visible to the block):
@@ -417,6 +420,89 @@ __device__ bool select_certain(SelectLds<MAXE>& s, uint32_t n, uint32_t k, int r
     }
     __syncthreads();
     return true;
+}
+
+// After select_certain failed: recomputes, in the reference's sequential order,
+// only the logits of experts involved in an undecided comparison (a selected
+// expert whose interval val +- (bnd + margin) overlaps another expert's), sets
+// their bounds to zero and decides again. Usually a handful of experts instead of
+// all n. Wave w takes needed experts w, w+4, ...: the expert's row streams through
+// the wave's share of `scratch` (LDS) in coalesced chunks and lane 0 adds the
+// products in order. Returns false when the selection is still not certain (or
+// too many experts are involved); the caller then runs select_sequential. xat(h)
+// returns x[h] (best from LDS). Block-wide; 256 threads.
+constexpr int kMaxRefine = 64;
+template <int MAXE, class XAt>
+__device__ bool select_refine(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
+                              XAt xat, uint32_t n, uint32_t hidden, uint32_t k, int renormalize, float* scratch,
+                              uint32_t scratch_floats) {
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) s.need[j] = 0;
+    if (threadIdx.x == 0) s.ncount = 0;
+    __syncthreads();
+    const float mx = s.val[s.sel[0]];
+    for (uint32_t w = threadIdx.x; w < k * n; w += kRThreads) {
+        const uint32_t b = w % n;
+        const int a = s.sel[w / n];
+        if (static_cast<int>(b) == a) continue;
+        const float m = 9.5367431640625e-07f * (1.0f + fabsf(s.val[a] - mx) + fabsf(s.val[b] - mx));
+        const bool apart = (s.val[a] - s.bnd[a] > s.val[b] + s.bnd[b] + m) || (s.val[b] - s.bnd[b] > s.val[a] + s.bnd[a] + m);
+        if (!apart) {
+            s.need[a] = 1;
+            s.need[b] = 1;
+        }
+    }
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
+        if (s.need[j]) {
+            const int slot = atomicAdd(&s.ncount, 1);
+            if (slot < kMaxRefine) s.nlist[slot] = static_cast<int>(j);
+        }
+    }
+    __syncthreads();
+    const int cnt = s.ncount;
+    const uint32_t chunk = (scratch_floats / kRWaves) & ~255u;
+    if (cnt == 0 || cnt > kMaxRefine || chunk == 0) return false;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* buf = scratch + wave * chunk;
+    for (int q = static_cast<int>(wave); q < cnt; q += kRWaves) {
+        const uint32_t e = static_cast<uint32_t>(s.nlist[q]);
+        const float* row = w_r + static_cast<size_t>(e) * hidden;
+        float acc = 0.0f;
+        for (uint32_t c0 = 0; c0 < hidden; c0 += chunk) {
+            const uint32_t m = hidden - c0 < chunk ? hidden - c0 : chunk;
+            // the whole chunk is requested before any of it is stored
+            for (uint32_t i0 = 0; i0 < m; i0 += 8 * 64) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t i = i0 + static_cast<uint32_t>(u) * 64 + lane;
+                    v[u] = row[c0 + (i < m ? i : m - 1)];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t i = i0 + static_cast<uint32_t>(u) * 64 + lane;
+                    if (i < m) buf[i] = v[u];
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane == 0) {
+#pragma unroll 16
+                for (uint32_t i = 0; i < m; ++i) acc = __fadd_rn(acc, __fmul_rn(buf[i], xat(c0 + i)));
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        if (lane == 0) {
+            if (bias) acc = __fadd_rn(acc, bias[e]);
+            s.val[e] = acc;
+            s.bnd[e] = 0.0f;
+        }
+    }
+    __syncthreads();
+    return select_certain(s, n, k, renormalize);
 }
 
 // The reference's order throughout (cpu_router): logits[e] = sum_h fl(W[e,h] * x[h])

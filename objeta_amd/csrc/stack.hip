@@ -322,12 +322,18 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
             if (i < E) S.sel.val[i] = v;
             else S.sel.bnd[i - E] = v;
         });
-        const bool certain = select_certain(S.sel, E, K, a.renormalize);
+        auto xat = [xs](uint32_t h) { return xs[(h >> 6) * kPad + (h & 63)]; };
+        // a close call is first settled by recomputing the few logits involved, which
+        // every workgroup does for itself (same inputs, same result; the activation
+        // area of LDS is free until the gather and holds the row chunks); only what
+        // that cannot settle goes to the publisher's full sequential path
+        const bool certain = select_certain(S.sel, E, K, a.renormalize) ||
+                             select_refine(S.sel, ly.w_r, ly.bias, xat, E, H, K, a.renormalize, as,
+                                           K * pairs_i * kPad);
         uint64_t* sw = a.sbuf + static_cast<size_t>(l) * 2 * K;
         if (!certain) {
             if (publisher) {
-                select_sequential(S.sel, ly.w_r, ly.bias, [xs](uint32_t h) { return xs[(h >> 6) * kPad + (h & 63)]; },
-                                  E, H, K);
+                select_sequential(S.sel, ly.w_r, ly.bias, xat, E, H, K);
                 if (threadIdx.x < K) {
                     store_word(sw + threadIdx.x, __builtin_bit_cast(float, static_cast<uint32_t>(S.sel.sel[threadIdx.x])),
                                epoch);
@@ -351,7 +357,7 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
             for (uint32_t r = 0; r < K; ++r) S.wsel[r] = a.renormalize ? __fdiv_rn(S.sel.e[r], sel_sum) : S.sel.e[r];
         }
 
-        // ---- every weight load of the layer, issued back to back
+        // ---- every gate/up weight load of the wave, issued back to back
         uint32_t eg = static_cast<uint32_t>(S.sel.sel[gj]);
         eg = eg < E ? eg : E - 1;
         uint32_t ed = static_cast<uint32_t>(S.sel.sel[dj]);
@@ -366,11 +372,9 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
             gm.load(r, lp_h, dg[u]);
             um.load(r, lp_h, du[u]);
         }
-#pragma unroll
-        for (int c = 0; c < CHI; ++c) dm.load(r_dn_c, lp_i + static_cast<uint32_t>(c) * lpr_i, dd[c]);
         // No barrier until the activation gather: a workgroup barrier also waits for
-        // every load in flight, and the down rows are not needed before then. (wsel,
-        // written by thread 0 above, is read after the gather's barriers.)
+        // every load in flight. (wsel, written by thread 0 above, is read after the
+        // gather's barriers.)
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- gate/up: silu(gate) * up, published as activation words. The lane's
@@ -402,6 +406,12 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
                 }
             }
         }
+        // The down rows are requested only now: they land while the workgroup waits
+        // for the other workgroups' activations, and the gate/up stream before them
+        // has the memory system (and the registers) to itself.
+#pragma unroll
+        for (int c = 0; c < CHI; ++c) dm.load(r_dn_c, lp_i + static_cast<uint32_t>(c) * lpr_i, dd[c]);
+        __builtin_amdgcn_sched_barrier(0);
         if (publisher && ly.ids_out) write_selection(S.sel, K, a.renormalize, ly.ids_out, ly.weights_out);
 
         // ---- down: gather every activation, finish the row sums from registers

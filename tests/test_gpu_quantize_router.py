@@ -144,3 +144,31 @@ def test_router_underflowing_probabilities_order_by_index(backend):
         assert list(ids[t]) == list(rid), f"token {t}"
         assert np.allclose(ws[t], rw, rtol=2e-5, atol=1e-6)
     assert zero_tail > 0  # the index-ordered zero-probability case is exercised
+
+
+def _close_calls(ne, hidden, seed, gaps):
+    """W_r whose logits for one token have adjacent top-ranked pairs `gaps` apart
+    (closer than the parallel error bound, farther than the probability margin)."""
+    w = orc.gauss(ne * hidden, seed, 0.02).reshape(ne, hidden).copy()
+    x = orc.gauss(hidden, seed + 1, 1.0)
+    j = int(np.argmax(np.abs(x)))
+    for r, gap in gaps:
+        logits = orc.router(w.ravel(), x, ne, hidden, 1)[2]
+        order = np.argsort(-logits.astype(np.float64), kind="stable")
+        a, b = order[r], order[r + 1]
+        w[b, j] += np.float32((float(logits[a]) - gap - float(logits[b])) / float(x[j]))
+    return w, x
+
+
+@pytest.mark.parametrize("seed", [31, 32, 33, 34])
+def test_router_close_calls_are_settled_exactly(backend, seed):
+    """Selected experts 3e-5 apart (and one pair at the top-8 boundary): the kernel
+    recomputes just those logits in the reference's order and must still agree."""
+    ne, hidden, k = 128, 2048, 8
+    w, x = _close_calls(ne, hidden, seed, [(1, 3e-5), (4, 2e-5), (7, 3e-5)])
+    ids, ws = _router(backend, w.ravel(), x, None, ne, hidden, k, 1)
+    rid, rw, logits, _ = orc.router(w.ravel(), x, ne, hidden, k)
+    order = np.argsort(-logits.astype(np.float64), kind="stable")
+    assert float(logits[order[7]] - logits[order[8]]) < 1e-4  # the construction made a close call
+    assert list(ids[0]) == list(rid)
+    assert np.allclose(ws[0], rw, rtol=2e-5, atol=1e-6)

@@ -160,3 +160,30 @@ def test_stack_rejects_unsupported_shapes(backend):
         MoeStack(backend, 0, layers, 8, 9, 256, 64)
     assert e.value.kind in ("Unsupported", "InvalidInput")
     del keep
+
+
+def test_stack_close_calls_are_settled_exactly(backend):
+    """Layer 0's router has adjacent selected experts 2-3e-5 apart for the run's token:
+    every workgroup recomputes those logits and the stack must match the oracle."""
+    from test_gpu_quantize_router import _close_calls
+    E, K, H, I = 64, 8, 512, 256
+    layers, host, keep = make_stack(backend, 0, 2, E, K, H, I, seed=7, bias=False)
+    w, x = _close_calls(E, H, 41, [(1, 3e-5), (4, 2e-5), (7, 3e-5)])
+    table, d_w, d_b, ids, wts = layers[0]
+    layers[0] = (table, backend.to_device(w.ravel()), d_b, ids, wts)
+    keep.append(layers[0][1])
+    experts_h, _, b = host[0]
+    host[0] = (experts_h, w.ravel(), b)
+    st = MoeStack(backend, 0, layers, E, K, H, I)
+    d_x = backend.to_device(x)
+    d_out = backend.alloc(4 * H)
+    st.run(d_x, d_out)
+    backend.synchronize()
+    assert MoeExecutor(backend).device_error() == 0
+    ref, rids, rws = oracle_stack(0, host, x, E, K, H, I, 6)
+    for l, (_, _, _, ids_l, wts_l) in enumerate(layers):
+        assert np.array_equal(ids_l.download(np.uint32, K), rids[l]), f"layer {l}"
+        np.testing.assert_allclose(wts_l.download(np.float32, K), rws[l], rtol=2e-5, atol=1e-7)
+    check_close(d_out.download(np.float32, H), ref)
+    st.close()
+    del keep
