@@ -263,6 +263,26 @@ int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, 
                                        uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
                                        float swiglu_limit);
 
+/* objeta_hip_moe_selected_device for a batch whose tokens share experts: the
+ * (token, slot) assignments are grouped by expert on the device and every selected
+ * expert's gate, up and down matrices are read once for all of its tokens, with
+ * the products on the matrix cores (fp16 weights, exact for every format, times
+ * activations split into two fp16 parts; fp32 accumulation). Same arguments and
+ * result (within the fp32 tolerance) as objeta_hip_moe_selected_device; no
+ * reference counterpart as one call (execute_selected_moe_cuda, moe.rs:352-751,
+ * runs each selected expert per token). Limits: n_experts <= 1024, n_tokens * k
+ * <= 1024, hidden and intermediate multiples of 64; Unsupported outside them.
+ * d_ids is required. An out-of-table id sets bit 1 of the device error word and
+ * makes that token's output NaN. Non-finite block scales give a non-finite output
+ * element, but not necessarily the same special value as the reference's
+ * per-weight products. */
+int32_t objeta_hip_moe_grouped_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                      const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                      const uint32_t* d_ids, const float* d_weights, uint64_t n_tokens,
+                                      uint64_t k, const float* d_x, const float* d_residual, float* d_out,
+                                      uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                      float swiglu_limit);
+
 /* The two launches of objeta_hip_moe_selected_device, for callers that keep the
  * activations: d_act [n_tokens*k][intermediate] f32 (16-byte aligned) receives
  * silu(gate x) * (up x) per (token, slot); the down phase combines them. */

@@ -332,6 +332,15 @@ class MoeExecutor:
             _addr(d_weights), n_tokens, k, _addr(d_x), _addr_or_none(d_residual), _addr(d_out), hidden,
             inter, out_dim, swiglu_limit))
 
+    def grouped_device(self, fmt, table: ExpertTable, d_ids, d_weights, n_tokens: int, k: int, d_x,
+                       d_residual, d_out, hidden: int, inter: int, out_dim: int,
+                       swiglu_limit: float = 0.0, stream=None) -> None:
+        """selected_device for a batch: assignments grouped by expert, each expert's
+        matrices read once for all its tokens, products on the matrix cores."""
+        check(self.L.objeta_hip_moe_grouped_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr(d_ids), _addr(d_weights), n_tokens,
+            k, _addr(d_x), _addr_or_none(d_residual), _addr(d_out), hidden, inter, out_dim, swiglu_limit))
+
     def gate_up_device(self, fmt, table: ExpertTable, d_ids, n_tokens: int, k: int, d_x, d_act,
                        hidden: int, inter: int, swiglu_limit: float = 0.0, stream=None) -> None:
         """The fused gate/up + SiLU phase alone: act[t*k + j] = silu(gate_e x_t) * up_e x_t."""

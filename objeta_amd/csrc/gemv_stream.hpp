@@ -99,6 +99,23 @@ struct Fp4Rows {
     }
 };
 
+// A row accessor over one expert tensor: pointer(s) from an expert table entry and
+// the tensor's column count.
+template <class R>
+struct RowsOf;
+template <int F>
+struct RowsOf<QRows<F>> {
+    static __device__ __forceinline__ QRows<F> make(const void* w, const void*, uint32_t cols) {
+        return QRows<F>{static_cast<const uint8_t*>(w), static_cast<size_t>(cols >> 5) * Fmt<F>::kBlockBytes};
+    }
+};
+template <>
+struct RowsOf<Fp4Rows> {
+    static __device__ __forceinline__ Fp4Rows make(const void* w, const void* s, uint32_t cols) {
+        return Fp4Rows{static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(s), cols >> 1, cols >> 5};
+    }
+};
+
 // Stages NT activation vectors of `cols` floats (cols % 64 == 0) into LDS, padded
 // per 64, with every global load issued before the first LDS write. The LDS
 // allocation must hold NT * pairs * kPad + 4 floats (a spare slot at the end).

@@ -71,7 +71,7 @@ struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
-enum WsSlot : int { kWsRouter = 0, kWsMoeAct = 1, kWsMoeTable = 2, kWsMoeOut = 3, kWsSlots = 4 };
+enum WsSlot : int { kWsRouter = 0, kWsMoeAct = 1, kWsMoeTable = 2, kWsMoeOut = 3, kWsGrouped = 4, kWsSlots = 5 };
 
 }  // namespace objeta
 

@@ -27,20 +27,6 @@
 namespace objeta {
 namespace dev {
 
-template <class R>
-struct RowsOf;
-template <int F>
-struct RowsOf<QRows<F>> {
-    static __device__ __forceinline__ QRows<F> make(const void* w, const void*, uint32_t cols) {
-        return QRows<F>{static_cast<const uint8_t*>(w), static_cast<size_t>(cols >> 5) * Fmt<F>::kBlockBytes};
-    }
-};
-template <>
-struct RowsOf<Fp4Rows> {
-    static __device__ __forceinline__ Fp4Rows make(const void* w, const void* s, uint32_t cols) {
-        return Fp4Rows{static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(s), cols >> 1, cols >> 5};
-    }
-};
 
 // silu_mul (kernels/moe.cu:2-22); the CPU reference is moe.rs:1308-1315.
 __device__ __forceinline__ float silu_mul(float g, float u, float limit) {

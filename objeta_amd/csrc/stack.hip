@@ -170,21 +170,6 @@ __device__ void gather(const uint64_t* __restrict__ p, uint32_t n, uint32_t epoc
     }
 }
 
-template <class R>
-struct RowsFor;
-template <int F>
-struct RowsFor<QRows<F>> {
-    static __device__ __forceinline__ QRows<F> make(const void* w, const void*, uint32_t cols) {
-        return QRows<F>{static_cast<const uint8_t*>(w), static_cast<size_t>(cols >> 5) * Fmt<F>::kBlockBytes};
-    }
-};
-template <>
-struct RowsFor<Fp4Rows> {
-    static __device__ __forceinline__ Fp4Rows make(const void* w, const void* s, uint32_t cols) {
-        return Fp4Rows{static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(s), cols >> 1, cols >> 5};
-    }
-};
-
 __device__ __forceinline__ float silu_mul_s(float g, float u, float limit) {
     if (limit > 0.0f) {
         u = fminf(limit, fmaxf(-limit, u));
@@ -362,9 +347,9 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
         eg = eg < E ? eg : E - 1;
         uint32_t ed = static_cast<uint32_t>(S.sel.sel[dj]);
         ed = ed < E ? ed : E - 1;
-        const R gm = RowsFor<R>::make(tab[eg].gate, tab[eg].gate_scale, H);
-        const R um = RowsFor<R>::make(tab[eg].up, tab[eg].up_scale, H);
-        const R dm = RowsFor<R>::make(tab[ed].down, tab[ed].down_scale, I);
+        const R gm = RowsOf<R>::make(tab[eg].gate, tab[eg].gate_scale, H);
+        const R um = RowsOf<R>::make(tab[eg].up, tab[eg].up_scale, H);
+        const R dm = RowsOf<R>::make(tab[ed].down, tab[ed].down_scale, I);
         uint32_t dg[UG][R::kDw], du[UG][R::kDw], dd[CHI][R::kDw];
 #pragma unroll
         for (int u = 0; u < UG; ++u) {

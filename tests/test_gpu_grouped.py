@@ -1,0 +1,124 @@
+"""Grouped-token expert product (objeta_hip_moe_grouped_device) on the GPU.
+
+A batch of tokens whose selections overlap: every token's output must equal the
+CPU oracle's selected_moe_cpu (moe.rs:1283-1324) / selected_moe_cpu_native_fp4
+(moe.rs:1665-1735) for that token plus its residual, within the fp32 bars used by
+the other MoE tests, and agree with the per-assignment path
+(objeta_hip_moe_selected_device) on the same inputs. Groups of more than 8 tokens
+cover several MFMA column sets."""
+import numpy as np
+import pytest
+
+from objeta_amd import HipError, MoeExecutor
+from oracle import oracle as orc
+from test_gpu_moe import FP4, IQ3, Q4, Q5, assert_moe_close, device_table, make_experts, oracle_experts
+
+pytestmark = pytest.mark.gpu
+
+
+def skewed_selection(T, K, E, seed):
+    """Per token K distinct experts, drawn from a Zipf-like popularity so that a few
+    experts are shared by many tokens; weights softmax-like and positive."""
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, E + 1) ** 1.2
+    p /= p.sum()
+    sel = []
+    for _ in range(T):
+        ids = rng.choice(E, size=K, replace=False, p=p)
+        w = rng.random(K).astype(np.float32) + np.float32(0.1)
+        w /= w.sum()
+        sel.append([(int(i), float(v)) for i, v in zip(ids, w)])
+    return sel
+
+
+def run_grouped(backend, fmt, experts, sel, xs, hidden, inter, out_dim, residual):
+    moe = MoeExecutor(backend)
+    table, keep = device_table(backend, fmt, experts)
+    T, K = len(sel), len(sel[0])
+    ids = np.array([[s[0] for s in row] for row in sel], np.uint32).ravel()
+    ws = np.array([[s[1] for s in row] for row in sel], np.float32).ravel()
+    d_ids, d_w = backend.to_device(ids), backend.to_device(ws)
+    d_x = backend.to_device(np.asarray(xs, np.float32).ravel())
+    d_r = backend.to_device(np.asarray(residual, np.float32).ravel())
+    out_g = backend.alloc(4 * T * out_dim)
+    out_s = backend.alloc(4 * T * out_dim)
+    moe.grouped_device(fmt, table, d_ids, d_w, T, K, d_x, d_r, out_g, hidden, inter, out_dim)
+    moe.selected_device(fmt, table, d_ids, d_w, T, K, d_x, d_r, out_s, hidden, inter, out_dim)
+    backend.synchronize()
+    err = moe.device_error()
+    g = out_g.download(np.float32, T * out_dim).reshape(T, out_dim)
+    s = out_s.download(np.float32, T * out_dim).reshape(T, out_dim)
+    del keep
+    return g, s, err
+
+
+@pytest.mark.parametrize("fmt,E,K,T,H,I,O", [
+    (Q4, 16, 4, 16, 512, 256, 512),
+    (Q4, 128, 8, 16, 2048, 768, 2048),   # Qwen3-A3B layer shape, batch 16
+    (Q5, 12, 3, 20, 256, 128, 192),
+    (IQ3, 10, 4, 12, 512, 192, 320),
+    (FP4, 12, 4, 24, 1024, 512, 1024),
+])
+def test_grouped_matches_oracle_and_per_assignment(backend, fmt, E, K, T, H, I, O):
+    experts = make_experts(fmt, E, H, I, O, seed=E * 7 + K, gen="gauss")
+    sel = skewed_selection(T, K, E, seed=T + fmt)
+    counts = np.bincount([e for row in sel for e, _ in row], minlength=E)
+    xs = orc.gauss(T * H, 11 + fmt, 1.0).reshape(T, H)
+    res = orc.gauss(T * O, 12 + fmt, 1.0).reshape(T, O)
+    g, s, err = run_grouped(backend, fmt, experts, sel, xs, H, I, O, res)
+    assert err == 0
+    oe = oracle_experts(fmt, experts)
+    for t in range(T):
+        ref = orc.selected_moe(fmt, oe, sel[t], xs[t], H, I, O) + res[t]
+        assert_moe_close(g[t], ref)
+    scale = float(np.max(np.abs(s)))
+    assert float(np.max(np.abs(g - s))) <= 1e-4 * scale
+    if T >= 16:
+        assert counts.max() > 8  # some group spans two MFMA column sets
+
+
+def test_grouped_lcg_experts_and_no_residual(backend):
+    """The reference tests' LCG weights (uniform(-1,1), moe.rs:1770-1790), out = 0 + sum."""
+    fmt, E, K, T, H, I, O = Q4, 6, 2, 9, 256, 128, 256
+    experts = make_experts(fmt, E, H, I, O, seed=0xC0FFEE)
+    sel = skewed_selection(T, K, E, seed=3)
+    xs = orc.seeded_f32s(T * H, 0xDEADBEEF).reshape(T, H)
+    moe = MoeExecutor(backend)
+    table, keep = device_table(backend, fmt, experts)
+    ids = np.array([[s[0] for s in row] for row in sel], np.uint32).ravel()
+    ws = np.array([[s[1] for s in row] for row in sel], np.float32).ravel()
+    out = backend.alloc(4 * T * O)
+    moe.grouped_device(fmt, table, backend.to_device(ids), backend.to_device(ws), T, K, backend.to_device(xs.ravel()),
+                       None, out, H, I, O)
+    backend.synchronize()
+    assert moe.device_error() == 0
+    got = out.download(np.float32, T * O).reshape(T, O)
+    oe = oracle_experts(fmt, experts)
+    for t in range(T):
+        assert_moe_close(got[t], orc.selected_moe(fmt, oe, sel[t], xs[t], H, I, O))
+    del keep
+
+
+def test_grouped_out_of_table_id_is_reported(backend):
+    fmt, E, K, T, H, I, O = Q4, 4, 2, 3, 256, 128, 256
+    experts = make_experts(fmt, E, H, I, O, seed=5, gen="gauss")
+    sel = [[(0, 0.5), (1, 0.5)], [(2, 0.5), (E + 3, 0.5)], [(3, 0.7), (0, 0.3)]]
+    xs = orc.gauss(T * H, 1, 1.0).reshape(T, H)
+    res = np.zeros((T, O), np.float32)
+    g, _, err = run_grouped(backend, fmt, experts, sel, xs, H, I, O, res)
+    assert err & 1
+    assert np.all(np.isnan(g[1]))
+    oe = oracle_experts(fmt, experts)
+    for t in (0, 2):
+        assert_moe_close(g[t], orc.selected_moe(fmt, oe, sel[t], xs[t], H, I, O))
+
+
+def test_grouped_rejects_unsupported_shapes(backend):
+    moe = MoeExecutor(backend)
+    experts = make_experts(Q4, 2, 96, 64, 64, seed=1, gen="gauss")
+    table, keep = device_table(backend, Q4, experts)
+    d = backend.alloc(4096)
+    with pytest.raises(HipError) as e:
+        moe.grouped_device(Q4, table, d, d, 1, 1, d, None, d, 96, 64, 64)  # hidden 96 is not a multiple of 64
+    assert e.value.kind == "Unsupported"
+    del keep
