@@ -120,6 +120,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20251201)
     ap.add_argument("--path", choices=("auto", "stack", "graph"), default="auto",
                     help="auto: time both and report the faster as the headline")
+    ap.add_argument("--batch", type=int, default=16,
+                    help="tokens of the batched side measurement (grouped-token path); 0 skips it")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus > 1 is not supported "
@@ -232,6 +234,53 @@ def main() -> int:
                 "frac": round(kernel_bytes / (gu_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
                 "avg_launch_us": round(gu_us, 3), "algorithmic_bytes_per_launch": kernel_bytes}
 
+    # ---- side measurement: a batch of tokens through the same 48 layers ----
+    batch = None
+    if args.batch > 0:
+        B = args.batch
+        xb = be.alloc(4 * B * H)
+        check(lib.objeta_hip_fill_gauss_device(ctx, None, xb.addr(), B * H, args.seed + 99, 0, C.c_float(1.0)))
+        hb = be.alloc(4 * B * H)
+        idsb = be.alloc(4 * L * B * K)
+        wtsb = be.alloc(4 * L * B * K)
+
+        def enqueue_batch(grouped: bool):
+            for l in range(L):
+                src = xb.addr() if l == 0 else hb.addr()
+                li, lw = idsb.addr(4 * l * B * K), wtsb.addr(4 * l * B * K)
+                if grouped:  # the layer entry point takes the grouped path for batches
+                    moe.layer_device(stack.fmt, stack.tables[l], stack.router_w[l], stack.router_b[l], K, B, src,
+                                     src, hb.addr(), li, lw, H, I, H, stream=stream)
+                else:  # router, then one expert pass per (token, slot)
+                    check(lib.objeta_hip_router_topk_device(ctx, stream, stack.router_w[l].addr(),
+                                                            stack.router_b[l].addr(), src, B, E, H, K, 1, li, lw))
+                    moe.selected_device(stack.fmt, stack.tables[l], li, lw, B, K, src, src, hb.addr(), H, I, H,
+                                        stream=stream)
+
+        res = {}
+        for grouped in (True, False):
+            enqueue_batch(grouped)
+            be.synchronize(stream)
+            check(lib.objeta_hip_graph_begin_capture(ctx, stream))
+            enqueue_batch(grouped)
+            gb = C.c_void_p()
+            check(lib.objeta_hip_graph_end_capture(ctx, stream, C.byref(gb)))
+            for i in range(3):
+                check(lib.objeta_hip_graph_launch(ctx, gb, stream))
+            be.synchronize(stream)
+            res[grouped] = timed(lambda i: check(lib.objeta_hip_graph_launch(ctx, gb, stream)),
+                                 max(5, args.steps // 20))
+        ids_all = idsb.download(np.uint32, L * B * K).reshape(L, B * K)
+        uniq = [len(set(int(v) for v in ids_all[l])) for l in range(L)]
+        unique_bytes = sum(uniq) * stack.expert_bytes
+        batch = {"tokens": B, "path": "grouped-token expert product (MFMA), three-kernel router + experts per layer",
+                 "us_per_step": round(res[True], 1),
+                 "us_per_token_layer": round(res[True] / (L * B), 3),
+                 "per_assignment_path_us_per_step": round(res[False], 1),
+                 "unique_experts_per_layer": round(sum(uniq) / L, 1),
+                 "unique_expert_bytes_per_step": unique_bytes,
+                 "expert_hbm_gbps": round(unique_bytes / (res[True] * 1e-6) / 1e9, 1)}
+
     # ---- CPU baseline: oracle restatement, one thread, same layers ----
     cpu = None
     if args.cpu_tokens > 0:
@@ -299,6 +348,7 @@ def main() -> int:
         "graph_us_per_token_layer": round(graph_us / L, 3) if graph_us is not None else None,
         "gate_up_kernel_us": round(gu_us, 3) if gu_us is not None else None,
         "stack_grid_workgroups": plan.info()["grid"],
+        "batch": batch,
         "cpu_baseline": cpu,
         "device": {"name": dev["name"], "arch": dev["arch"], "compute_units": dev["compute_units"]},
     }

@@ -9,9 +9,9 @@
 //   moe_group_kernel     assignments (token, slot) sorted by expert, stable; one
 //                        group per distinct selected expert
 //   moe_split_kernel     activation rows -> two fp16 parts (see below), per token
-//   moe_grouped_gate_up  per (group, 64 rows): silu(gate x) * (up x) for the group
+//   moe_grouped_kernel   per (group, 16 rows): silu(gate x) * (up x) for the group
 //   moe_split_kernel     the activations of every assignment
-//   moe_grouped_down     per (group, 64 rows): down act for every assignment
+//   moe_grouped_kernel   per (group, 16 rows): down act for every assignment
 //   moe_combine_kernel   out = residual + sum_j w_j down_j in slot order
 //
 // Exactness. Weights enter the MFMA as fp16 values that are exact for every
@@ -301,21 +301,46 @@ struct LaneBlock<Fp4Rows> {
 };
 
 // ----------------------------------------------------------- grouped GEMMs
-// grid = (ceil(rows / 64), max groups); wave w of block b owns output rows
-// [(4b + w) * 16, +16) of the group's expert; 8 group members per MFMA column set.
-// GATEUP: rows = inter over x (cols = hidden), writes act; else rows = out_dim
-// over act (cols = inter), writes part.
+// Cached (not non-temporal) pair loads: the four lanes of a row read the same
+// bytes and consecutive pairs share cache lines, so the lines must stay in L1/L2
+// until the wave has used them.
+template <class R>
+struct PairLoad;
+template <int F>
+struct PairLoad<QRows<F>> {
+    static __device__ __forceinline__ void load(const QRows<F>& m, uint32_t r, uint32_t p, uint32_t (&d)[Fmt<F>::kPairDw]) {
+        const gptr<uint32_t> q = as_global(reinterpret_cast<const uint32_t*>(m.pair_ptr(r, p)));
+#pragma unroll
+        for (int i = 0; i < Fmt<F>::kPairDw; ++i) d[i] = q[i];
+    }
+};
+template <>
+struct PairLoad<Fp4Rows> {
+    static __device__ __forceinline__ void load(const Fp4Rows& m, uint32_t r, uint32_t p, uint32_t (&d)[9]) {
+        const gptr<uint32_t> q = as_global(reinterpret_cast<const uint32_t*>(m.w + static_cast<size_t>(r) * m.wrow + p * 32u));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[i] = q[i];
+        d[8] = *as_global(reinterpret_cast<const uint16_t*>(m.s + static_cast<size_t>(r) * m.srow + p * 2u));
+    }
+};
+
+constexpr int kGPairs = 1;  // pairs per wave per step (more in flight measured slower: registers)
+
+// grid = (ceil(rows / 16), max groups), 4 waves: the workgroup owns output rows
+// [16 blockIdx.x, +16) of the group's expert and wave w the w-th quarter of the
+// pairs (k split); the four partial sums meet in LDS. 8 group members per MFMA
+// column set. GATEUP: rows = inter over x (cols = hidden), writes act; else
+// rows = out_dim over act (cols = inter), writes part.
 template <class R, bool GATEUP>
 __global__ __launch_bounds__(256) void moe_grouped_kernel(
     const objeta_hip_expert_ptrs* __restrict__ table, GroupWs gw, const _Float16* __restrict__ vh,
     const _Float16* __restrict__ vl, const float* __restrict__ vmult, float* __restrict__ out, uint32_t cols,
     uint32_t rows, uint32_t k, float limit) {
+    __shared__ f32x4 red[GATEUP ? 2 : 1][3][64];
     const uint32_t g = blockIdx.y;
     if (g >= gw.hdr[0]) return;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t tile = (blockIdx.x * 4 + wave) * 16;
-    if (tile >= rows) return;
-    const uint32_t row = tile + (lane & 15), kg = lane >> 4;
+    const uint32_t row = blockIdx.x * 16 + (lane & 15), kg = lane >> 4;
     const uint32_t rc = row < rows ? row : rows - 1;
     const uint32_t e = gw.grp_expert[g];
     const uint32_t s0 = gw.grp_start[g], m = gw.grp_start[g + 1] - s0;
@@ -323,58 +348,88 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(
     const R w0 = GATEUP ? RowsOf<R>::make(P.gate, P.gate_scale, cols) : RowsOf<R>::make(P.down, P.down_scale, cols);
     const R w1 = RowsOf<R>::make(P.up, P.up_scale, cols);
     const uint32_t pairs = cols >> 6;
+    const uint32_t ppw = (pairs + 3) / 4;
+    const uint32_t p0 = wave * ppw < pairs ? wave * ppw : pairs;
+    const uint32_t p1 = p0 + ppw < pairs ? p0 + ppw : pairs;
     for (uint32_t c0 = 0; c0 < m; c0 += 8) {
         // A operand: member c0 + (lane&15)/2 of the group, part (lane&1)
         const uint32_t jm = c0 + ((lane & 15) >> 1);
         const uint32_t am = gw.alist[s0 + (jm < m ? jm : m - 1)];
         const uint32_t vrow = GATEUP ? am / k : am;  // token row of x, or the assignment's act row
-        const _Float16* src = ((lane & 1) ? vl : vh) + static_cast<size_t>(vrow) * cols + 8 * kg;
+        const gptr<half8> src = as_global(reinterpret_cast<const half8*>(
+            ((lane & 1) ? vl : vh) + static_cast<size_t>(vrow) * cols + 8 * kg));
         f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-        for (uint32_t p = 0; p < pairs; ++p) {
-            uint32_t d0[R::kDw], d1[R::kDw];
-            w0.load(rc, p, d0);
-            if constexpr (GATEUP) w1.load(rc, p, d1);
-            const half8 x0 = *reinterpret_cast<const half8*>(src + 64 * p);
-            const half8 x1 = *reinterpret_cast<const half8*>(src + 64 * p + 32);
+        for (uint32_t pb = p0; pb < p1; pb += kGPairs) {
+            uint32_t d0[kGPairs][R::kDw], d1[kGPairs][R::kDw];
+            half8 xa[kGPairs][2];
 #pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-                const half8 xa = blk ? x1 : x0;
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                float sc0;
-                const half8 b0 = LaneBlock<R>::get(d0, blk, kg, sc0);
-                const f32x4 r0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b0, z, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc0[i] = __builtin_fmaf(sc0, r0[i], acc0[i]);
-                if constexpr (GATEUP) {
-                    float sc1;
-                    const half8 b1 = LaneBlock<R>::get(d1, blk, kg, sc1);
-                    const f32x4 r1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b1, z, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc1[i] = __builtin_fmaf(sc1, r1[i], acc1[i]);
-                }
+            for (int i = 0; i < kGPairs; ++i) {
+                const uint32_t p = pb + i < p1 ? pb + i : p1 - 1;
+                PairLoad<R>::load(w0, rc, p, d0[i]);
+                if constexpr (GATEUP) PairLoad<R>::load(w1, rc, p, d1[i]);
+                xa[i][0] = src[8 * p];  // half8 units: 64 halves per pair
+                xa[i][1] = src[8 * p + 4];
             }
-        }
-        // lane: output row `row`, members c0 + 2kg + q (q = 0, 1) as (hi, lo) in i = 2q, 2q+1
+            // every load of the batch is in flight before the first product; pairs
+            // past p1 (clamped copies) are computed and dropped, so the batch has no
+            // branch for the scheduler to sink loads into
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const uint32_t j = c0 + 2 * kg + static_cast<uint32_t>(q);
-            if (j < m && row < rows) {
-                const uint32_t a = gw.alist[s0 + j];
-                const float mul = vmult[GATEUP ? a / k : a];
-                const float v0 = (acc0[2 * q] + acc0[2 * q + 1]) * mul;
-                if constexpr (GATEUP) {
-                    const float v1 = (acc1[2 * q] + acc1[2 * q + 1]) * mul;
-                    float gv = v0, uv = v1;
-                    if (limit > 0.0f) {
-                        uv = fminf(limit, fmaxf(-limit, uv));
-                        gv = fminf(limit, gv);
+            for (int i = 0; i < kGPairs; ++i) {
+                const bool use = pb + i < p1;
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk) {
+                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    float sc0;
+                    const half8 b0 = LaneBlock<R>::get(d0[i], blk, kg, sc0);
+                    const f32x4 r0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[i][blk], b0, z, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc0[q] = use ? __builtin_fmaf(sc0, r0[q], acc0[q]) : acc0[q];
+                    if constexpr (GATEUP) {
+                        float sc1;
+                        const half8 b1 = LaneBlock<R>::get(d1[i], blk, kg, sc1);
+                        const f32x4 r1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[i][blk], b1, z, 0, 0, 0);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) acc1[q] = use ? __builtin_fmaf(sc1, r1[q], acc1[q]) : acc1[q];
                     }
-                    out[static_cast<size_t>(a) * rows + row] = (gv / (1.0f + expf(-gv))) * uv;
-                } else {
-                    out[static_cast<size_t>(a) * rows + row] = v0;
                 }
             }
         }
+        // the four waves' partial sums (same lane layout) meet in LDS; wave 0 adds
+        if (wave > 0) {
+            red[0][wave - 1][lane] = acc0;
+            if constexpr (GATEUP) red[GATEUP ? 1 : 0][wave - 1][lane] = acc1;
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int v = 0; v < 3; ++v) {
+                acc0 += red[0][v][lane];
+                if constexpr (GATEUP) acc1 += red[GATEUP ? 1 : 0][v][lane];
+            }
+            // lane: output row `row`, members c0 + 2kg + q (q = 0, 1) as (hi, lo) in 2q, 2q+1
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const uint32_t j = c0 + 2 * kg + static_cast<uint32_t>(q);
+                if (j < m && row < rows) {
+                    const uint32_t a = gw.alist[s0 + j];
+                    const float mul = vmult[GATEUP ? a / k : a];
+                    const float v0 = (acc0[2 * q] + acc0[2 * q + 1]) * mul;
+                    if constexpr (GATEUP) {
+                        const float v1 = (acc1[2 * q] + acc1[2 * q + 1]) * mul;
+                        float gv = v0, uv = v1;
+                        if (limit > 0.0f) {
+                            uv = fminf(limit, fmaxf(-limit, uv));
+                            gv = fminf(limit, gv);
+                        }
+                        out[static_cast<size_t>(a) * rows + row] = (gv / (1.0f + expf(-gv))) * uv;
+                    } else {
+                        out[static_cast<size_t>(a) * rows + row] = v0;
+                    }
+                }
+            }
+        }
+        __syncthreads();  // red is reused by the next member set
     }
 }
 
@@ -402,15 +457,22 @@ hipError_t launch_grouped(hipStream_t s, const objeta_hip_expert_ptrs* table, Gr
                           const _Float16* xl, const float* xmult, float* act, _Float16* ah, _Float16* al,
                           float* amult, float* part, uint32_t n_assign, uint32_t max_groups, uint32_t k,
                           uint32_t hidden, uint32_t inter, uint32_t out_dim, float limit) {
-    hipLaunchKernelGGL((moe_grouped_kernel<R, true>), dim3((inter + 63) / 64, max_groups), dim3(256), 0, s, table, gw,
+    hipLaunchKernelGGL((moe_grouped_kernel<R, true>), dim3((inter + 15) / 16, max_groups), dim3(256), 0, s, table, gw,
                        xh, xl, xmult, act, hidden, inter, k, limit);
     hipLaunchKernelGGL(moe_split_kernel, dim3(n_assign), dim3(256), 0, s, act, inter, ah, al, amult);
-    hipLaunchKernelGGL((moe_grouped_kernel<R, false>), dim3((out_dim + 63) / 64, max_groups), dim3(256), 0, s, table,
+    hipLaunchKernelGGL((moe_grouped_kernel<R, false>), dim3((out_dim + 15) / 16, max_groups), dim3(256), 0, s, table,
                        gw, ah, al, amult, part, inter, out_dim, k, 0.0f);
     return hipGetLastError();
 }
 
 }  // namespace
+
+bool grouped_supported(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden, uint64_t inter,
+                       uint64_t out_dim) {
+    return n_table > 0 && n_table <= kGMaxTable && k > 0 && k <= 32 && n_tokens * k <= kGMaxAssign && hidden > 0 &&
+           inter > 0 && hidden % 64 == 0 && inter % 64 == 0 && hidden <= (1u << 20) && inter <= (1u << 20) &&
+           out_dim <= (1u << 20);
+}
 
 int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
