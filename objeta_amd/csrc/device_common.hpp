@@ -194,7 +194,7 @@ __device__ __forceinline__ int reg_value(const uint32_t (&n)[4], uint32_t m, int
 }
 
 template <int F, int NT>
-__device__ __forceinline__ void block_dot_reference_form(const uint32_t (&n)[4], uint32_t m, float scale,
+__device__ __noinline__ void block_dot_reference_form(const uint32_t (&n)[4], uint32_t m, float scale,
                                                          const float* const (&xs)[NT], int xoff,
                                                          float (&acc)[NT]) {
 #pragma unroll 1

@@ -433,7 +433,7 @@ __device__ bool select_certain(SelectLds<MAXE>& s, uint32_t n, uint32_t k, int r
 // returns x[h] (best from LDS). Block-wide; 256 threads.
 constexpr int kMaxRefine = 64;
 template <int MAXE, class XAt>
-__device__ bool select_refine(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
+__device__ __noinline__ bool select_refine(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
                               XAt xat, uint32_t n, uint32_t hidden, uint32_t k, int renormalize, float* scratch,
                               uint32_t scratch_floats) {
     for (uint32_t j = threadIdx.x; j < n; j += kRThreads) s.need[j] = 0;
@@ -512,7 +512,7 @@ __device__ bool select_refine(SelectLds<MAXE>& s, const float* __restrict__ w_r,
 // arguments (only a probability tie could expose that). Fills s.sel and s.e (the
 // probabilities). xat(h) returns x[h]. Block-wide; 256 threads.
 template <int MAXE, class XAt>
-__device__ void select_sequential(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
+__device__ __noinline__ void select_sequential(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
                                   XAt xat, uint32_t n, uint32_t hidden, uint32_t k) {
     __shared__ float s_sum_exp;
     for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
