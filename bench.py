@@ -109,6 +109,46 @@ class Stack:
         return g, u, d
 
 
+TRAFFIC_PROFILE = "profiles/moe_layer_q4_qwen3a3b_hbm_traffic.md"
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (counters cannot be read from inside the run)."""
+    path = os.path.join(ROOT, TRAFFIC_PROFILE)
+    try:
+        for line in open(path):
+            if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_calibration(be, lib) -> int:
+    """Kernels of known traffic for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE: a fill of
+    64 MiB (writes only) and a Q4_0 GEMV over a 16384 x 4096 matrix (37,748,736 B read
+    once, plus 16 KiB of x)."""
+    from objeta_amd import check
+    ctx = be.ctx
+    fill = be.alloc(64 << 20)
+    rows, cols = 16384, 4096
+    wq = be.alloc(rows * (cols // 32) * 18)
+    check(lib.objeta_hip_fill_gauss_quantized_device(ctx, 0, None, wq.addr(), rows, cols, 5, C.c_float(0.02)))
+    x = be.alloc(4 * cols)
+    y = be.alloc(4 * rows)
+    check(lib.objeta_hip_fill_gauss_device(ctx, None, x.addr(), cols, 6, 0, C.c_float(1.0)))
+    be.synchronize()
+    for _ in range(5):
+        check(lib.objeta_hip_zero_device(ctx, None, fill.addr(), 64 << 20))
+        check(lib.objeta_hip_qgemv_device(ctx, 0, None, wq.addr(), x.addr(), y.addr(), rows, cols, 1))
+    be.synchronize()
+    print(json.dumps({"calibration": {"fill_bytes": 64 << 20, "gemv_weight_bytes": rows * (cols // 32) * 18,
+                                      "gemv_x_bytes": 4 * cols, "gemv_y_bytes": 4 * rows}}), flush=True)
+    be.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +160,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20251201)
     ap.add_argument("--path", choices=("auto", "stack", "graph"), default="auto",
                     help="auto: time both and report the faster as the headline")
+    ap.add_argument("--pmc-calibrate", action="store_true",
+                    help="only run the counter calibration kernels (a 64 MiB fill, a 37.7 MB streaming read)")
     ap.add_argument("--batch", type=int, default=16,
                     help="tokens of the batched side measurement (grouped-token path); 0 skips it")
     args = ap.parse_args()
@@ -135,6 +177,8 @@ def main() -> int:
     be = HipBackend(0, 2)
     lib = load()
     ctx = be.ctx
+    if args.pmc_calibrate:
+        return pmc_calibration(be, lib)
     t0 = time.time()
     stack = Stack(be, L, H, E, K, I, args.seed)
     print(f"# generated {L} layers x {E} experts ({L * E * stack.expert_bytes / 1e9:.2f} GB) in "
@@ -229,9 +273,11 @@ def main() -> int:
     else:
         # 8 experts' gate and up matrices + x in + activations out
         kernel_bytes = K * 2 * stack.gu_bytes + 4 * H + 4 * K * I
+        traffic = measured_traffic("moe_gate_up_kernel")
         roof = {"kernel": "moe_gate_up_kernel (fused gate/up + SiLU, 8 selected experts, one layer)", "bound": "hbm",
                 "achieved": round(kernel_bytes / (gu_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(kernel_bytes / (gu_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(kernel_bytes / (gu_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                "traffic_source": TRAFFIC_PROFILE if traffic else None,
                 "avg_launch_us": round(gu_us, 3), "algorithmic_bytes_per_launch": kernel_bytes}
 
     # ---- side measurement: a batch of tokens through the same 48 layers ----
