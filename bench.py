@@ -260,6 +260,32 @@ def main() -> int:
         be.synchronize(stream)
         gu_us = timed(gate_up, args.steps)
 
+    # ---- side measurement: the fused single-launch layer (one selection slot per XCD) ----
+    fused_us = None
+    if args.path == "auto" and moe.layer_fused_supported(stack.fmt, E, K, H, I, H, stream=stream):
+        def enqueue_fused(p: int):
+            x0 = xs.addr(4 * p * H)
+            for l in range(L):
+                src = x0 if l == 0 else h.addr()
+                moe.layer_fused_device(stack.fmt, stack.tables[l], stack.router_w[l], stack.router_b[l], K, src, src,
+                                       h.addr(), ids.addr(4 * l * K), wts.addr(4 * l * K), H, I, H, stream=stream)
+        enqueue_fused(0)
+        be.synchronize(stream)
+        fgraphs = []
+        for p in range(P):
+            check(lib.objeta_hip_graph_begin_capture(ctx, stream))
+            enqueue_fused(p)
+            g = C.c_void_p()
+            check(lib.objeta_hip_graph_end_capture(ctx, stream, C.byref(g)))
+            fgraphs.append(g)
+        for i in range(args.warmup):
+            check(lib.objeta_hip_graph_launch(ctx, fgraphs[i % P], stream))
+        be.synchronize(stream)
+        fused_us = timed(lambda i: check(lib.objeta_hip_graph_launch(ctx, fgraphs[i % P], stream)),
+                         max(10, args.steps // 2))
+        for g in fgraphs:
+            check(lib.objeta_hip_graph_destroy(ctx, g))
+
     use_stack = graph_us is None or (stack_us is not None and stack_us <= graph_us)
     token_us = stack_us if use_stack else graph_us
     layer_us = token_us / L
@@ -398,6 +424,7 @@ def main() -> int:
         "roofline": roof,
         "stack_us_per_token_layer": round(stack_us / L, 3) if stack_us is not None else None,
         "graph_us_per_token_layer": round(graph_us / L, 3) if graph_us is not None else None,
+        "fused_us_per_token_layer": round(fused_us / L, 3) if fused_us is not None else None,
         "gate_up_kernel_us": round(gu_us, 3) if gu_us is not None else None,
         "stack_grid_workgroups": plan.info()["grid"],
         "batch": batch,

@@ -311,6 +311,30 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
                                     float* d_weights_out, uint64_t hidden, uint64_t intermediate,
                                     uint64_t out_dim, float swiglu_limit);
 
+/* The layer of objeta_hip_moe_layer_device for one token (same arguments and
+ * results, n_tokens == 1) as a single launch: XCD x of the device computes every
+ * router logit itself, selects, and streams selection slot x's gate/up and down
+ * rows; activations pass between the CUs of an XCD through its L2 and only the
+ * down row sums cross XCDs. Unsupported (kind Unsupported) outside the limits of
+ * objeta_hip_moe_layer_fused_supported. No host synchronisation; graph-capturable
+ * after one call outside capture. No reference counterpart. */
+int32_t objeta_hip_moe_layer_fused_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                          const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
+                                          const float* d_router_w, const float* d_router_bias, uint64_t k,
+                                          int32_t renormalize, const float* d_x, const float* d_residual,
+                                          float* d_out, uint32_t* d_ids_out, float* d_weights_out, uint64_t hidden,
+                                          uint64_t intermediate, uint64_t out_dim, float swiglu_limit);
+
+/* *out = 1 when objeta_hip_moe_layer_fused_device takes these arguments, else 0:
+ * top-8 routing, n_experts <= 256,
+ * hidden a power-of-two multiple of 64 in 256..2048, intermediate a multiple of
+ * 64, out_dim == hidden, a grid that fits on the device at once, and consecutive
+ * workgroups dispatched to consecutive XCDs of 8 (probed on the first call made
+ * outside graph capture). No reference counterpart. */
+int32_t objeta_hip_moe_layer_fused_supported(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                             uint64_t n_experts, uint64_t k, uint64_t hidden,
+                                             uint64_t intermediate, uint64_t out_dim, int32_t* out);
+
 /* ------------------------------------------------------------ decode stack */
 /* One MoE layer of a decode stack: its expert table (n_experts entries), router
  * weights [n_experts][hidden] (16-byte aligned) and optional bias, and optional

@@ -139,6 +139,9 @@ SIGNATURES = {
                                              U64, F32]),
     "objeta_hip_moe_layer_device": (I32, [P, I32, P, P, U64, P, P, U64, I32, U64, P, P, P, P, P,
                                           U64, U64, U64, F32]),
+    "objeta_hip_moe_layer_fused_supported": (I32, [P, I32, P, U64, U64, U64, U64, U64, P]),
+    "objeta_hip_moe_layer_fused_device": (I32, [P, I32, P, P, U64, P, P, U64, I32, P, P, P, P, P, U64, U64, U64,
+                                                F32]),
     "objeta_hip_device_error": (I32, [P, P]),
     "objeta_hip_moe_grouped_device": (I32, [P, I32, P, P, U64, P, P, U64, U64, P, P, P, U64, U64, U64, F32]),
     "objeta_hip_moe_gate_up_device": (I32, [P, I32, P, P, U64, P, U64, U64, P, P, U64, U64, F32]),

@@ -365,6 +365,23 @@ class MoeExecutor:
             _addr_or_none(d_residual), _addr(d_out), _addr(d_ids_out), _addr(d_weights_out), hidden,
             inter, out_dim, swiglu_limit))
 
+    def layer_fused_device(self, fmt, table: ExpertTable, d_router_w, d_router_bias, k: int, d_x, d_residual, d_out,
+                           d_ids_out, d_weights_out, hidden: int, inter: int, out_dim: int, renormalize: bool = True,
+                           swiglu_limit: float = 0.0, stream=None) -> None:
+        """layer_device for one token as a single launch (one selection slot per XCD)."""
+        check(self.L.objeta_hip_moe_layer_fused_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr(d_router_w),
+            _addr_or_none(d_router_bias), k, 1 if renormalize else 0, _addr(d_x), _addr_or_none(d_residual),
+            _addr(d_out), _addr(d_ids_out), _addr(d_weights_out), hidden, inter, out_dim, swiglu_limit))
+
+    def layer_fused_supported(self, fmt, n_experts: int, k: int, hidden: int, inter: int, out_dim: int,
+                              stream=None) -> bool:
+        """Whether layer_fused_device takes these arguments."""
+        v = C.c_int32(0)
+        check(self.L.objeta_hip_moe_layer_fused_supported(self.backend.ctx, int(fmt), stream, n_experts, k, hidden,
+                                                          inter, out_dim, C.byref(v)))
+        return bool(v.value)
+
     def device_error(self) -> int:
         v = C.c_uint32(0)
         check(self.L.objeta_hip_device_error(self.backend.ctx, C.byref(v)))

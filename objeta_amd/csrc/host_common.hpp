@@ -71,7 +71,15 @@ struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
-enum WsSlot : int { kWsRouter = 0, kWsMoeAct = 1, kWsMoeTable = 2, kWsMoeOut = 3, kWsGrouped = 4, kWsSlots = 5 };
+enum WsSlot : int {
+    kWsRouter = 0,
+    kWsMoeAct = 1,
+    kWsMoeTable = 2,
+    kWsMoeOut = 3,
+    kWsGrouped = 4,
+    kWsFused = 5,
+    kWsSlots = 6
+};
 
 }  // namespace objeta
 
@@ -90,6 +98,9 @@ struct objeta_hip_context {
                                         // followed by the device error word
 
     size_t counter_words = 0;
+    // workgroup b runs on XCD b % 8 of an 8-XCD device (probed once): -1 unknown,
+    // 0 no, 1 yes
+    int xcd_round_robin = -1;
     std::mutex mu;
 };
 

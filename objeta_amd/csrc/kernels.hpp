@@ -41,4 +41,17 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
                            const float* x, const float* resid, float* out, uint64_t hidden, uint64_t inter,
                            uint64_t out_dim, float limit);
 
+// One layer of one token in a single launch (router, gate/up + SiLU, down +
+// combine, top-8, one selection slot per XCD); false when the shape is outside it,
+// its grid does not fit at once, or workgroups are not dispatched round-robin over
+// the 8 XCDs (probed on the first call outside graph capture).
+bool fused_layer_supported(objeta_hip_context* ctx, hipStream_t s, int32_t format, uint64_t n_experts, uint64_t k,
+                           uint64_t hidden, uint64_t inter, uint64_t out_dim);
+
+int32_t launch_moe_layer_fused(objeta_hip_context* ctx, int32_t format, hipStream_t s,
+                               const objeta_hip_expert_ptrs* table, uint64_t n_experts, const float* w_r,
+                               const float* bias, uint64_t k, int32_t renormalize, const float* x, const float* resid,
+                               float* out, uint32_t* ids_out, float* weights_out, uint64_t hidden, uint64_t inter,
+                               float limit);
+
 }  // namespace objeta

@@ -626,6 +626,40 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
     OBJ_GUARD_END
 }
 
+int32_t objeta_hip_moe_layer_fused_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                          const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
+                                          const float* d_router_w, const float* d_router_bias, uint64_t k,
+                                          int32_t renormalize, const float* d_x, const float* d_residual,
+                                          float* d_out, uint32_t* d_ids_out, float* d_weights_out, uint64_t hidden,
+                                          uint64_t intermediate, uint64_t out_dim, float swiglu_limit) {
+    OBJ_GUARD_BEGIN
+    const char* action = "moe_layer_fused_device";
+    OBJ_TRY(check_ctx(ctx, action));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    if (!d_ids_out || !d_weights_out) OBJ_FAIL(kInvalidInput, action, "NULL routing output");
+    if (!fused_layer_supported(ctx, s, format, n_experts, k, hidden, intermediate, out_dim))
+        OBJ_FAIL(kUnsupported, action, "shape, grid or XCD placement outside the fused layer");
+    return launch_moe_layer_fused(ctx, format, s, d_table, n_experts, d_router_w, d_router_bias, k, renormalize, d_x,
+                                  d_residual, d_out, d_ids_out, d_weights_out, hidden, intermediate, swiglu_limit);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_moe_layer_fused_supported(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                             uint64_t n_experts, uint64_t k, uint64_t hidden,
+                                             uint64_t intermediate, uint64_t out_dim, int32_t* out) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "moe_layer_fused_supported"));
+    if (!out) OBJ_FAIL(kInvalidInput, "moe_layer_fused_supported", "out is NULL");
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    *out = fused_layer_supported(ctx, resolve_stream(ctx, stream), format, n_experts, k, hidden, intermediate,
+                                   out_dim)
+                 ? 1
+                 : 0;
+    return 0;
+    OBJ_GUARD_END
+}
+
 int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out) {
     OBJ_GUARD_BEGIN
     OBJ_TRY(check_ctx(ctx, "device error word"));

@@ -353,6 +353,49 @@ __device__ __forceinline__ void exact_logit_lanes(const float4 (&w)[NB], const f
     abs_bound = wave_sum_d(b);
 }
 
+// exact_logit_lanes for a row split over the four waves of a workgroup: wave w owns
+// elements [w*H/4, (w+1)*H/4) and its lane l the 4*n4 elements from
+// w*H/4 + 4*n4*l, held as w[0..n4) (H = 1024*n4, n4 <= NB). Each lane runs one
+// chain of prefix sums s_i and sum |s_i|; a wave scan gives the lane's offset
+// inside its wave, the four wave totals meet in LDS (added in wave order), and a
+// lane at global offset T adds 4*n4*|T| + sum |s_i| to the bound. Block-wide: every
+// thread reaches both barriers. red: 8 doubles of LDS. total and abs_bound are
+// returned in every thread.
+template <int NB>
+__device__ __forceinline__ void exact_logit_split(const float4 (&w)[NB], const float* __restrict__ x_lds,
+                                                  uint32_t n4, uint32_t lane, uint32_t wave, double* red,
+                                                  double& total, double& abs_bound) {
+    double s = 0.0, a = 0.0;
+    const uint32_t base = wave * n4 * 256u + lane * n4 * 4u;
+#pragma unroll
+    for (int g = 0; g < NB; ++g) {
+        if (static_cast<uint32_t>(g) < n4) {
+            const uint32_t h = base + 4u * static_cast<uint32_t>(g);
+            const float4 v = *reinterpret_cast<const float4*>(x_lds + (h >> 6) * kPadX + (h & 63));
+            s += static_cast<double>(__fmul_rn(w[g].x, v.x));
+            a += fabs(s);
+            s += static_cast<double>(__fmul_rn(w[g].y, v.y));
+            a += fabs(s);
+            s += static_cast<double>(__fmul_rn(w[g].z, v.z));
+            a += fabs(s);
+            s += static_cast<double>(__fmul_rn(w[g].w, v.w));
+            a += fabs(s);
+        }
+    }
+    const double incl = wave_scan_d(s, static_cast<int>(lane));
+    double t = __shfl_up(incl, 1, 64);
+    if (lane == 0) t = 0.0;
+    if (lane == 63) red[wave] = incl;
+    __syncthreads();
+    double tw = 0.0;
+    for (uint32_t q = 0; q < wave; ++q) tw += red[q];
+    total = ((red[0] + red[1]) + red[2]) + red[3];
+    const double bw = wave_sum_d(static_cast<double>(4u * n4) * fabs(tw + t) + a);
+    if (lane == 0) red[4 + wave] = bw;
+    __syncthreads();
+    abs_bound = ((red[4] + red[5]) + red[6]) + red[7];
+}
+
 // -------------------------------------------------------------------- selection
 template <int MAXE>
 struct SelectLds {
@@ -360,8 +403,10 @@ struct SelectLds {
     float bnd[MAXE];
     int rank[MAXE];
     int part[kRThreads];
-    __align__(16) uint64_t key[MAXE + 8];
+    __align__(16) uint64_t key[MAXE + 16];
     int sel[kMaxTopK + 1];
+    float sv[kMaxTopK + 1];  // val and bnd of the ranked experts, in rank order
+    float sb[kMaxTopK + 1];
     float red[kRWaves];
     float e[kMaxTopK];
     int flag;
@@ -378,45 +423,74 @@ struct SelectLds {
 // threads.
 template <int MAXE>
 __device__ bool select_certain(SelectLds<MAXE>& s, uint32_t n, uint32_t k, int renormalize) {
-    if (threadIdx.x == 0) s.flag = 0;
-    for (uint32_t j = threadIdx.x; j < ((n + 7) & ~7u); j += kRThreads) s.key[j] = j < n ? order_key(s.val[j], j) : 0ull;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t n16 = (n + 15) & ~15u;
+    for (uint32_t j = tid; j < n16; j += kRThreads) s.key[j] = j < n ? order_key(s.val[j], j) : 0ull;
+    if (tid == 0) s.flag = 0;
     __syncthreads();
+    // rank of every key: P adjacent lanes share a key's comparisons and add their
+    // counts with xor shuffles (no barrier); each lane reads its keys 16 at a time
+    // with all reads in flight together. The ranked experts' values and bounds are
+    // recorded in rank order for the checks below.
     const uint32_t want = k + 1 <= n ? k + 1 : n;
-    rank_select(s.key, static_cast<int>(n), static_cast<int>(want), s.rank, s.sel, s.part);
-    __syncthreads();
-    const float mx = s.val[s.sel[0]];
-    {
-        const float lk = s.val[s.sel[k - 1]];
-        const float kmin_lo = lk - s.bnd[s.sel[k - 1]];
-        int unsure = 0;
-        for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
-            if (s.rank[j] >= static_cast<int>(k)) {
-                const float margin = 9.5367431640625e-07f * (1.0f + fabsf(s.val[j] - mx) + fabsf(lk - mx));
-                if (!(s.val[j] + s.bnd[j] + margin < kmin_lo)) unsure = 1;
+    uint32_t P = 1;
+    while (P < 8 && P * 2 * n <= kRThreads) P *= 2;
+    const uint32_t groups = n16 >> 4;
+    const uint32_t per = (groups + P - 1) / P;
+    for (uint32_t w = tid; w < n * P; w += kRThreads) {
+        const uint32_t e = w / P, part = w % P;
+        const uint64_t me = s.key[e];
+        int r = 0;
+        const uint32_t g0 = part * per, g1 = g0 + per < groups ? g0 + per : groups;
+        for (uint32_t g = g0; g < g1; ++g) {
+            ulonglong2 kv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kv[i] = *reinterpret_cast<const ulonglong2*>(&s.key[16 * g + 2 * i]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r += (kv[i].x > me) + (kv[i].y > me);
+        }
+        for (uint32_t off = 1; off < P; off <<= 1) r += __shfl_xor(r, static_cast<int>(off), 64);
+        if (part == 0) {
+            s.rank[e] = r;
+            if (r < static_cast<int>(want)) {
+                s.sel[r] = static_cast<int>(e);
+                s.sv[r] = s.val[e];
+                s.sb[r] = s.bnd[e];
             }
         }
-        if (threadIdx.x + 1 < k) {
-            const int a = s.sel[threadIdx.x], b = s.sel[threadIdx.x + 1];
-            const float margin = 9.5367431640625e-07f * (1.0f + fabsf(s.val[a] - mx) + fabsf(s.val[b] - mx));
-            if (!(s.val[a] - s.bnd[a] > s.val[b] + s.bnd[b] + margin)) unsure = 1;
-        }
-        // The margins assume normal probabilities: once exp(l_k - max) / sum can be
-        // subnormal or zero, distinct logits can give equal probabilities, which the
-        // reference's stable sort orders by index.
-        if (threadIdx.x == 0 && !(lk - s.bnd[s.sel[k - 1]] - mx > -80.0f)) unsure = 1;
-        if (unsure) s.flag = 1;
     }
+    __syncthreads();
+    const float mx = s.sv[0];
+    const float lk = s.sv[k - 1];
+    const float kmin_lo = lk - s.sb[k - 1];
+    int unsure = 0;
+    for (uint32_t j = tid; j < n; j += kRThreads) {
+        if (s.rank[j] >= static_cast<int>(k)) {
+            const float margin = 9.5367431640625e-07f * (1.0f + fabsf(s.val[j] - mx) + fabsf(lk - mx));
+            if (!(s.val[j] + s.bnd[j] + margin < kmin_lo)) unsure = 1;
+        }
+    }
+    if (tid + 1 < k) {
+        const float va = s.sv[tid], vb = s.sv[tid + 1];
+        const float margin = 9.5367431640625e-07f * (1.0f + fabsf(va - mx) + fabsf(vb - mx));
+        if (!(va - s.sb[tid] > vb + s.sb[tid + 1] + margin)) unsure = 1;
+    }
+    // The margins assume normal probabilities: once exp(l_k - max) / sum can be
+    // subnormal or zero, distinct logits can give equal probabilities, which the
+    // reference's stable sort orders by index.
+    if (tid == 0 && !(kmin_lo - mx > -80.0f)) unsure = 1;
+    if (unsure) s.flag = 1;
     __syncthreads();
     if (s.flag) return false;
     float z = 1.0f;
     if (!renormalize) {
         float part = 0.0f;
-        for (uint32_t j = threadIdx.x; j < n; j += kRThreads) part += expf(s.val[j] - mx);
+        for (uint32_t j = tid; j < n; j += kRThreads) part += expf(s.val[j] - mx);
         z = block_sum(part, s.red);
     }
-    if (threadIdx.x < k) {
-        const float ev = expf(__fsub_rn(s.val[s.sel[threadIdx.x]], mx));
-        s.e[threadIdx.x] = renormalize ? ev : __fdiv_rn(ev, z);
+    if (tid < k) {
+        const float ev = expf(__fsub_rn(s.sv[tid], mx));
+        s.e[tid] = renormalize ? ev : __fdiv_rn(ev, z);
     }
     __syncthreads();
     return true;
