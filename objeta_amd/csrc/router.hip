@@ -158,6 +158,58 @@ __global__ __launch_bounds__(kRThreads) void router_lanes_kernel(
                   ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch);
 }
 
+// hidden % 1024 == 0, hidden <= 1024 * NB: one workgroup per expert, the row split
+// over its four waves (exact_logit_split), so each lane holds 4*hidden/1024
+// elements and the exact sum is a short chain per lane; four times as many
+// workgroups as router_lanes_kernel share the row loads.
+template <int NB>
+__global__ __launch_bounds__(kRThreads) void router_split_kernel(
+    const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
+    uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
+    float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
+    uint32_t* __restrict__ err) {
+    extern __shared__ float xs[];  // x in the padded pair layout: (hidden / 64) * kPadX floats
+    __shared__ double red[8];
+    const uint32_t t = blockIdx.y;
+    const uint32_t e = blockIdx.x;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float* xt = x + static_cast<size_t>(t) * hidden;
+    uint64_t* ws_logit = ws + static_cast<size_t>(t) * 2 * kMaxExperts;
+    uint64_t* ws_bound = ws_logit + kMaxExperts;
+    const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    const uint32_t n4 = hidden >> 10;  // float4 per lane
+    float4 wr[NB];
+    {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const gptr<f32x4> r4 = as_global(reinterpret_cast<const f32x4*>(w_r + static_cast<size_t>(e) * hidden));
+        const uint32_t q0 = wave * n4 * 64u + lane * n4;
+#pragma unroll
+        for (int g = 0; g < NB; ++g) {
+            const f32x4 v = r4[q0 + (static_cast<uint32_t>(g) < n4 ? static_cast<uint32_t>(g) : n4 - 1)];
+            wr[g] = make_float4(v.x, v.y, v.z, v.w);
+        }
+    }
+    for (uint32_t i = threadIdx.x; i < (hidden >> 2); i += kRThreads) {
+        const uint32_t c = i << 2;
+        *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = reinterpret_cast<const float4*>(xt)[i];
+    }
+    __syncthreads();
+    double total, abs_bound;
+    exact_logit_split<NB>(wr, xs, n4, lane, wave, red, total, abs_bound);
+    if (threadIdx.x == 0) {
+        float lhat, bnd;
+        finish_logit(total, abs_bound, bias, e, hidden, lhat, bnd);
+        __hip_atomic_store(&ws_logit[e], tag(lhat, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ws_bound[e], tag(bnd, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (blockIdx.x != 0) return;
+    const uint32_t x_floats = (hidden / 64) * kPadX;
+    const float* xl = xs;
+    router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,
+                  renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit,
+                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch);
+}
+
 }  // namespace
 
 int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, const float* bias,
@@ -177,7 +229,19 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
     const bool vec = hidden % 4 == 0 && reinterpret_cast<uintptr_t>(w_r) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     uint32_t* err = ctx->counters + ctx->counter_words;
     const bool lanes = vec && hidden % 256 == 0 && hidden <= 256u * 32u;
-    if (lanes) {
+    const bool split = vec && hidden % 1024 == 0 && hidden <= 1024u * 8u;
+    if (split) {
+        const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
+        const dim3 sgrid(static_cast<uint32_t>(n_experts), static_cast<uint32_t>(n_tokens));
+        if (hidden <= 1024u * 2u)
+            hipLaunchKernelGGL(router_split_kernel<2>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
+                               static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+        else
+            hipLaunchKernelGGL(router_split_kernel<8>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
+                               static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+    } else if (lanes) {
         const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
         if (hidden <= 256u * 8u)
             hipLaunchKernelGGL(router_lanes_kernel<8>, grid, dim3(kRThreads), lds, s, w_r, bias, x,
