@@ -147,6 +147,48 @@ __device__ __forceinline__ void stage_x(float* __restrict__ lds, const float* __
     }
 }
 
+// Staging in two steps around the weight loads. Vector-memory loads complete in
+// issue order, so a wait for activations requested after the weights also waits
+// for the weights; requesting the activations first (stage_x_issue), then the
+// weights, then writing the activations to LDS (stage_x_commit) waits for the
+// activations only. Thread t holds float4s t, t + 256, ... of the NT vectors
+// (NV per thread: NT * cols <= 1024 * NV).
+template <int NV>
+struct XRegs {
+    float4 v[NV];
+};
+
+template <int NT, int NV>
+__device__ __forceinline__ void stage_x_issue(const float* __restrict__ x, uint32_t cols, XRegs<NV>& r) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const uint32_t n4 = NT * cols / 4;
+    const gptr<f32x4> src = as_global(reinterpret_cast<const f32x4*>(x));
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = threadIdx.x + static_cast<uint32_t>(j) * kThreads;
+        if (i < n4) {
+            const f32x4 v = src[i];
+            r.v[j] = make_float4(v.x, v.y, v.z, v.w);
+        }
+    }
+}
+
+template <int NT, int NV>
+__device__ __forceinline__ void stage_x_commit(float* __restrict__ lds, uint32_t cols, uint32_t pairs,
+                                               const XRegs<NV>& r) {
+    const uint32_t n4 = NT * cols / 4;
+    const uint32_t per_tok4 = cols / 4;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = threadIdx.x + static_cast<uint32_t>(j) * kThreads;
+        if (i < n4) {
+            const uint32_t t = i / per_tok4;
+            const uint32_t c = (i - t * per_tok4) * 4;
+            *reinterpret_cast<float4*>(lds + (t * pairs + (c >> 6)) * kPad + (c & 63)) = r.v[j];
+        }
+    }
+}
+
 // Segmented sum over the lpr lanes of a row; the total lands in the row's first lane.
 __device__ __forceinline__ float row_reduce(float v, uint32_t lp, uint32_t lpr) {
 #pragma unroll

@@ -74,6 +74,12 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     const uint32_t a = blockIdx.x / blocks_per_assign;
     const uint32_t rb = blockIdx.x - a * blocks_per_assign;
     const uint32_t t = a / k;
+    // the activations are requested before the expert id is known and before the
+    // weights, so that writing them to LDS waits for them alone
+    constexpr int kXV = 8;
+    const bool x_regs = hidden <= 4u * kXV * kThreads;
+    XRegs<kXV> xr;
+    if (x_regs) stage_x_issue<1, kXV>(x + static_cast<size_t>(t) * hidden, hidden, xr);
     uint32_t e;
     const bool ok = expert_of(ids, a, n_table, err, e);
     const objeta_hip_expert_ptrs P = table[e];
@@ -97,7 +103,8 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
             um.load(rc, p, du[u][c]);
         }
     }
-    stage_x<1>(lds, x + static_cast<size_t>(t) * hidden, hidden, pairs);
+    if (x_regs) stage_x_commit<1, kXV>(lds, hidden, pairs, xr);
+    else stage_x<1>(lds, x + static_cast<size_t>(t) * hidden, hidden, pairs);
     __syncthreads();
 
     // with one pair per lane, the lane's 64 activations are read from LDS once and
@@ -145,24 +152,56 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
     const uint32_t t = blockIdx.x / blocks_per_token;
     const uint32_t rb = blockIdx.x - t * blocks_per_token;
     const uint32_t pairs = inter >> 6;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // wave-uniform, so the expert id and table entry come through scalar loads,
+    // which do not wait behind the vector loads of the activations
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t gs = 64 / lpr, slot = lane / lpr, lp = lane - slot * lpr;
     const uint32_t rows_blk = gs * U;
     const uint32_t row0 = rb * rows_blk;
     float* red = lds;
     float* xst = lds + ((k * rows_blk + 3u) & ~3u) + wave * JW * pairs * kPad;
 
+    // the wave's activation slots are requested before the weights (loads complete
+    // in order, so the LDS writes below then wait for the activations alone): lane l
+    // holds float4s l, l + 64, ... of each of its JW slots
+    constexpr int kAV = 8 / JW;
+    const uint32_t n4a = inter >> 2;
+    const bool a_regs = n4a <= 64u * kAV;
+    float4 av[JW][kAV];
+    if (a_regs) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int jj = 0; jj < JW; ++jj) {
+            const uint32_t j = wave * JW + jj;
+            const uint32_t jc = j < k ? j : k - 1;
+            const gptr<f32x4> src = as_global(reinterpret_cast<const f32x4*>(act + (static_cast<size_t>(t) * k + jc) * inter));
+#pragma unroll
+            for (int q = 0; q < kAV; ++q) {
+                const uint32_t i = lane + static_cast<uint32_t>(q) * 64;
+                if (i < n4a) {
+                    const f32x4 v = src[i];
+                    av[jj][q] = make_float4(v.x, v.y, v.z, v.w);
+                }
+            }
+        }
+    }
     R m[JW];
     bool ok[JW];
     uint32_t d[JW][U][CH][R::kDw];
+    // every slot's id, then every slot's table entry, then the weights: one scalar
+    // round trip per step rather than per slot
+    uint32_t es[JW];
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
         const uint32_t j = wave * JW + jj;
         const uint32_t jc = j < k ? j : k - 1;
-        uint32_t e;
-        ok[jj] = expert_of(ids, t * k + jc, n_table, err, e);
-        const objeta_hip_expert_ptrs P = table[e];
-        m[jj] = RowsOf<R>::make(P.down, P.down_scale, inter);
+        ok[jj] = expert_of(ids, t * k + jc, n_table, err, es[jj]);
+        es[jj] = __builtin_amdgcn_readfirstlane(es[jj]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) m[jj] = RowsOf<R>::make(table[es[jj]].down, table[es[jj]].down_scale, inter);
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t r = row0 + static_cast<uint32_t>(u) * gs + slot;
@@ -173,9 +212,20 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
     }
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
-        const uint32_t j = wave * JW + jj;
-        const uint32_t jc = j < k ? j : k - 1;
-        stage_vec_wave(xst + jj * pairs * kPad, act + (static_cast<size_t>(t) * k + jc) * inter, inter, lane);
+        if (a_regs) {
+#pragma unroll
+            for (int q = 0; q < kAV; ++q) {
+                const uint32_t i = lane + static_cast<uint32_t>(q) * 64;
+                if (i < n4a) {
+                    const uint32_t c = i << 2;
+                    *reinterpret_cast<float4*>(xst + jj * pairs * kPad + (c >> 6) * kPad + (c & 63)) = av[jj][q];
+                }
+            }
+        } else {
+            const uint32_t j = wave * JW + jj;
+            const uint32_t jc = j < k ? j : k - 1;
+            stage_vec_wave(xst + jj * pairs * kPad, act + (static_cast<size_t>(t) * k + jc) * inter, inter, lane);
+        }
     }
     __syncthreads();
 
