@@ -47,24 +47,26 @@ __device__ __forceinline__ gptr<T> as_global(const T* p) {
     return (gptr<T>)(p);
 }
 
-// Loads N dwords starting at a 4-byte aligned address. Weight bytes are read
-// exactly once per launch, so the loads are non-temporal (they bypass cache
-// retention and leave L2/MALL to the activations).
+// Loads N dwords starting at a 4-byte aligned address. Lanes of a wave read
+// consecutive 36/44/28-byte pairs, so every cache line is touched by each of the
+// (up to three) load instructions of a pair: ordinary cached loads let the CU's L1
+// serve the second and third touch, where non-temporal loads sent each of them on
+// to the L2 (measured on MI355X: the Qwen3-A3B gate/up kernel 7.1 -> 6.3 us).
 template <int N>
 __device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint32_t (&d)[N]) {
     const gptr<uint32_t> g = as_global(p);
     int i = 0;
 #pragma unroll
     for (; i + 4 <= N; i += 4) {
-        u32x4 v = __builtin_nontemporal_load((gptr<u32x4>)(g + i));
+        const u32x4 v = *(gptr<u32x4>)(g + i);
         d[i] = v.x; d[i + 1] = v.y; d[i + 2] = v.z; d[i + 3] = v.w;
     }
     if constexpr (N % 4 >= 2) {
-        u32x2 v = __builtin_nontemporal_load((gptr<u32x2>)(g + i));
+        const u32x2 v = *(gptr<u32x2>)(g + i);
         d[i] = v.x; d[i + 1] = v.y;
         i += 2;
     }
-    if constexpr (N % 2 == 1) d[i] = __builtin_nontemporal_load(g + i);
+    if constexpr (N % 2 == 1) d[i] = g[i];
 }
 
 // ---------------------------------------------------------------- Q4_0

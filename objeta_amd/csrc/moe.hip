@@ -74,14 +74,15 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     const uint32_t a = blockIdx.x / blocks_per_assign;
     const uint32_t rb = blockIdx.x - a * blocks_per_assign;
     const uint32_t t = a / k;
-    // the activations are requested before the expert id is known and before the
-    // weights, so that writing them to LDS waits for them alone
+    // The expert id and table entry come through scalar loads, issued first; the
+    // activations are requested while they are in flight and before the weights,
+    // so that writing them to LDS waits for them alone.
+    uint32_t e;
+    const bool ok = expert_of(ids, a, n_table, err, e);
     constexpr int kXV = 8;
     const bool x_regs = hidden <= 4u * kXV * kThreads;
     XRegs<kXV> xr;
     if (x_regs) stage_x_issue<1, kXV>(x + static_cast<size_t>(t) * hidden, hidden, xr);
-    uint32_t e;
-    const bool ok = expert_of(ids, a, n_table, err, e);
     const objeta_hip_expert_ptrs P = table[e];
     const R gm = RowsOf<R>::make(P.gate, P.gate_scale, hidden);
     const R um = RowsOf<R>::make(P.up, P.up_scale, hidden);
