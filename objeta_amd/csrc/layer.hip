@@ -164,7 +164,8 @@ __device__ void select_xcd(const LayerParams& a, LayerLds& S, const float* xs, f
         auto xat = [xs](uint32_t h) { return xs[(h >> 6) * kPad + (h & 63)]; };
         const bool settled = select_refine(S.sel, a.w_r, a.bias, xat, E, a.H, kLK, a.renormalize, scratch, kRefineFloats);
         if (settler) {
-            if (!settled) select_sequential(S.sel, a.w_r, a.bias, xat, E, a.H, kLK);
+            if (!settled && !select_underflow(S.sel, a.w_r, a.bias, xat, E, a.H, kLK, scratch, kRefineFloats))
+                select_sequential(S.sel, a.w_r, a.bias, xat, E, a.H, kLK);
             __syncthreads();
             if (threadIdx.x < static_cast<uint32_t>(kLK)) {
                 store_l2(sb + threadIdx.x, __builtin_bit_cast(float, static_cast<uint32_t>(S.sel.sel[threadIdx.x])),

@@ -60,7 +60,8 @@ __device__ void router_select(const float* __restrict__ w_r, const float* __rest
         __builtin_amdgcn_s_sleep(1);
     }
     if (!select_certain(s, n_experts, k, renormalize) &&
-        !select_refine(s, w_r, bias, xat, n_experts, hidden, k, renormalize, scratch, scratch_floats))
+        !select_refine(s, w_r, bias, xat, n_experts, hidden, k, renormalize, scratch, scratch_floats) &&
+        !select_underflow(s, w_r, bias, xat, n_experts, hidden, k, scratch, scratch_floats))
         select_sequential(s, w_r, bias, xat, n_experts, hidden, k);
     write_selection(s, k, renormalize, ids, weights);
     if (threadIdx.x == 0) __hip_atomic_store(counter, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

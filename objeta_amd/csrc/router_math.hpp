@@ -496,14 +496,86 @@ __device__ bool select_certain(SelectLds<MAXE>& s, uint32_t n, uint32_t k, int r
     return true;
 }
 
+// Recomputes the logits of experts s.nlist[0..cnt) in the reference's order (each
+// product rounded, then added in sequence, then the bias) into s.val, with bound 0.
+// A sequential sum is one long dependency chain, so the candidates' chains run side
+// by side: lane j of wave 0 adds candidate j's products while waves 1..3 stream the
+// rows in chunks of C elements (coalesced loads), round the products and store them
+// in LDS, one chunk ahead (double buffer; a candidate's chunk is C floats at stride
+// C + 4, so the wave's 16-byte reads of 16 consecutive lanes hit distinct banks).
+// Up to 64 candidates per pass, fewer when the scratch (>= 40 floats) is small.
+// Block-wide; 256 threads.
+template <int MAXE, class XAt>
+__device__ void refine_rows(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
+                            XAt xat, uint32_t hidden, int cnt, float* scratch, uint32_t scratch_floats) {
+    // every product and every add rounds on its own, as in the reference, also in
+    // translation units built with contraction on: the operators are written in this
+    // scope (a multiply and an add inlined from __fmul_rn / __fadd_rn could fuse)
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t G = cnt < 64 ? static_cast<uint32_t>(cnt) : 64u;  // candidates per pass
+    if (G > scratch_floats / 40u) G = scratch_floats / 40u;
+    const uint32_t h16 = (hidden + 15u) & ~15u;
+    for (uint32_t g0 = 0; g0 < static_cast<uint32_t>(cnt); g0 += G) {
+        const uint32_t ng = static_cast<uint32_t>(cnt) - g0 < G ? static_cast<uint32_t>(cnt) - g0 : G;
+        uint32_t C = (scratch_floats / (2u * ng) - 4u) & ~15u;
+        if (C > h16) C = h16;
+        const uint32_t S = C + 4u;
+        const uint32_t nchunks = (hidden + C - 1u) / C;
+        // waves 1..3: rounded products of chunk c into buffer c & 1
+        auto fill = [&](uint32_t c) {
+            float* buf = scratch + (c & 1u) * ng * S;
+            const uint32_t c0 = c * C;
+            const uint32_t m = hidden - c0 < C ? hidden - c0 : C;
+#pragma unroll 4
+            for (uint32_t item = threadIdx.x - 64u; item < ng * C; item += kRThreads - 64u) {
+                const uint32_t r = item / C, i = item - r * C;
+                if (i < m) {
+                    const uint32_t e = static_cast<uint32_t>(s.nlist[g0 + r]);
+                    const float w = w_r[static_cast<size_t>(e) * hidden + c0 + i];
+                    const float p = w * xat(c0 + i);
+                    buf[r * S + i] = p;
+                }
+            }
+        };
+        if (wave != 0) fill(0);
+        __syncthreads();
+        float acc = 0.0f;
+        for (uint32_t c = 0; c < nchunks; ++c) {
+            if (wave != 0) {
+                if (c + 1u < nchunks) fill(c + 1u);
+            } else if (lane < ng) {
+                const float* row = scratch + (c & 1u) * ng * S + lane * S;
+                const uint32_t m = hidden - c * C < C ? hidden - c * C : C;
+                const uint32_t m4 = m & ~3u;
+                for (uint32_t i = 0; i < m4; i += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(row + i);
+                    acc = acc + v.x;
+                    acc = acc + v.y;
+                    acc = acc + v.z;
+                    acc = acc + v.w;
+                }
+                for (uint32_t i = m4; i < m; ++i) acc = acc + row[i];
+            }
+            __syncthreads();
+        }
+        if (wave == 0 && lane < ng) {
+            const uint32_t e = static_cast<uint32_t>(s.nlist[g0 + lane]);
+            if (bias) acc = acc + bias[e];
+            s.val[e] = acc;
+            s.bnd[e] = 0.0f;
+        }
+    }
+    __syncthreads();
+}
+
 // After select_certain failed: recomputes, in the reference's sequential order,
 // only the logits of experts involved in an undecided comparison (a selected
 // expert whose interval val +- (bnd + margin) overlaps another expert's), sets
 // their bounds to zero and decides again. Usually a handful of experts instead of
-// all n. Wave w takes needed experts w, w+4, ...: the expert's row streams through
-// the wave's share of `scratch` (LDS) in coalesced chunks and lane 0 adds the
-// products in order. Returns false when the selection is still not certain (or
-// too many experts are involved); the caller then runs select_sequential. xat(h)
+// all n, recomputed side by side by refine_rows through `scratch` (LDS). Returns
+// false when the selection is still not certain (or too many experts are
+// involved); the caller then runs select_underflow or select_sequential. xat(h)
 // returns x[h] (best from LDS). Block-wide; 256 threads.
 constexpr int kMaxRefine = 64;
 template <int MAXE, class XAt>
@@ -534,48 +606,8 @@ __device__ __noinline__ bool select_refine(SelectLds<MAXE>& s, const float* __re
     }
     __syncthreads();
     const int cnt = s.ncount;
-    const uint32_t chunk = (scratch_floats / kRWaves) & ~255u;
-    if (cnt == 0 || cnt > kMaxRefine || chunk == 0) return false;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* buf = scratch + wave * chunk;
-    for (int q = static_cast<int>(wave); q < cnt; q += kRWaves) {
-        const uint32_t e = static_cast<uint32_t>(s.nlist[q]);
-        const float* row = w_r + static_cast<size_t>(e) * hidden;
-        float acc = 0.0f;
-        for (uint32_t c0 = 0; c0 < hidden; c0 += chunk) {
-            const uint32_t m = hidden - c0 < chunk ? hidden - c0 : chunk;
-            // the whole chunk is requested before any of it is stored
-            for (uint32_t i0 = 0; i0 < m; i0 += 8 * 64) {
-                float v[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const uint32_t i = i0 + static_cast<uint32_t>(u) * 64 + lane;
-                    v[u] = row[c0 + (i < m ? i : m - 1)];
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const uint32_t i = i0 + static_cast<uint32_t>(u) * 64 + lane;
-                    if (i < m) buf[i] = v[u];
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (lane == 0) {
-#pragma unroll 16
-                for (uint32_t i = 0; i < m; ++i) acc = __fadd_rn(acc, __fmul_rn(buf[i], xat(c0 + i)));
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        }
-        if (lane == 0) {
-            if (bias) acc = __fadd_rn(acc, bias[e]);
-            s.val[e] = acc;
-            s.bnd[e] = 0.0f;
-        }
-    }
-    __syncthreads();
+    if (cnt == 0 || cnt > kMaxRefine || scratch_floats < 40u) return false;
+    refine_rows(s, w_r, bias, xat, hidden, cnt, scratch, scratch_floats);
     return select_certain(s, n, k, renormalize);
 }
 
@@ -585,23 +617,13 @@ __device__ __noinline__ bool select_refine(SelectLds<MAXE>& s, const float* __re
 // in double and rounded once, which agrees with glibc's expf on all but ~0.03% of
 // arguments (only a probability tie could expose that). Fills s.sel and s.e (the
 // probabilities). xat(h) returns x[h]. Block-wide; 256 threads.
-template <int MAXE, class XAt>
-__device__ __noinline__ void select_sequential(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
-                                  XAt xat, uint32_t n, uint32_t hidden, uint32_t k) {
+// With s.val holding the logits the reference computes (or -inf where its exp
+// is exactly 0): the reference's softmax in fp32 (exp through double, the sum in
+// expert order, one division each) and its stable descending sort of the
+// probabilities; the top k ids go to s.sel, their probabilities to s.e. Block-wide.
+template <int MAXE>
+__device__ void softmax_rank(SelectLds<MAXE>& s, uint32_t n, uint32_t k) {
     __shared__ float s_sum_exp;
-    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
-        // every product and every add rounds on its own, as in the reference
-#pragma clang fp contract(off)
-        const float* row = w_r + static_cast<size_t>(j) * hidden;
-        float sacc = 0.0f;
-        for (uint32_t h = 0; h < hidden; ++h) {
-            const float p = row[h] * xat(h);
-            sacc = sacc + p;
-        }
-        if (bias) sacc = sacc + bias[j];
-        s.val[j] = sacc;
-    }
-    __syncthreads();
     float mx = -INFINITY;
     for (uint32_t j = threadIdx.x; j < n; j += kRThreads) mx = fmaxf(mx, s.val[j]);
     mx = block_max(mx, s.red);
@@ -623,6 +645,63 @@ __device__ __noinline__ void select_sequential(SelectLds<MAXE>& s, const float* 
     __syncthreads();
     if (threadIdx.x < k) s.e[threadIdx.x] = s.bnd[s.sel[threadIdx.x]];
     __syncthreads();
+}
+
+template <int MAXE, class XAt>
+__device__ __noinline__ void select_sequential(SelectLds<MAXE>& s, const float* __restrict__ w_r, const float* __restrict__ bias,
+                                  XAt xat, uint32_t n, uint32_t hidden, uint32_t k) {
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
+        // every product and every add rounds on its own, as in the reference
+#pragma clang fp contract(off)
+        const float* row = w_r + static_cast<size_t>(j) * hidden;
+        float sacc = 0.0f;
+        for (uint32_t h = 0; h < hidden; ++h) {
+            const float p = row[h] * xat(h);
+            sacc = sacc + p;
+        }
+        if (bias) sacc = sacc + bias[j];
+        s.val[j] = sacc;
+    }
+    __syncthreads();
+    softmax_rank(s, n, k);
+}
+
+// When the softmax cannot be ranked on logits alone (some selected probability may
+// be subnormal or zero, where the reference's stable sort breaks equal
+// probabilities by index): an expert whose logit upper bound lies more than 110
+// below the lower bound of the largest logit has exp(l - max) < 2^-158 in double,
+// which is 0 in fp32 in the reference too. Only the others need their logits in the
+// reference's order; the rest enter the softmax as -inf (exactly 0). Returns false
+// (nothing changed) when more than kMaxRefine experts remain.
+template <int MAXE, class XAt>
+__device__ __noinline__ bool select_underflow(SelectLds<MAXE>& s, const float* __restrict__ w_r,
+                                              const float* __restrict__ bias, XAt xat, uint32_t n, uint32_t hidden,
+                                              uint32_t k, float* scratch, uint32_t scratch_floats) {
+    float lo = -INFINITY;
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) lo = fmaxf(lo, s.val[j] - s.bnd[j]);
+    lo = block_max(lo, s.red);
+    if (threadIdx.x == 0) s.ncount = 0;
+    __syncthreads();
+    const float cut = lo - 110.0f;
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) {
+        if (s.val[j] + s.bnd[j] >= cut || !(s.val[j] == s.val[j])) {
+            const int slot = atomicAdd(&s.ncount, 1);
+            if (slot < kMaxRefine) s.nlist[slot] = static_cast<int>(j);
+        }
+    }
+    __syncthreads();
+    const int cnt = s.ncount;
+    if (cnt == 0 || cnt > kMaxRefine || scratch_floats < 40u || !(cut > -INFINITY)) return false;
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads) s.need[j] = 0;
+    __syncthreads();
+    for (int q = static_cast<int>(threadIdx.x); q < cnt; q += kRThreads) s.need[s.nlist[q]] = 1;
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < n; j += kRThreads)
+        if (!s.need[j]) s.val[j] = -INFINITY;
+    __syncthreads();
+    refine_rows(s, w_r, bias, xat, hidden, cnt, scratch, scratch_floats);
+    softmax_rank(s, n, k);
+    return true;
 }
 
 // The k selected weights in selection order: renormalised (p / sum of the selected

@@ -207,7 +207,8 @@ __device__ void gemv_role(const StackParams& a, StackLds& S, float* xs, float* a
         uint64_t* sw = a.sbuf + static_cast<size_t>(l) * 2 * K;
         if (!certain) {
             if (publisher) {
-                select_sequential(S.sel, ly.w_r, ly.bias, xat, E, H, K);
+                if (!select_underflow(S.sel, ly.w_r, ly.bias, xat, E, H, K, as, K * pairs_i * kPad))
+                    select_sequential(S.sel, ly.w_r, ly.bias, xat, E, H, K);
                 if (threadIdx.x < K) {
                     store_word(sw + threadIdx.x, __builtin_bit_cast(float, static_cast<uint32_t>(S.sel.sel[threadIdx.x])),
                                epoch);
