@@ -36,7 +36,7 @@
 //
 // Close calls in the selection: gate/up workgroups settle them with select_refine
 // (x is in their LDS); what that cannot settle, workgroup li == 0 of the XCD settles
-// with select_sequential. Whenever the fast check fails that workgroup stores the
+// with select_underflow or select_sequential. Whenever the fast check fails that workgroup stores the
 // selection it arrived at for its XCD, and the down workgroups wait for it rather
 // than read x, which other down workgroups may already be overwriting when out
 // aliases x.
