@@ -134,17 +134,18 @@ __device__ __forceinline__ void reduce_groups(float (&v)[N], uint32_t lpr) {
 }
 
 // ------------------------------------------------- hand-offs inside one XCD
-// Producer and consumers on the same XCD share its L2. A producer writes a word
-// with a plain store (the CU's L1 writes through to the L2); a consumer
-// invalidates its CU's L1 and loads from the L2. No request leaves the XCD, so a
-// hand-off costs an L2 round trip instead of a trip to memory, and hundreds of
-// pollers do not queue at one memory channel.
+// Words exchanged among the workgroups of one XCD (the producers and consumers of
+// a word share an XCD, so its pollers come from 32 CUs, not from the whole
+// device). Both sides use relaxed agent-scope atomics, like the cross-XCD words:
+// a workgroup-scope load may be served by the CU's L1 and never see the update.
+// Atomics (not volatile accesses, which the compiler serialises, waiting for each
+// to complete) let a thread keep a batch of loads in flight.
 __device__ __forceinline__ void l1_invalidate() { asm volatile("buffer_inv sc0" ::: "memory"); }
 __device__ __forceinline__ uint64_t load_l2(const uint64_t* p) {
-    return *(volatile const __attribute__((address_space(1))) uint64_t*)(p);
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void store_l2(uint64_t* p, float v, uint32_t epoch) {
-    *(volatile __attribute__((address_space(1))) uint64_t*)(p) = tag(v, epoch);
+    __hip_atomic_store(p, tag(v, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Block-wide gather of n words written on this XCD that must carry `epoch`;

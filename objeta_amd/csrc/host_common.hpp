@@ -78,7 +78,8 @@ enum WsSlot : int {
     kWsMoeOut = 3,
     kWsGrouped = 4,
     kWsFused = 5,
-    kWsSlots = 6
+    kWsExperts = 6,
+    kWsSlots = 7
 };
 
 }  // namespace objeta
@@ -101,6 +102,10 @@ struct objeta_hip_context {
     // workgroup b runs on XCD b % 8 of an 8-XCD device (probed once): -1 unknown,
     // 0 no, 1 yes
     int xcd_round_robin = -1;
+    // batch-1 layers run their experts in one XCD-aligned launch when the shape
+    // allows and OBJETA_HIP_EXPERTS_XCD=1 was set at context creation (off by
+    // default: on MI355X it is slower than the gate/up and down kernels today)
+    bool experts_xcd = false;
     std::mutex mu;
 };
 

@@ -54,4 +54,17 @@ int32_t launch_moe_layer_fused(objeta_hip_context* ctx, int32_t format, hipStrea
                                float* out, uint32_t* ids_out, float* weights_out, uint64_t hidden, uint64_t inter,
                                float limit);
 
+// The selected experts of one token (k == 8 ids and weights already on the device)
+// as one launch laid out over the XCDs: gate/up + SiLU and down + combine, the
+// down rows streaming with the gate/up rows. Same limits and probe as the fused
+// layer. Each launch must follow a router launch on the same context (the router's
+// token-0 counter is its epoch).
+bool experts_xcd_supported(objeta_hip_context* ctx, hipStream_t s, int32_t format, uint64_t n_experts, uint64_t k,
+                           uint64_t hidden, uint64_t inter, uint64_t out_dim);
+
+int32_t launch_moe_experts_xcd(objeta_hip_context* ctx, int32_t format, hipStream_t s,
+                               const objeta_hip_expert_ptrs* table, uint64_t n_experts, const uint32_t* ids,
+                               const float* wts, const float* x, const float* resid, float* out, uint64_t hidden,
+                               uint64_t inter, float limit);
+
 }  // namespace objeta

@@ -670,6 +670,11 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
         reinterpret_cast<uintptr_t>(d_x) % 16 == 0)
         return launch_moe_grouped(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, n_tokens, k, d_x,
                                   d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit);
+    // one token, top-8: gate/up and down in one launch over the XCDs
+    if (n_tokens == 1 && ctx->experts_xcd && reinterpret_cast<uintptr_t>(d_x) % 16 == 0 &&
+        experts_xcd_supported(ctx, s, format, n_experts, k, hidden, intermediate, out_dim))
+        return launch_moe_experts_xcd(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, d_x, d_residual,
+                                      d_out, hidden, intermediate, swiglu_limit);
     float* act = nullptr;
     OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k, intermediate ? intermediate : 1, &act));
     return launch_moe_selected(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, n_tokens, k, d_x,

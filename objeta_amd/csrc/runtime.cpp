@@ -1,6 +1,7 @@
 // runtime.cpp — device discovery, context, streams, memory, events and graph
 // capture behind the C ABI. Mirrors the reference's L1 device runtime
 // (crates/objeta-cuda/src/{context,stream,memory,telemetry,lib}.rs).
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -69,7 +70,11 @@ int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, int slot, 
     size_t grow = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
     void* p = nullptr;
     OBJ_HIP(hipMalloc(&p, grow), "allocate workspace");
-    OBJ_HIP(hipMemset(p, 0, grow), "clear workspace");
+    // cleared on the caller's stream and waited for: a clear on the null stream is
+    // not ordered before kernels on the context's non-blocking streams, and the
+    // epoch-tagged words and counters in a workspace must start at zero
+    OBJ_HIP(hipMemsetAsync(p, 0, grow, stream), "clear workspace");
+    OBJ_HIP(hipStreamSynchronize(stream), "clear workspace");
     if (ws.ptr) ctx->retired_ws.push_back(ws.ptr);
     ws.ptr = p;
     ws.bytes = grow;
@@ -201,6 +206,7 @@ int32_t objeta_hip_init(const objeta_hip_init_options* opts, objeta_hip_context*
     auto* ctx = new objeta_hip_context();
     ctx->device = static_cast<int>(o.device_ordinal);
     ctx->info = info;
+    if (const char* v = std::getenv("OBJETA_HIP_EXPERTS_XCD")) ctx->experts_xcd = std::strcmp(v, "1") == 0;
     auto fail_cleanup = [&](int32_t rc) {
         objeta_hip_destroy(ctx);
         return rc;

@@ -523,7 +523,8 @@ int32_t objeta_hip_moe_stack_run(objeta_hip_moe_stack* st, objeta_hip_stream str
         OBJ_HIP(hipStreamSynchronize(s), "synchronize before epoch reset");
         char* base = static_cast<char*>(st->dev);
         const size_t desc_b = (static_cast<size_t>(st->p.L) * sizeof(StackLayerDev) + 255) & ~size_t(255);
-        OBJ_HIP(hipMemset(base + desc_b, 0, st->dev_bytes - desc_b), "clear decode-stack words");
+        // on the run's stream, so the clear is ordered before the launch below
+        OBJ_HIP(hipMemsetAsync(base + desc_b, 0, st->dev_bytes - desc_b, s), "clear decode-stack words");
         st->next_epoch = 1;
     }
     StackParams p = st->p;
