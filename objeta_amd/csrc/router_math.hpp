@@ -25,20 +25,48 @@ constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kChunkBatch = 8;  // 256-element chunks loaded per batch (8 float4 per lane)
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Wave-wide double scans through DPP row shifts and lane reads, not shuffles: a
+// shuffle goes through the LDS crossbar (over 100 cycles a step, 12 dependent
+// steps per scan), a DPP move is an ordinary VALU operation.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {  // lanes without a source read 0
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), CTRL, 0xF, 0xF, true));
+    const uint32_t hi = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)), CTRL, 0xF, 0xF, true));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u)), l));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u >> 32)), l));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+// Inclusive scan within each row of 16 lanes (row_shr 1, 2, 4, 8).
+__device__ __forceinline__ double row_scan_d(double v) {
+    v += dpp_d<0x111>(v);
+    v += dpp_d<0x112>(v);
+    v += dpp_d<0x114>(v);
+    v += dpp_d<0x118>(v);
     return v;
 }
 
-// Inclusive scan over the wave (Hillis-Steele, in double).
+// Sum over the wave, in every lane.
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v = row_scan_d(v);
+    return ((readlane_d(v, 15) + readlane_d(v, 31)) + readlane_d(v, 47)) + readlane_d(v, 63);
+}
+
+// Inclusive scan over the wave (in double): rows of 16 lanes, then the totals of
+// the rows before.
 __device__ __forceinline__ double wave_scan_d(double v, int lane) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const double o = __shfl_up(v, off, 64);
-        if (lane >= off) v += o;
-    }
-    return v;
+    v = row_scan_d(v);
+    const double r0 = readlane_d(v, 15);
+    const double r01 = r0 + readlane_d(v, 31);
+    const double r012 = r01 + readlane_d(v, 47);
+    const int row = lane >> 4;
+    return row == 0 ? v : v + (row == 1 ? r0 : (row == 2 ? r01 : r012));
 }
 
 // The exact sum S of the rounded products fl(row[h] * x[h]) (accumulated in
@@ -112,7 +140,7 @@ __device__ __forceinline__ void exact_logit_scalar(const float* __restrict__ row
         run += static_cast<double>(__fmul_rn(row[h], xt[h]));
         absacc += fabs(run);
     }
-    total = __shfl(incl, 63, 64);
+    total = readlane_d(incl, 63);
     abs_prefix = wave_sum_d(absacc);
 }
 
@@ -339,8 +367,8 @@ __device__ __forceinline__ void exact_logit_lanes(const float4 (&w)[NB], const f
     }
     const double lane_sum = ((s[0] + s[1]) + s[2]) + s[3];
     const double incl = wave_scan_d(lane_sum, static_cast<int>(lane));
-    double t = __shfl_up(incl, 1, 64);
-    if (lane == 0) t = 0.0;
+    // the lanes before (within a double rounding, which the bound's margin covers)
+    double t = lane == 0 ? 0.0 : incl - lane_sum;
     double b = 0.0;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
@@ -349,7 +377,7 @@ __device__ __forceinline__ void exact_logit_lanes(const float4 (&w)[NB], const f
         b += static_cast<double>(4 * cnt) * fabs(t) + a[sb];
         t += s[sb];
     }
-    total = __shfl(incl, 63, 64);
+    total = readlane_d(incl, 63);
     abs_bound = wave_sum_d(b);
 }
 
@@ -383,8 +411,8 @@ __device__ __forceinline__ void exact_logit_split(const float4 (&w)[NB], const f
         }
     }
     const double incl = wave_scan_d(s, static_cast<int>(lane));
-    double t = __shfl_up(incl, 1, 64);
-    if (lane == 0) t = 0.0;
+    // the lanes before (within a double rounding, which the bound's margin covers)
+    const double t = lane == 0 ? 0.0 : incl - s;
     if (lane == 63) red[wave] = incl;
     __syncthreads();
     double tw = 0.0;
