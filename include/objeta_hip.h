@@ -298,9 +298,9 @@ int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, obje
 /* One MoE layer on the device: the router of objeta_hip_router_topk_device over
  * d_router_w [n_experts][hidden] (+ d_router_bias) writes d_ids_out/d_weights_out
  * [n_tokens][k], then objeta_hip_moe_selected_device runs the selected experts of
- * d_table (n_experts entries); batches of 4 or more tokens within the limits of
- * objeta_hip_moe_grouped_device run through it instead (each selected expert read
- * once for the batch). No host synchronisation; graph-capturable. No
+ * d_table (n_experts entries), for any number of tokens (the per-assignment
+ * kernels measure faster than objeta_hip_moe_grouped_device at 16, 32 and 64
+ * tokens on MI355X). No host synchronisation; graph-capturable. No
  * reference counterpart as one call: the reference routes on the host
  * (deepseek_single_layer_moe.rs:687-743) and then calls execute_selected_moe_cuda. */
 int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,

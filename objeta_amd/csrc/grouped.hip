@@ -467,13 +467,6 @@ hipError_t launch_grouped(hipStream_t s, const objeta_hip_expert_ptrs* table, Gr
 
 }  // namespace
 
-bool grouped_supported(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden, uint64_t inter,
-                       uint64_t out_dim) {
-    return n_table > 0 && n_table <= kGMaxTable && k > 0 && k <= 32 && n_tokens * k <= kGMaxAssign && hidden > 0 &&
-           inter > 0 && hidden % 64 == 0 && inter % 64 == 0 && hidden <= (1u << 20) && inter <= (1u << 20) &&
-           out_dim <= (1u << 20);
-}
-
 int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                            const float* x, const float* resid, float* out, uint64_t hidden, uint64_t inter,

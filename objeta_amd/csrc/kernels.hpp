@@ -30,12 +30,6 @@ int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, 
 int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
                         float** out);
 
-// Batches of at least this many tokens go through the grouped-token path in
-// objeta_hip_moe_layer_device.
-constexpr uint64_t kGroupedMinTokens = 4;
-bool grouped_supported(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden, uint64_t inter,
-                       uint64_t out_dim);
-
 int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                            const float* x, const float* resid, float* out, uint64_t hidden, uint64_t inter,

@@ -665,11 +665,6 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
     OBJ_TRY(objeta_hip_router_topk_device(ctx, s, d_router_w, d_router_bias, d_x, n_tokens, n_experts, hidden, k,
                                           renormalize, d_ids_out, d_weights_out));
     if (out_dim == 0) return 0;
-    // a batch whose tokens may share experts: each selected expert read once
-    if (n_tokens >= kGroupedMinTokens && grouped_supported(n_experts, n_tokens, k, hidden, intermediate, out_dim) &&
-        reinterpret_cast<uintptr_t>(d_x) % 16 == 0)
-        return launch_moe_grouped(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, n_tokens, k, d_x,
-                                  d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit);
     // one token, top-8: gate/up and down in one launch over the XCDs
     if (n_tokens == 1 && ctx->experts_xcd && reinterpret_cast<uintptr_t>(d_x) % 16 == 0 &&
         experts_xcd_supported(ctx, s, format, n_experts, k, hidden, intermediate, out_dim))

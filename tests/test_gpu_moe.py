@@ -210,8 +210,7 @@ def test_moe_bad_expert_id_sets_device_error(backend):
     (Q4, 2048, 768, 128, 8, 16, True), (FP4, 1024, 512, 16, 4, 6, False), (Q5, 512, 256, 24, 3, 8, True)])
 def test_moe_layer_router_then_experts(backend, fmt, hidden, inter, n, k, T, bias):
     """Router (softmax -> top-k -> renormalise) feeding the experts, one call. The
-    table's n entries cycle over a pool of at most 12 distinct experts. Batches of
-    4 or more tokens take the grouped-token path."""
+    table's n entries cycle over a pool of at most 12 distinct experts."""
     pool = make_experts(fmt, min(n, 12), hidden, inter, hidden, 21, gen="gauss")
     experts = [pool[i % len(pool)] for i in range(n)]
     table, keep = device_table(backend, fmt, experts)
