@@ -560,8 +560,14 @@ int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, 
     uint32_t* err = ctx->counters + ctx->counter_words;
     uint32_t jw = 0;
     if (fast_shape(sh.inter)) {
-        if (down_lds_bytes(sh, 2, 1) <= max_lds(ctx) && (sh.k + 1) / 2 <= 16) jw = 2;
-        else if (down_lds_bytes(sh, 1, 1) <= max_lds(ctx) && sh.k <= 16) jw = 1;
+        // one token: one selection slot per wave (k waves per workgroup), measured
+        // 0.2 us faster per Qwen3-A3B layer; batches: two slots per wave (16 tokens:
+        // 4.3 against 4.7 ms per 48-layer step)
+        const bool jw1 = down_lds_bytes(sh, 1, 1) <= max_lds(ctx) && sh.k <= 16;
+        const bool jw2 = down_lds_bytes(sh, 2, 1) <= max_lds(ctx) && (sh.k + 1) / 2 <= 16;
+        if (sh.n_tokens == 1 && jw1) jw = 1;
+        else if (jw2) jw = 2;
+        else if (jw1) jw = 1;
     }
     hipError_t e;
     if (jw) {
