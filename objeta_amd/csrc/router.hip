@@ -179,24 +179,24 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
     uint64_t* ws_bound = ws_logit + kMaxExperts;
     const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     const uint32_t n4 = hidden >> 10;  // float4 per lane
-    float4 wr[NB];
+    // the lane's row elements and the matching activations, straight into registers
+    float4 wr[NB], xv[NB];
     {
         typedef float f32x4 __attribute__((ext_vector_type(4)));
         const gptr<f32x4> r4 = as_global(reinterpret_cast<const f32x4*>(w_r + static_cast<size_t>(e) * hidden));
+        const gptr<f32x4> x4 = as_global(reinterpret_cast<const f32x4*>(xt));
         const uint32_t q0 = wave * n4 * 64u + lane * n4;
 #pragma unroll
         for (int g = 0; g < NB; ++g) {
-            const f32x4 v = r4[q0 + (static_cast<uint32_t>(g) < n4 ? static_cast<uint32_t>(g) : n4 - 1)];
+            const uint32_t q = q0 + (static_cast<uint32_t>(g) < n4 ? static_cast<uint32_t>(g) : n4 - 1);
+            const f32x4 v = r4[q];
             wr[g] = make_float4(v.x, v.y, v.z, v.w);
+            const f32x4 u = x4[q];
+            xv[g] = make_float4(u.x, u.y, u.z, u.w);
         }
     }
-    for (uint32_t i = threadIdx.x; i < (hidden >> 2); i += kRThreads) {
-        const uint32_t c = i << 2;
-        *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = reinterpret_cast<const float4*>(xt)[i];
-    }
-    __syncthreads();
     double total, abs_bound;
-    exact_logit_split<NB>(wr, xs, n4, lane, wave, red, total, abs_bound);
+    exact_logit_split<NB>(wr, xv, n4, lane, wave, red, total, abs_bound);
     if (threadIdx.x == 0) {
         float lhat, bnd;
         finish_logit(total, abs_bound, bias, e, hidden, lhat, bnd);
@@ -204,6 +204,13 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
         __hip_atomic_store(&ws_bound[e], tag(bnd, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (blockIdx.x != 0) return;
+    // workgroup 0 selects; x in LDS serves the recomputation of close calls (staged
+    // while the other workgroups still publish)
+    for (uint32_t i = threadIdx.x; i < (hidden >> 2); i += kRThreads) {
+        const uint32_t c = i << 2;
+        *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = reinterpret_cast<const float4*>(xt)[i];
+    }
+    __syncthreads();
     const uint32_t x_floats = (hidden / 64) * kPadX;
     const float* xl = xs;
     router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,

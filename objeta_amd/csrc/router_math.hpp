@@ -383,23 +383,22 @@ __device__ __forceinline__ void exact_logit_lanes(const float4 (&w)[NB], const f
 
 // exact_logit_lanes for a row split over the four waves of a workgroup: wave w owns
 // elements [w*H/4, (w+1)*H/4) and its lane l the 4*n4 elements from
-// w*H/4 + 4*n4*l, held as w[0..n4) (H = 1024*n4, n4 <= NB). Each lane runs one
+// w*H/4 + 4*n4*l, held as w[0..n4) with the matching activations in xv[0..n4)
+// (H = 1024*n4, n4 <= NB). Each lane runs one
 // chain of prefix sums s_i and sum |s_i|; a wave scan gives the lane's offset
 // inside its wave, the four wave totals meet in LDS (added in wave order), and a
 // lane at global offset T adds 4*n4*|T| + sum |s_i| to the bound. Block-wide: every
 // thread reaches both barriers. red: 8 doubles of LDS. total and abs_bound are
 // returned in every thread.
 template <int NB>
-__device__ __forceinline__ void exact_logit_split(const float4 (&w)[NB], const float* __restrict__ x_lds,
+__device__ __forceinline__ void exact_logit_split(const float4 (&w)[NB], const float4 (&xv)[NB],
                                                   uint32_t n4, uint32_t lane, uint32_t wave, double* red,
                                                   double& total, double& abs_bound) {
     double s = 0.0, a = 0.0;
-    const uint32_t base = wave * n4 * 256u + lane * n4 * 4u;
 #pragma unroll
     for (int g = 0; g < NB; ++g) {
         if (static_cast<uint32_t>(g) < n4) {
-            const uint32_t h = base + 4u * static_cast<uint32_t>(g);
-            const float4 v = *reinterpret_cast<const float4*>(x_lds + (h >> 6) * kPadX + (h & 63));
+            const float4 v = xv[g];
             s += static_cast<double>(__fmul_rn(w[g].x, v.x));
             a += fabs(s);
             s += static_cast<double>(__fmul_rn(w[g].y, v.y));
