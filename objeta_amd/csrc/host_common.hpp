@@ -79,7 +79,8 @@ enum WsSlot : int {
     kWsGrouped = 4,
     kWsFused = 5,
     kWsExperts = 6,
-    kWsSlots = 7
+    kWsSelTab = 7,
+    kWsSlots = 8
 };
 
 }  // namespace objeta

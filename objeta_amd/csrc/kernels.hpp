@@ -19,13 +19,29 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
 
 int32_t launch_zero(hipStream_t s, void* d, uint64_t bytes);
 
+// The router launch behind objeta_hip_router_topk_device (ws: kMaxExperts * 2 words
+// per token). With table and sel_tab given and *sel_tab non-null, the router also
+// writes the selected experts' table entries to (*sel_tab)[t * k + r] when it can
+// (up to kSelTabMaxExperts experts, hidden a multiple of 1024); *sel_tab is set to
+// nullptr when it does not.
+constexpr uint64_t kSelTabMaxExperts = 256;
+constexpr uint64_t kMaxRouterExperts = 1024;  // router workspace: 2 words per expert and token
+int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, const float* bias,
+                      const float* x, uint64_t n_tokens, uint64_t n_experts, uint64_t hidden, uint64_t k,
+                      int32_t renormalize, uint32_t* ids, float* weights, uint64_t* ws,
+                      const objeta_hip_expert_ptrs* table, objeta_hip_expert_ptrs** sel_tab);
+
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
-                           float* act, uint64_t hidden, uint64_t inter, float limit);
+                           float* act, uint64_t hidden, uint64_t inter, float limit,
+                           const objeta_hip_expert_ptrs* sel = nullptr);
 
+// sel (optional): the assignments' table entries as the router resolved them; the
+// kernels then skip the id and table lookups.
 int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                         uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
-                        const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim);
+                        const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim,
+                        const objeta_hip_expert_ptrs* sel = nullptr);
 
 int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
                         float** out);

@@ -69,7 +69,8 @@ template <class R, int U, int CH>
 __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
-    uint32_t lpr, uint32_t blocks_per_assign, float limit, uint32_t* __restrict__ err) {
+    uint32_t lpr, uint32_t blocks_per_assign, float limit, uint32_t* __restrict__ err,
+    const objeta_hip_expert_ptrs* __restrict__ sel) {
     extern __shared__ float lds[];
     const uint32_t a = blockIdx.x / blocks_per_assign;
     const uint32_t rb = blockIdx.x - a * blocks_per_assign;
@@ -77,13 +78,14 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     // The expert id and table entry come through scalar loads, issued first; the
     // activations are requested while they are in flight and before the weights,
     // so that writing them to LDS waits for them alone.
-    uint32_t e;
-    const bool ok = expert_of(ids, a, n_table, err, e);
+    // sel: the router resolved the assignments to table entries (valid ids)
+    uint32_t e = 0;
+    const bool ok = sel ? true : expert_of(ids, a, n_table, err, e);
     constexpr int kXV = 8;
     const bool x_regs = hidden <= 4u * kXV * kThreads;
     XRegs<kXV> xr;
     if (x_regs) stage_x_issue<1, kXV>(x + static_cast<size_t>(t) * hidden, hidden, xr);
-    const objeta_hip_expert_ptrs P = table[e];
+    const objeta_hip_expert_ptrs P = sel ? sel[a] : table[e];
     const R gm = RowsOf<R>::make(P.gate, P.gate_scale, hidden);
     const R um = RowsOf<R>::make(P.up, P.up_scale, hidden);
 
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ wts, const float* __restrict__ act, const float* resid, float* out,
     uint32_t inter, uint32_t out_dim, uint32_t k, uint32_t lpr, uint32_t blocks_per_token,
-    uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ sel) {
     extern __shared__ float lds[];
     const uint32_t t = blockIdx.x / blocks_per_token;
     const uint32_t rb = blockIdx.x - t * blocks_per_token;
@@ -192,15 +194,25 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
     // every slot's id, then every slot's table entry, then the weights: one scalar
     // round trip per step rather than per slot
     uint32_t es[JW];
+    if (sel) {  // the router resolved the assignments to table entries (valid ids)
 #pragma unroll
-    for (int jj = 0; jj < JW; ++jj) {
-        const uint32_t j = wave * JW + jj;
-        const uint32_t jc = j < k ? j : k - 1;
-        ok[jj] = expert_of(ids, t * k + jc, n_table, err, es[jj]);
-        es[jj] = __builtin_amdgcn_readfirstlane(es[jj]);
+        for (int jj = 0; jj < JW; ++jj) {
+            const uint32_t j = wave * JW + jj;
+            const objeta_hip_expert_ptrs* f = sel + (t * k + (j < k ? j : k - 1));
+            ok[jj] = true;
+            m[jj] = RowsOf<R>::make(f->down, f->down_scale, inter);
+        }
+    } else {
+#pragma unroll
+        for (int jj = 0; jj < JW; ++jj) {
+            const uint32_t j = wave * JW + jj;
+            const uint32_t jc = j < k ? j : k - 1;
+            ok[jj] = expert_of(ids, t * k + jc, n_table, err, es[jj]);
+            es[jj] = __builtin_amdgcn_readfirstlane(es[jj]);
+        }
+#pragma unroll
+        for (int jj = 0; jj < JW; ++jj) m[jj] = RowsOf<R>::make(table[es[jj]].down, table[es[jj]].down_scale, inter);
     }
-#pragma unroll
-    for (int jj = 0; jj < JW; ++jj) m[jj] = RowsOf<R>::make(table[es[jj]].down, table[es[jj]].down_scale, inter);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
 #pragma unroll
@@ -385,21 +397,22 @@ size_t max_lds(const objeta_hip_context* ctx) {
 
 template <class R, int U, int CH>
 hipError_t gate_up_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids, const float* x,
-                        float* act, const MoeShape& sh, uint32_t lpr, float limit, uint32_t* err) {
+                        float* act, const MoeShape& sh, uint32_t lpr, float limit, uint32_t* err,
+                        const objeta_hip_expert_ptrs* sel) {
     const uint32_t gs = 64 / lpr;
     const uint32_t rows_blk = kWaves * gs * U;
     const uint32_t bpa = (sh.inter + rows_blk - 1) / rows_blk;
     const uint32_t n_assign = sh.n_tokens * sh.k;
     const size_t lds = static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 4 * sizeof(float);
     hipLaunchKernelGGL((moe_gate_up_kernel<R, U, CH>), dim3(n_assign * bpa), dim3(kThreads), lds, s, table,
-                       sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k, lpr, bpa, limit, err);
+                       sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k, lpr, bpa, limit, err, sel);
     return hipGetLastError();
 }
 
 template <class R, int U, int CH, int JW>
 hipError_t down_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids, const float* wts,
                      const float* act, const float* resid, float* out, const MoeShape& sh, uint32_t lpr,
-                     uint32_t* err) {
+                     uint32_t* err, const objeta_hip_expert_ptrs* sel) {
     const uint32_t gs = 64 / lpr;
     const uint32_t rows_blk = gs * U;
     const uint32_t bpt = (sh.out_dim + rows_blk - 1) / rows_blk;
@@ -407,7 +420,7 @@ hipError_t down_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, const u
     const size_t lds = (((sh.k * rows_blk + 3u) & ~3u) + static_cast<size_t>(waves) * JW * (sh.inter >> 6) * kPad) *
                        sizeof(float);
     hipLaunchKernelGGL((moe_down_kernel<R, U, CH, JW>), dim3(sh.n_tokens * bpt), dim3(waves * 64), lds, s, table,
-                       sh.n_table, ids, wts, act, resid, out, sh.inter, sh.out_dim, sh.k, lpr, bpt, err);
+                       sh.n_table, ids, wts, act, resid, out, sh.inter, sh.out_dim, sh.k, lpr, bpt, err, sel);
     return hipGetLastError();
 }
 
@@ -422,7 +435,7 @@ size_t down_lds_bytes(const MoeShape& sh, uint32_t jw, uint32_t u) {
 template <class R>
 hipError_t launch_gate_up_rows(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids,
                                const float* x, float* act, const MoeShape& sh, float limit, uint32_t* err,
-                               uint32_t cus) {
+                               uint32_t cus, const objeta_hip_expert_ptrs* sel) {
     const uint32_t pairs = sh.hidden >> 6;
     const uint32_t lpr = pick_lpr(pairs);
     const uint32_t ch = pairs / lpr;
@@ -431,35 +444,35 @@ hipError_t launch_gate_up_rows(hipStream_t s, const objeta_hip_expert_ptrs* tabl
     const uint64_t blocks_u2 = static_cast<uint64_t>(sh.n_tokens) * sh.k * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2));
     const bool u2 = blocks_u2 >= 2ull * cus && ch <= 2;
     switch (ch) {
-        case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err)
-                          : gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err);
-        case 2: return u2 ? gate_up_fast<R, 2, 2>(s, table, ids, x, act, sh, lpr, limit, err)
-                          : gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err);
-        case 3: return gate_up_fast<R, 1, 3>(s, table, ids, x, act, sh, lpr, limit, err);
-        default: return gate_up_fast<R, 1, 4>(s, table, ids, x, act, sh, lpr, limit, err);
+        case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel)
+                          : gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+        case 2: return u2 ? gate_up_fast<R, 2, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel)
+                          : gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+        case 3: return gate_up_fast<R, 1, 3>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+        default: return gate_up_fast<R, 1, 4>(s, table, ids, x, act, sh, lpr, limit, err, sel);
     }
 }
 
 template <class R>
 hipError_t launch_down_rows(hipStream_t s, const objeta_hip_expert_ptrs* table, const uint32_t* ids,
                             const float* wts, const float* act, const float* resid, float* out, const MoeShape& sh,
-                            uint32_t jw, uint32_t* err) {
+                            uint32_t jw, uint32_t* err, const objeta_hip_expert_ptrs* sel) {
     const uint32_t pairs = sh.inter >> 6;
     const uint32_t lpr = pick_lpr(pairs);
     const uint32_t ch = pairs / lpr;
     if (jw == 2) {
         switch (ch) {
-            case 1: return down_fast<R, 1, 1, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
-            case 2: return down_fast<R, 1, 2, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
-            case 3: return down_fast<R, 1, 3, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
-            default: return down_fast<R, 1, 4, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+            case 1: return down_fast<R, 1, 1, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+            case 2: return down_fast<R, 1, 2, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+            case 3: return down_fast<R, 1, 3, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+            default: return down_fast<R, 1, 4, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
         }
     }
     switch (ch) {
-        case 1: return down_fast<R, 1, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
-        case 2: return down_fast<R, 1, 2, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
-        case 3: return down_fast<R, 1, 3, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
-        default: return down_fast<R, 1, 4, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err);
+        case 1: return down_fast<R, 1, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+        case 2: return down_fast<R, 1, 2, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+        case 3: return down_fast<R, 1, 3, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+        default: return down_fast<R, 1, 4, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
     }
 }
 
@@ -518,7 +531,8 @@ MoeShape shape_of(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidd
 
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
-                           float* act, uint64_t hidden, uint64_t inter, float limit) {
+                           float* act, uint64_t hidden, uint64_t inter, float limit,
+                           const objeta_hip_expert_ptrs* sel) {
     const char* action = "launch MoE gate/up";
     OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, hidden, inter, 1));
     if (n_tokens == 0) return 0;
@@ -531,10 +545,10 @@ int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t 
     hipError_t e;
     if (fast) {
         switch (format) {
-            case OBJETA_HIP_Q4_0: e = launch_gate_up_rows<QRows<kQ4>>(s, table, ids, x, act, sh, limit, err, cus); break;
-            case OBJETA_HIP_Q5_0: e = launch_gate_up_rows<QRows<kQ5>>(s, table, ids, x, act, sh, limit, err, cus); break;
-            case OBJETA_HIP_IQ3_0: e = launch_gate_up_rows<QRows<kIQ3>>(s, table, ids, x, act, sh, limit, err, cus); break;
-            default: e = launch_gate_up_rows<Fp4Rows>(s, table, ids, x, act, sh, limit, err, cus); break;
+            case OBJETA_HIP_Q4_0: e = launch_gate_up_rows<QRows<kQ4>>(s, table, ids, x, act, sh, limit, err, cus, sel); break;
+            case OBJETA_HIP_Q5_0: e = launch_gate_up_rows<QRows<kQ5>>(s, table, ids, x, act, sh, limit, err, cus, sel); break;
+            case OBJETA_HIP_IQ3_0: e = launch_gate_up_rows<QRows<kIQ3>>(s, table, ids, x, act, sh, limit, err, cus, sel); break;
+            default: e = launch_gate_up_rows<Fp4Rows>(s, table, ids, x, act, sh, limit, err, cus, sel); break;
         }
     } else {
         switch (format) {
@@ -550,7 +564,8 @@ int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t 
 
 int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                         uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
-                        const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim) {
+                        const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim,
+                        const objeta_hip_expert_ptrs* sel) {
     const char* action = "launch MoE down + combine";
     OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, 32, inter, out_dim));
     if (n_tokens == 0 || out_dim == 0) return 0;
@@ -572,10 +587,10 @@ int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, 
     hipError_t e;
     if (jw) {
         switch (format) {
-            case OBJETA_HIP_Q4_0: e = launch_down_rows<QRows<kQ4>>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
-            case OBJETA_HIP_Q5_0: e = launch_down_rows<QRows<kQ5>>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
-            case OBJETA_HIP_IQ3_0: e = launch_down_rows<QRows<kIQ3>>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
-            default: e = launch_down_rows<Fp4Rows>(s, table, ids, wts, act, resid, out, sh, jw, err); break;
+            case OBJETA_HIP_Q4_0: e = launch_down_rows<QRows<kQ4>>(s, table, ids, wts, act, resid, out, sh, jw, err, sel); break;
+            case OBJETA_HIP_Q5_0: e = launch_down_rows<QRows<kQ5>>(s, table, ids, wts, act, resid, out, sh, jw, err, sel); break;
+            case OBJETA_HIP_IQ3_0: e = launch_down_rows<QRows<kIQ3>>(s, table, ids, wts, act, resid, out, sh, jw, err, sel); break;
+            default: e = launch_down_rows<Fp4Rows>(s, table, ids, wts, act, resid, out, sh, jw, err, sel); break;
         }
     } else {
         switch (format) {
@@ -592,11 +607,13 @@ int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, 
 int32_t launch_moe_selected(objeta_hip_context* ctx, int32_t format, hipStream_t s,
                             const objeta_hip_expert_ptrs* table, uint64_t n_table, const uint32_t* ids,
                             const float* wts, uint64_t n_tokens, uint64_t k, const float* x, const float* resid,
-                            float* out, uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit, float* act) {
+                            float* out, uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit, float* act,
+                            const objeta_hip_expert_ptrs* sel) {
     OBJ_TRY(validate_moe("launch selected-expert MoE", format, n_table, n_tokens, k, hidden, inter, out_dim));
     if (n_tokens == 0 || out_dim == 0) return 0;
-    OBJ_TRY(launch_moe_gate_up(ctx, format, s, table, n_table, ids, n_tokens, k, x, act, hidden, inter, limit));
-    return launch_moe_down(ctx, format, s, table, n_table, ids, wts, n_tokens, k, act, resid, out, inter, out_dim);
+    OBJ_TRY(launch_moe_gate_up(ctx, format, s, table, n_table, ids, n_tokens, k, x, act, hidden, inter, limit, sel));
+    return launch_moe_down(ctx, format, s, table, n_table, ids, wts, n_tokens, k, act, resid, out, inter, out_dim,
+                           sel);
 }
 
 int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
@@ -627,7 +644,7 @@ int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, 
     float* act = nullptr;
     OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k ? k : 1, intermediate ? intermediate : 1, &act));
     return launch_moe_selected(ctx, format, s, d_table, n_table, d_ids, d_weights, n_tokens, k, d_x, d_residual,
-                               d_out, hidden, intermediate, out_dim, swiglu_limit, act);
+                               d_out, hidden, intermediate, out_dim, swiglu_limit, act, nullptr);
     OBJ_GUARD_END
 }
 
@@ -668,8 +685,16 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
     hipStream_t s = resolve_stream(ctx, stream);
     if (n_tokens == 0) return 0;
     if (!d_ids_out || !d_weights_out) OBJ_FAIL(kInvalidInput, "moe_layer_device", "NULL routing output");
-    OBJ_TRY(objeta_hip_router_topk_device(ctx, s, d_router_w, d_router_bias, d_x, n_tokens, n_experts, hidden, k,
-                                          renormalize, d_ids_out, d_weights_out));
+    // the router also resolves the selection to table entries for the expert kernels
+    void* rws = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsRouter, static_cast<size_t>(n_tokens) * kMaxRouterExperts * 2 * sizeof(uint64_t),
+                             &rws));
+    void* sws = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsSelTab, static_cast<size_t>(n_tokens * (k ? k : 1)) * sizeof(objeta_hip_expert_ptrs),
+                             &sws));
+    objeta_hip_expert_ptrs* sel = d_table ? static_cast<objeta_hip_expert_ptrs*>(sws) : nullptr;
+    OBJ_TRY(launch_router(ctx, s, d_router_w, d_router_bias, d_x, n_tokens, n_experts, hidden, k, renormalize,
+                          d_ids_out, d_weights_out, static_cast<uint64_t*>(rws), d_table, &sel));
     if (out_dim == 0) return 0;
     // one token, top-8: gate/up and down in one launch over the XCDs
     if (n_tokens == 1 && ctx->experts_xcd && reinterpret_cast<uintptr_t>(d_x) % 16 == 0 &&
@@ -679,7 +704,7 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
     float* act = nullptr;
     OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k, intermediate ? intermediate : 1, &act));
     return launch_moe_selected(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, n_tokens, k, d_x,
-                               d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit, act);
+                               d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit, act, sel);
     OBJ_GUARD_END
 }
 

@@ -36,7 +36,8 @@ __device__ void router_select(const float* __restrict__ w_r, const float* __rest
                               int renormalize, uint32_t* __restrict__ ids, float* __restrict__ weights,
                               const uint64_t* ws_logit, const uint64_t* ws_bound, uint32_t epoch,
                               uint32_t* __restrict__ counter, uint32_t* __restrict__ err, float* scratch,
-                              uint32_t scratch_floats) {
+                              uint32_t scratch_floats, const objeta_hip_expert_ptrs* tab_lds = nullptr,
+                              objeta_hip_expert_ptrs* sel_tab = nullptr) {
     __shared__ SelectLds<kMaxExperts> s;
     __shared__ int s_pending;
     for (uint32_t spin = 0;; ++spin) {
@@ -64,6 +65,9 @@ __device__ void router_select(const float* __restrict__ w_r, const float* __rest
         !select_underflow(s, w_r, bias, xat, n_experts, hidden, k, scratch, scratch_floats))
         select_sequential(s, w_r, bias, xat, n_experts, hidden, k);
     write_selection(s, k, renormalize, ids, weights);
+    // the selected experts' table entries (the table was staged in LDS while the
+    // logits were awaited), so that the expert kernels need not look up id, then table
+    if (sel_tab && threadIdx.x < k) sel_tab[threadIdx.x] = tab_lds[s.sel[threadIdx.x]];
     if (threadIdx.x == 0) __hip_atomic_store(counter, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -168,11 +172,25 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
     const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
     uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
     float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
-    uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ table,
+    objeta_hip_expert_ptrs* __restrict__ sel_tab) {
     extern __shared__ float xs[];  // x in the padded pair layout: (hidden / 64) * kPadX floats
     __shared__ double red[8];
     const uint32_t t = blockIdx.y;
     const uint32_t e = blockIdx.x;
+    // workgroup 0 resolving the selection to table entries: the table's words are
+    // requested first (they wait in registers until the selection needs them)
+    constexpr uint32_t kTabWords = static_cast<uint32_t>(kSelTabMaxExperts) * 6 / kRThreads;
+    uint64_t tw[kTabWords];
+    const uint32_t n_tab = n_experts * 6;
+    if (sel_tab && blockIdx.x == 0) {
+        const uint64_t* tsrc = reinterpret_cast<const uint64_t*>(table);
+#pragma unroll
+        for (uint32_t q = 0; q < kTabWords; ++q) {
+            const uint32_t i = threadIdx.x + q * kRThreads;
+            tw[q] = tsrc[i < n_tab ? i : n_tab - 1];
+        }
+    }
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float* xt = x + static_cast<size_t>(t) * hidden;
     uint64_t* ws_logit = ws + static_cast<size_t>(t) * 2 * kMaxExperts;
@@ -205,24 +223,37 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
     }
     if (blockIdx.x != 0) return;
     // workgroup 0 selects; x in LDS serves the recomputation of close calls (staged
-    // while the other workgroups still publish)
+    // while the other workgroups still publish), the table its resolution
     for (uint32_t i = threadIdx.x; i < (hidden >> 2); i += kRThreads) {
         const uint32_t c = i << 2;
         *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = reinterpret_cast<const float4*>(xt)[i];
     }
-    __syncthreads();
     const uint32_t x_floats = (hidden / 64) * kPadX;
+    auto* tab_lds = reinterpret_cast<objeta_hip_expert_ptrs*>(xs + x_floats + kRefineScratch);
+    if (sel_tab) {
+        uint64_t* tl = reinterpret_cast<uint64_t*>(tab_lds);
+#pragma unroll
+        for (uint32_t q = 0; q < kTabWords; ++q) {
+            const uint32_t i = threadIdx.x + q * kRThreads;
+            if (i < n_tab) tl[i] = tw[q];
+        }
+    }
+    __syncthreads();
     const float* xl = xs;
     router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,
                   renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit,
-                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch);
+                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch, tab_lds,
+                  sel_tab ? sel_tab + static_cast<size_t>(t) * k : nullptr);
 }
 
 }  // namespace
 
+static_assert(kMaxRouterExperts == static_cast<uint64_t>(kMaxExperts), "router workspace layout");
+
 int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, const float* bias,
                       const float* x, uint64_t n_tokens, uint64_t n_experts, uint64_t hidden, uint64_t k,
-                      int32_t renormalize, uint32_t* ids, float* weights, uint64_t* ws) {
+                      int32_t renormalize, uint32_t* ids, float* weights, uint64_t* ws,
+                      const objeta_hip_expert_ptrs* table, objeta_hip_expert_ptrs** sel_tab) {
     const char* action = "launch router_topk";
     if (n_experts == 0 || n_experts > kMaxExperts)
         OBJ_FAIL(kInvalidInput, action, strf("num_experts %llu must be in 1..=%d", (unsigned long long)n_experts, kMaxExperts));
@@ -238,17 +269,23 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
     uint32_t* err = ctx->counters + ctx->counter_words;
     const bool lanes = vec && hidden % 256 == 0 && hidden <= 256u * 32u;
     const bool split = vec && hidden % 1024 == 0 && hidden <= 1024u * 8u;
+    // table resolution (split kernel, up to kSelTabMaxExperts experts) or none
+    objeta_hip_expert_ptrs* st = (sel_tab && table && split && n_experts <= kSelTabMaxExperts) ? *sel_tab : nullptr;
+    if (sel_tab) *sel_tab = st;
     if (split) {
-        const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
+        const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float) +
+                           (st ? static_cast<size_t>(n_experts) * sizeof(objeta_hip_expert_ptrs) : 0);
         const dim3 sgrid(static_cast<uint32_t>(n_experts), static_cast<uint32_t>(n_tokens));
         if (hidden <= 1024u * 2u)
             hipLaunchKernelGGL(router_split_kernel<2>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err,
+                               st ? table : nullptr, st);
         else
             hipLaunchKernelGGL(router_split_kernel<8>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err,
+                               st ? table : nullptr, st);
     } else if (lanes) {
         const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
         if (hidden <= 256u * 8u)
@@ -288,6 +325,6 @@ extern "C" int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta
     void* ws = nullptr;
     OBJ_TRY(ensure_workspace(ctx, s, kWsRouter, need, &ws));
     return launch_router(ctx, s, d_w_r, d_bias, d_x, n_tokens, n_experts, hidden, k, renormalize, d_ids,
-                         d_weights, static_cast<uint64_t*>(ws));
+                         d_weights, static_cast<uint64_t*>(ws), nullptr, nullptr);
     OBJ_GUARD_END
 }
