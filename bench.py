@@ -166,8 +166,9 @@ def main() -> int:
                     help="tokens of the batched side measurement (layer entry point and grouped-token path); 0 skips it")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; --gpus > 1 is not supported "
-                                   "(the multi-GPU sharding is described in DESIGN.md)"}))
+        print(json.dumps({"error": "one GPU is measured; --gpus > 1 is not supported (a layer would "
+                                   "shard each selected expert's rows over the GPUs and all-reduce "
+                                   "the partial outputs)"}))
         return 2
 
     from objeta_amd import HipBackend, MoeExecutor, MoeStack, check

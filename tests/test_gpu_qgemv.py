@@ -2,7 +2,7 @@
 
 Tolerance: GPU and CPU sum the same products in different orders, so results
 differ by fp32 rounding only. Per element we require
-    |y - ref| <= 1e-4 * max|ref|     (the north star's 1e-4 relative bound)
+    |y - ref| <= 1e-4 * max|ref|     (the path's 1e-4 relative bound)
 and, tighter, |y - ref| <= 2^-18 * sum_j |w_j x_j| + 1e-30 (a few hundred ulps of
 the dot product's magnitude)."""
 import ctypes as C
