@@ -7,15 +7,14 @@ blocks), router W_r ~N(0, 0.02) with logits biased by ln Zipf(s=1.1) over a
 per-layer rank permutation, hidden ~N(0, 1), batch 1 decode. Each layer computes
     h <- h + sum_j w_j * down_j(silu(gate_j h) * up_j h)
 over the router's softmax -> top-8 -> renormalised selection. Every expert of every
-layer is resident in HBM (16.3 GB); one step is one token through all 48 layers in
-one launch of the persistent decode-stack kernel (router, top-8, fused gate/up +
-SiLU, down + combine for every layer, handed between workgroups on the device).
-The same stack run as three kernels per layer from a hipGraph is reported beside it.
+layer is resident in HBM (16.3 GB); one step is one token through all 48 layers,
+three kernels per layer (router + top-8, fused gate/up + SiLU, down + combine)
+replayed from a hipGraph.
 
-Reported: MoE layer us/token (stack time / 48), the stack's us/token, achieved HBM
+Reported: MoE layer us/token (step time / 48), the step's us/token, achieved HBM
 GB/s on expert-weight bytes (8 experts x 2,654,208 B per layer) and its fraction of
-MI355X's 8 TB/s, a roofline record for the dominant kernel (the decode-stack
-kernel, one launch per token) timed with HIP events on its stream, and the CPU
+MI355X's 8 TB/s, a roofline record for a layer kernel timed with HIP events on
+its stream, and the CPU
 baseline: the oracle's single-thread restatement of the reference CPU path
 (cpu_router + selected_moe_cpu) on a few tokens.
 
@@ -158,8 +157,6 @@ def main() -> int:
     ap.add_argument("--tokens-pool", type=int, default=16, help="distinct input tokens cycled over steps")
     ap.add_argument("--cpu-tokens", type=int, default=4, help="tokens in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=20251201)
-    ap.add_argument("--path", choices=("auto", "stack", "graph"), default="auto",
-                    help="auto: time both and report the faster as the headline")
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="only run the counter calibration kernels (a 64 MiB fill, a 37.7 MB streaming read)")
     ap.add_argument("--batch", type=int, default=16,
@@ -171,7 +168,7 @@ def main() -> int:
                                    "the partial outputs)"}))
         return 2
 
-    from objeta_amd import HipBackend, MoeExecutor, MoeStack, check
+    from objeta_amd import HipBackend, MoeExecutor, check
     from objeta_amd._lib import load
 
     H, E, K, I, L = 2048, 128, 8, 768, args.layers
@@ -220,21 +217,10 @@ def main() -> int:
             raise RuntimeError("device error word set during a timed run")
         return ms.value * 1000.0 / steps
 
-    # ---- the persistent decode-stack kernel, one launch per token ----
-    layers = [(stack.tables[l], stack.router_w[l], stack.router_b[l], ids.addr(4 * l * K), wts.addr(4 * l * K))
-              for l in range(L)]
-    plan = MoeStack(be, stack.fmt, layers, E, K, H, I)
-    stack_us = None
-    if args.path in ("auto", "stack"):
-        for i in range(args.warmup):
-            plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream)
-        be.synchronize(stream)
-        stack_us = timed(lambda i: plan.run(xs.addr(4 * (i % P) * H), h.addr(), stream=stream), args.steps)
-
     # ---- three kernels per layer (router, gate/up + SiLU, down + combine), replayed from a hipGraph ----
     graph_us = None
     gu_us = None
-    if args.path in ("auto", "graph"):
+    if True:
         enqueue_token(0)
         be.synchronize(stream)
         graphs = []
@@ -247,8 +233,7 @@ def main() -> int:
         for i in range(args.warmup):
             check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream))
         be.synchronize(stream)
-        gsteps = args.steps if args.path == "graph" else max(10, args.steps // 2)
-        graph_us = timed(lambda i: check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream)), gsteps)
+        graph_us = timed(lambda i: check(lib.objeta_hip_graph_launch(ctx, graphs[i % P], stream)), args.steps)
         # the graph's largest kernel on its own: gate/up + SiLU of one layer's 8 selected experts
         act = be.alloc(4 * K * I)
         lids = ids.addr(4 * 0 * K)
@@ -261,43 +246,10 @@ def main() -> int:
         be.synchronize(stream)
         gu_us = timed(gate_up, args.steps)
 
-    # ---- side measurement: the fused single-launch layer (one selection slot per XCD) ----
-    fused_us = None
-    if args.path == "auto" and moe.layer_fused_supported(stack.fmt, E, K, H, I, H, stream=stream):
-        def enqueue_fused(p: int):
-            x0 = xs.addr(4 * p * H)
-            for l in range(L):
-                src = x0 if l == 0 else h.addr()
-                moe.layer_fused_device(stack.fmt, stack.tables[l], stack.router_w[l], stack.router_b[l], K, src, src,
-                                       h.addr(), ids.addr(4 * l * K), wts.addr(4 * l * K), H, I, H, stream=stream)
-        enqueue_fused(0)
-        be.synchronize(stream)
-        fgraphs = []
-        for p in range(P):
-            check(lib.objeta_hip_graph_begin_capture(ctx, stream))
-            enqueue_fused(p)
-            g = C.c_void_p()
-            check(lib.objeta_hip_graph_end_capture(ctx, stream, C.byref(g)))
-            fgraphs.append(g)
-        for i in range(args.warmup):
-            check(lib.objeta_hip_graph_launch(ctx, fgraphs[i % P], stream))
-        be.synchronize(stream)
-        fused_us = timed(lambda i: check(lib.objeta_hip_graph_launch(ctx, fgraphs[i % P], stream)),
-                         max(10, args.steps // 2))
-        for g in fgraphs:
-            check(lib.objeta_hip_graph_destroy(ctx, g))
-
-    use_stack = graph_us is None or (stack_us is not None and stack_us <= graph_us)
-    token_us = stack_us if use_stack else graph_us
+    token_us = graph_us
     layer_us = token_us / L
     gbps = expert_bytes_token / (token_us * 1e-6) / 1e9
-    if use_stack:
-        kernel_bytes = expert_bytes_token + router_bytes_token + 4 * H * 2
-        roof = {"kernel": f"moe_stack_kernel (persistent decode stack, {L} layers per launch)", "bound": "hbm",
-                "achieved": round(kernel_bytes / (stack_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(kernel_bytes / (stack_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
-                "avg_launch_us": round(stack_us, 3), "algorithmic_bytes_per_launch": kernel_bytes}
-    else:
+    if True:
         # 8 experts' gate and up matrices + x in + activations out
         kernel_bytes = K * 2 * stack.gu_bytes + 4 * H + 4 * K * I
         traffic = measured_traffic("moe_gate_up_kernel")
@@ -417,23 +369,18 @@ def main() -> int:
         "config": {"workload": "qwen3_a3b_moe_stack", "layers": L, "hidden": H, "experts": E, "top_k": K,
                    "moe_intermediate": I, "batch": 1, "format": "Q4_0", "residency": "all experts in HBM",
                    "tokens_pool": P},
-        "path": "persistent decode stack" if use_stack else "three kernels per layer from a hipGraph",
+        "path": "three kernels per layer from a hipGraph",
         "us_per_token": round(token_us, 2),
         "expert_bytes_per_token": expert_bytes_token,
         "expert_hbm_gbps": round(gbps, 1),
         "expert_hbm_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
         "roofline": roof,
-        "stack_us_per_token_layer": round(stack_us / L, 3) if stack_us is not None else None,
-        "graph_us_per_token_layer": round(graph_us / L, 3) if graph_us is not None else None,
-        "fused_us_per_token_layer": round(fused_us / L, 3) if fused_us is not None else None,
         "gate_up_kernel_us": round(gu_us, 3) if gu_us is not None else None,
-        "stack_grid_workgroups": plan.info()["grid"],
         "batch": batch,
         "cpu_baseline": cpu,
         "device": {"name": dev["name"], "arch": dev["arch"], "compute_units": dev["compute_units"]},
     }
     print(json.dumps(rec), flush=True)
-    plan.close()
     be.close()
     return 0
 

@@ -311,68 +311,6 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
                                     float* d_weights_out, uint64_t hidden, uint64_t intermediate,
                                     uint64_t out_dim, float swiglu_limit);
 
-/* The layer of objeta_hip_moe_layer_device for one token (same arguments and
- * results, n_tokens == 1) as a single launch: XCD x of the device computes every
- * router logit itself, selects, and streams selection slot x's gate/up and down
- * rows; activations pass between the CUs of an XCD through its L2 and only the
- * down row sums cross XCDs. Unsupported (kind Unsupported) outside the limits of
- * objeta_hip_moe_layer_fused_supported. No host synchronisation; graph-capturable
- * after one call outside capture. No reference counterpart. */
-int32_t objeta_hip_moe_layer_fused_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
-                                          const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
-                                          const float* d_router_w, const float* d_router_bias, uint64_t k,
-                                          int32_t renormalize, const float* d_x, const float* d_residual,
-                                          float* d_out, uint32_t* d_ids_out, float* d_weights_out, uint64_t hidden,
-                                          uint64_t intermediate, uint64_t out_dim, float swiglu_limit);
-
-/* *out = 1 when objeta_hip_moe_layer_fused_device takes these arguments, else 0:
- * top-8 routing, n_experts <= 256,
- * hidden a power-of-two multiple of 64 in 256..2048, intermediate a multiple of
- * 64, out_dim == hidden, a grid that fits on the device at once, and consecutive
- * workgroups dispatched to consecutive XCDs of 8 (probed on the first call made
- * outside graph capture). No reference counterpart. */
-int32_t objeta_hip_moe_layer_fused_supported(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
-                                             uint64_t n_experts, uint64_t k, uint64_t hidden,
-                                             uint64_t intermediate, uint64_t out_dim, int32_t* out);
-
-/* ------------------------------------------------------------ decode stack */
-/* One MoE layer of a decode stack: its expert table (n_experts entries), router
- * weights [n_experts][hidden] (16-byte aligned) and optional bias, and optional
- * outputs receiving the layer's k expert ids and weights. */
-typedef struct {
-    const objeta_hip_expert_ptrs* d_table;
-    const float* d_router_w;
-    const float* d_router_bias;
-    uint32_t* d_ids_out;
-    float* d_weights_out;
-} objeta_hip_moe_stack_layer;
-
-/* A decode stack plan: h <- h + MoE_l(h) for l = 0..n_layers-1 at batch 1, each
- * layer routed on the device (objeta_hip_router_topk_device semantics, ids
- * bit-exact with the reference's sequential router) and computed as
- * objeta_hip_moe_selected_device. One cooperative launch per run: all layers
- * in one kernel whose workgroups hand router logits, selections, activations and
- * hidden states to each other through epoch-tagged words, with no host
- * synchronisation and no kernel boundaries. No reference counterpart as one call:
- * the reference runs execute_selected_moe_cuda layer by layer with host routing.
- * Limits: n_experts <= 256, k <= 8, hidden a multiple of 256 and <= 2048,
- * intermediate a multiple of 64. Returns Unsupported outside them (use the
- * per-layer entry points). The plan owns its buffers; runs on one plan must be
- * serialised (the library's streams order them). */
-typedef struct objeta_hip_moe_stack objeta_hip_moe_stack;
-int32_t objeta_hip_moe_stack_create(objeta_hip_context* ctx, int32_t format, const objeta_hip_moe_stack_layer* layers,
-                                    uint64_t n_layers, uint64_t n_experts, uint64_t k, int32_t renormalize,
-                                    uint64_t hidden, uint64_t intermediate, float swiglu_limit,
-                                    objeta_hip_moe_stack** out);
-/* Runs the stack on d_x [hidden] and writes the final hidden state to d_h_out
- * [hidden] (may alias d_x). Asynchronous on `stream`. Not capturable into a graph
- * (cooperative launch). */
-int32_t objeta_hip_moe_stack_run(objeta_hip_moe_stack* st, objeta_hip_stream stream, const float* d_x,
-                                 float* d_h_out);
-/* Launch geometry of the plan (workgroups, dynamic LDS bytes). */
-int32_t objeta_hip_moe_stack_info(const objeta_hip_moe_stack* st, uint32_t* grid, uint32_t* lds_bytes);
-int32_t objeta_hip_moe_stack_destroy(objeta_hip_moe_stack* st);
-
 /* Reads and clears the context's device error word (non-zero after a kernel met
  * an expert id outside its table). Synchronises the context's streams. */
 int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out);

@@ -87,10 +87,6 @@ class MoeTelemetry(C.Structure):
                 [(n, U64) for n in _TEL_U64_TAIL])
 
 
-class StackLayer(C.Structure):
-    _fields_ = [("d_table", P), ("d_router_w", P), ("d_router_bias", P), ("d_ids_out", P), ("d_weights_out", P)]
-
-
 class QGemvTelemetry(C.Structure):
     _fields_ = [("h2d_ms", F32), ("kernel_ms", F32), ("d2h_ms", F32), ("unaccounted_ms", F32),
                 ("total_ms", F32), ("effective_gbps", F32), ("bytes_read", U64)]
@@ -139,9 +135,6 @@ SIGNATURES = {
                                              U64, F32]),
     "objeta_hip_moe_layer_device": (I32, [P, I32, P, P, U64, P, P, U64, I32, U64, P, P, P, P, P,
                                           U64, U64, U64, F32]),
-    "objeta_hip_moe_layer_fused_supported": (I32, [P, I32, P, U64, U64, U64, U64, U64, P]),
-    "objeta_hip_moe_layer_fused_device": (I32, [P, I32, P, P, U64, P, P, U64, I32, P, P, P, P, P, U64, U64, U64,
-                                                F32]),
     "objeta_hip_device_error": (I32, [P, P]),
     "objeta_hip_moe_grouped_device": (I32, [P, I32, P, P, U64, P, P, U64, U64, P, P, P, U64, U64, U64, F32]),
     "objeta_hip_moe_gate_up_device": (I32, [P, I32, P, P, U64, P, U64, U64, P, P, U64, U64, F32]),
@@ -163,10 +156,6 @@ SIGNATURES = {
     "objeta_hip_cache_order": (I32, [P, P, U64, P]),
     "objeta_hip_moe_execute_selected": (I32, [P, I32, P, P, U64, P, P, U64, P, U64, U64, U64, U64, U64, P,
                                               P, P]),
-    "objeta_hip_moe_stack_create": (I32, [P, I32, P, U64, U64, U64, I32, U64, U64, F32, P]),
-    "objeta_hip_moe_stack_run": (I32, [P, P, P, P]),
-    "objeta_hip_moe_stack_info": (I32, [P, P, P]),
-    "objeta_hip_moe_stack_destroy": (I32, [P]),
 }
 
 

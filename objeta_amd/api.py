@@ -16,7 +16,7 @@ import numpy as np
 
 from . import _lib
 from ._lib import (CacheKey, CacheStats, DeviceInfo, Error, ExpertPtrs, HostExpert, InitOptions, MoeTelemetry,
-                   QGemvTelemetry, StackLayer)
+                   QGemvTelemetry)
 
 KIND_NAMES = ["Driver", "Runtime", "Nvrtc", "Io", "InvalidInput", "Unsupported", "Internal"]
 
@@ -365,23 +365,6 @@ class MoeExecutor:
             _addr_or_none(d_residual), _addr(d_out), _addr(d_ids_out), _addr(d_weights_out), hidden,
             inter, out_dim, swiglu_limit))
 
-    def layer_fused_device(self, fmt, table: ExpertTable, d_router_w, d_router_bias, k: int, d_x, d_residual, d_out,
-                           d_ids_out, d_weights_out, hidden: int, inter: int, out_dim: int, renormalize: bool = True,
-                           swiglu_limit: float = 0.0, stream=None) -> None:
-        """layer_device for one token as a single launch (one selection slot per XCD)."""
-        check(self.L.objeta_hip_moe_layer_fused_device(
-            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr(d_router_w),
-            _addr_or_none(d_router_bias), k, 1 if renormalize else 0, _addr(d_x), _addr_or_none(d_residual),
-            _addr(d_out), _addr(d_ids_out), _addr(d_weights_out), hidden, inter, out_dim, swiglu_limit))
-
-    def layer_fused_supported(self, fmt, n_experts: int, k: int, hidden: int, inter: int, out_dim: int,
-                              stream=None) -> bool:
-        """Whether layer_fused_device takes these arguments."""
-        v = C.c_int32(0)
-        check(self.L.objeta_hip_moe_layer_fused_supported(self.backend.ctx, int(fmt), stream, n_experts, k, hidden,
-                                                          inter, out_dim, C.byref(v)))
-        return bool(v.value)
-
     def device_error(self) -> int:
         v = C.c_uint32(0)
         check(self.L.objeta_hip_device_error(self.backend.ctx, C.byref(v)))
@@ -587,41 +570,3 @@ MoeExecutor.execute_selected_moe = _moe_execute_selected
 MoeExecutor.execute_selected_moe_cuda = _moe_execute_selected
 MoeExecutor.execute_selected_moe_native_fp4 = _moe_execute_native_fp4
 MoeExecutor.execute_selected_moe_native_fp4_cuda = _moe_execute_native_fp4
-
-
-class MoeStack:
-    """Decode-stack plan over the library's persistent kernel: h <- h + MoE_l(h) for
-    every layer, one launch per run. layers: list of (ExpertTable, router_w,
-    router_bias or None, ids_out or None, weights_out or None)."""
-
-    def __init__(self, backend: HipBackend, fmt, layers, n_experts: int, k: int, hidden: int, inter: int,
-                 renormalize: bool = True, swiglu_limit: float = 0.0):
-        self.backend = backend
-        self.L = backend.L
-        arr = (StackLayer * len(layers))()
-        self._keep = layers
-        for i, (table, w, b, ids, ws) in enumerate(layers):
-            arr[i] = StackLayer(_ptr_int(table.buf), _ptr_int(w), _ptr_int(b), _ptr_int(ids), _ptr_int(ws))
-        h = C.c_void_p()
-        check(self.L.objeta_hip_moe_stack_create(backend.ctx, int(fmt), arr, len(layers), n_experts, k,
-                                                 1 if renormalize else 0, hidden, inter, swiglu_limit, C.byref(h)))
-        self.h = h
-
-    def run(self, d_x, d_out, stream=None) -> None:
-        check(self.L.objeta_hip_moe_stack_run(self.h, stream, _addr(d_x), _addr(d_out)))
-
-    def info(self) -> dict:
-        g, lds = C.c_uint32(), C.c_uint32()
-        check(self.L.objeta_hip_moe_stack_info(self.h, C.byref(g), C.byref(lds)))
-        return {"grid": g.value, "lds_bytes": lds.value}
-
-    def close(self) -> None:
-        if self.h:
-            check(self.L.objeta_hip_moe_stack_destroy(self.h))
-            self.h = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass

@@ -514,7 +514,7 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
     auto* ah = reinterpret_cast<_Float16*>(b + o_ah);
     auto* al = reinterpret_cast<_Float16*>(b + o_all);
     float* part = reinterpret_cast<float*>(b + o_part);
-    uint32_t* err = ctx->counters + ctx->counter_words;
+    uint32_t* err = ctx->err_word;
     const uint32_t max_groups = A < n_table ? A : static_cast<uint32_t>(n_table);
     hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, s, ids, A, static_cast<uint32_t>(n_table), gw, err);
     hipLaunchKernelGGL(moe_split_kernel, dim3(T), dim3(256), 0, s, x, H, xh, xl, xmult);

@@ -75,13 +75,21 @@ enum WsSlot : int {
     kWsRouter = 0,
     kWsMoeAct = 1,
     kWsMoeTable = 2,
-    kWsMoeOut = 3,
-    kWsGrouped = 4,
-    kWsFused = 5,
-    kWsExperts = 6,
-    kWsSelTab = 7,
-    kWsSlots = 8
+    kWsGrouped = 3,
+    kWsSelTab = 4,
+    kWsSlots = 5
 };
+
+// The scratch of one stream. Calls on different streams of a context may be in
+// flight at the same time, so every stream that a call names gets its own
+// workspace regions and its own router epoch counters (created on the first call
+// on that stream made outside graph capture).
+struct StreamScratch {
+    hipStream_t stream = nullptr;
+    Workspace ws[kWsSlots];
+    uint32_t* epochs = nullptr;  // kEpochWords zero-initialised router counters, one per token
+};
+constexpr size_t kEpochWords = 4096;
 
 }  // namespace objeta
 
@@ -90,23 +98,13 @@ struct objeta_hip_context {
     objeta_hip_device_info info{};
     std::vector<hipStream_t> streams;  // streams[0] is the default compute stream
     hipStream_t copy_stream = nullptr;  // side stream for cache H2D traffic
-    objeta::Workspace ws[objeta::kWsSlots];  // scratch for multi-kernel entry points
-    std::vector<void*> retired_ws;           // replaced regions, freed at destroy
-    void* host_stage = nullptr;              // pinned host staging (expert tables)
-    void* transient_pool = nullptr;          // objeta_hip_expert_cache for uncached copies
-    std::vector<void*> caches;               // live caches created on this context
+    std::vector<objeta::StreamScratch*> scratch;  // per-stream scratch, see StreamScratch
+    std::vector<void*> retired_ws;                // replaced regions, freed at destroy
+    void* host_stage = nullptr;                   // pinned host staging (expert tables)
+    void* transient_pool = nullptr;               // objeta_hip_expert_cache for uncached copies
+    std::vector<void*> caches;                    // live caches created on this context
     size_t host_stage_bytes = 0;
-    uint32_t* counters = nullptr;       // zero-initialised device counters (self-resetting),
-                                        // followed by the device error word
-
-    size_t counter_words = 0;
-    // workgroup b runs on XCD b % 8 of an 8-XCD device (probed once): -1 unknown,
-    // 0 no, 1 yes
-    int xcd_round_robin = -1;
-    // batch-1 layers run their experts in one XCD-aligned launch when the shape
-    // allows and OBJETA_HIP_EXPERTS_XCD=1 was set at context creation (off by
-    // default: on MI355X it is slower than the gate/up and down kernels today)
-    bool experts_xcd = false;
+    uint32_t* err_word = nullptr;  // device error word (bits set by kernels, read by objeta_hip_device_error)
     std::mutex mu;
 };
 
@@ -114,8 +112,11 @@ namespace objeta {
 
 int32_t check_ctx(const objeta_hip_context* ctx, const char* action);
 hipStream_t resolve_stream(objeta_hip_context* ctx, objeta_hip_stream s);
-// Makes sure workspace region `slot` holds at least `bytes` and returns it in *out;
-// fails (Unsupported) if it would have to grow while `stream` is capturing.
+// The scratch of `stream` (created on first use; Unsupported while `stream` is
+// capturing and has none yet).
+int32_t stream_scratch(objeta_hip_context* ctx, hipStream_t stream, StreamScratch** out);
+// Makes sure workspace region `slot` of `stream` holds at least `bytes` and returns
+// it in *out; fails (Unsupported) if it would have to grow while `stream` is capturing.
 int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, int slot, size_t bytes, void** out);
 // Releases the device memory of every cache still alive on `ctx` (the caches stay
 // valid as accounting-only objects until destroyed).

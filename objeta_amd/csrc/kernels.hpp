@@ -19,8 +19,8 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
 
 int32_t launch_zero(hipStream_t s, void* d, uint64_t bytes);
 
-// The router launch behind objeta_hip_router_topk_device (ws: kMaxExperts * 2 words
-// per token). With table and sel_tab given and *sel_tab non-null, the router also
+// The router launch behind objeta_hip_router_topk_device (its epoch words and
+// counters are the scratch of stream `s`). With table and sel_tab given and *sel_tab non-null, the router also
 // writes the selected experts' table entries to (*sel_tab)[t * k + r] when it can
 // (up to kSelTabMaxExperts experts, hidden a multiple of 1024); *sel_tab is set to
 // nullptr when it does not.
@@ -28,7 +28,7 @@ constexpr uint64_t kSelTabMaxExperts = 256;
 constexpr uint64_t kMaxRouterExperts = 1024;  // router workspace: 2 words per expert and token
 int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, const float* bias,
                       const float* x, uint64_t n_tokens, uint64_t n_experts, uint64_t hidden, uint64_t k,
-                      int32_t renormalize, uint32_t* ids, float* weights, uint64_t* ws,
+                      int32_t renormalize, uint32_t* ids, float* weights,
                       const objeta_hip_expert_ptrs* table, objeta_hip_expert_ptrs** sel_tab);
 
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
@@ -50,31 +50,5 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
                            uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                            const float* x, const float* resid, float* out, uint64_t hidden, uint64_t inter,
                            uint64_t out_dim, float limit);
-
-// One layer of one token in a single launch (router, gate/up + SiLU, down +
-// combine, top-8, one selection slot per XCD); false when the shape is outside it,
-// its grid does not fit at once, or workgroups are not dispatched round-robin over
-// the 8 XCDs (probed on the first call outside graph capture).
-bool fused_layer_supported(objeta_hip_context* ctx, hipStream_t s, int32_t format, uint64_t n_experts, uint64_t k,
-                           uint64_t hidden, uint64_t inter, uint64_t out_dim);
-
-int32_t launch_moe_layer_fused(objeta_hip_context* ctx, int32_t format, hipStream_t s,
-                               const objeta_hip_expert_ptrs* table, uint64_t n_experts, const float* w_r,
-                               const float* bias, uint64_t k, int32_t renormalize, const float* x, const float* resid,
-                               float* out, uint32_t* ids_out, float* weights_out, uint64_t hidden, uint64_t inter,
-                               float limit);
-
-// The selected experts of one token (k == 8 ids and weights already on the device)
-// as one launch laid out over the XCDs: gate/up + SiLU and down + combine, the
-// down rows streaming with the gate/up rows. Same limits and probe as the fused
-// layer. Each launch must follow a router launch on the same context (the router's
-// token-0 counter is its epoch).
-bool experts_xcd_supported(objeta_hip_context* ctx, hipStream_t s, int32_t format, uint64_t n_experts, uint64_t k,
-                           uint64_t hidden, uint64_t inter, uint64_t out_dim);
-
-int32_t launch_moe_experts_xcd(objeta_hip_context* ctx, int32_t format, hipStream_t s,
-                               const objeta_hip_expert_ptrs* table, uint64_t n_experts, const uint32_t* ids,
-                               const float* wts, const float* x, const float* resid, float* out, uint64_t hidden,
-                               uint64_t inter, float limit);
 
 }  // namespace objeta

@@ -539,7 +539,7 @@ int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t 
     if (!table || !x || !act) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     if (reinterpret_cast<uintptr_t>(x) % 16) OBJ_FAIL(kInvalidInput, action, "x must be 16-byte aligned");
     const MoeShape sh = shape_of(n_table, n_tokens, k, hidden, inter, 1);
-    uint32_t* err = ctx->counters + ctx->counter_words;
+    uint32_t* err = ctx->err_word;
     const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
     const bool fast = fast_shape(sh.hidden) && static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 16 <= max_lds(ctx);
     hipError_t e;
@@ -572,7 +572,7 @@ int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, 
     if (!table || !wts || !act || !out) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     if (reinterpret_cast<uintptr_t>(act) % 16) OBJ_FAIL(kInvalidInput, action, "act must be 16-byte aligned");
     const MoeShape sh = shape_of(n_table, n_tokens, k, 32, inter, out_dim);
-    uint32_t* err = ctx->counters + ctx->counter_words;
+    uint32_t* err = ctx->err_word;
     uint32_t jw = 0;
     if (fast_shape(sh.inter)) {
         // one token: one selection slot per wave (k waves per workgroup), measured
@@ -686,59 +686,17 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
     if (n_tokens == 0) return 0;
     if (!d_ids_out || !d_weights_out) OBJ_FAIL(kInvalidInput, "moe_layer_device", "NULL routing output");
     // the router also resolves the selection to table entries for the expert kernels
-    void* rws = nullptr;
-    OBJ_TRY(ensure_workspace(ctx, s, kWsRouter, static_cast<size_t>(n_tokens) * kMaxRouterExperts * 2 * sizeof(uint64_t),
-                             &rws));
     void* sws = nullptr;
     OBJ_TRY(ensure_workspace(ctx, s, kWsSelTab, static_cast<size_t>(n_tokens * (k ? k : 1)) * sizeof(objeta_hip_expert_ptrs),
                              &sws));
     objeta_hip_expert_ptrs* sel = d_table ? static_cast<objeta_hip_expert_ptrs*>(sws) : nullptr;
     OBJ_TRY(launch_router(ctx, s, d_router_w, d_router_bias, d_x, n_tokens, n_experts, hidden, k, renormalize,
-                          d_ids_out, d_weights_out, static_cast<uint64_t*>(rws), d_table, &sel));
+                          d_ids_out, d_weights_out, d_table, &sel));
     if (out_dim == 0) return 0;
-    // one token, top-8: gate/up and down in one launch over the XCDs
-    if (n_tokens == 1 && ctx->experts_xcd && reinterpret_cast<uintptr_t>(d_x) % 16 == 0 &&
-        experts_xcd_supported(ctx, s, format, n_experts, k, hidden, intermediate, out_dim))
-        return launch_moe_experts_xcd(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, d_x, d_residual,
-                                      d_out, hidden, intermediate, swiglu_limit);
     float* act = nullptr;
     OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k, intermediate ? intermediate : 1, &act));
     return launch_moe_selected(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, n_tokens, k, d_x,
                                d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit, act, sel);
-    OBJ_GUARD_END
-}
-
-int32_t objeta_hip_moe_layer_fused_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
-                                          const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
-                                          const float* d_router_w, const float* d_router_bias, uint64_t k,
-                                          int32_t renormalize, const float* d_x, const float* d_residual,
-                                          float* d_out, uint32_t* d_ids_out, float* d_weights_out, uint64_t hidden,
-                                          uint64_t intermediate, uint64_t out_dim, float swiglu_limit) {
-    OBJ_GUARD_BEGIN
-    const char* action = "moe_layer_fused_device";
-    OBJ_TRY(check_ctx(ctx, action));
-    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
-    hipStream_t s = resolve_stream(ctx, stream);
-    if (!d_ids_out || !d_weights_out) OBJ_FAIL(kInvalidInput, action, "NULL routing output");
-    if (!fused_layer_supported(ctx, s, format, n_experts, k, hidden, intermediate, out_dim))
-        OBJ_FAIL(kUnsupported, action, "shape, grid or XCD placement outside the fused layer");
-    return launch_moe_layer_fused(ctx, format, s, d_table, n_experts, d_router_w, d_router_bias, k, renormalize, d_x,
-                                  d_residual, d_out, d_ids_out, d_weights_out, hidden, intermediate, swiglu_limit);
-    OBJ_GUARD_END
-}
-
-int32_t objeta_hip_moe_layer_fused_supported(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
-                                             uint64_t n_experts, uint64_t k, uint64_t hidden,
-                                             uint64_t intermediate, uint64_t out_dim, int32_t* out) {
-    OBJ_GUARD_BEGIN
-    OBJ_TRY(check_ctx(ctx, "moe_layer_fused_supported"));
-    if (!out) OBJ_FAIL(kInvalidInput, "moe_layer_fused_supported", "out is NULL");
-    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
-    *out = fused_layer_supported(ctx, resolve_stream(ctx, stream), format, n_experts, k, hidden, intermediate,
-                                   out_dim)
-                 ? 1
-                 : 0;
-    return 0;
     OBJ_GUARD_END
 }
 
@@ -748,7 +706,7 @@ int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out) {
     if (!out) OBJ_FAIL(kInvalidInput, "device error word", "out is NULL");
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     for (hipStream_t st : ctx->streams) OBJ_HIP(hipStreamSynchronize(st), "synchronize stream");
-    uint32_t* err = ctx->counters + ctx->counter_words;
+    uint32_t* err = ctx->err_word;
     OBJ_HIP(hipMemcpy(out, err, sizeof(uint32_t), hipMemcpyDeviceToHost), "read device error word");
     const uint32_t zero = 0;
     OBJ_HIP(hipMemcpy(err, &zero, sizeof(uint32_t), hipMemcpyHostToDevice), "clear device error word");

@@ -127,11 +127,7 @@ uint32_t grid_for_stream(const objeta_hip_context* ctx, K kernel, size_t lds, ui
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
-    int want = kStreamWgsPerCu;
-#ifdef OBJETA_TUNE
-    if (const char* e = getenv("OBJETA_TUNE_WGS_PER_CU")) want = atoi(e);
-#endif
-    if (per_cu > want) per_cu = want;
+    if (per_cu > kStreamWgsPerCu) per_cu = kStreamWgsPerCu;
     const uint32_t need = (n_groups + kWaves - 1) / kWaves;
     const uint32_t cap = cus * static_cast<uint32_t>(per_cu);
     return need < cap ? need : cap;
@@ -148,28 +144,12 @@ hipError_t launch_stream_u(const objeta_hip_context* ctx, hipStream_t s, const R
     return hipGetLastError();
 }
 
-// Rows per wave item: 2 when the matrix has enough rows to keep every resident
-// wave busy, else 1 (more, smaller items).
+// One row group per wave item: the streaming grid already keeps every resident
+// wave busy at the shapes of the MoE layers (two rows per item measured no faster).
 template <class R, int NT>
 hipError_t launch_stream(const objeta_hip_context* ctx, hipStream_t s, const R& rm, const float* x, float* y,
                          uint32_t rows, uint32_t cols, uint32_t lpr, size_t lds) {
-    if constexpr (NT == 1) {
-        const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
-        const uint32_t g = 64 / lpr;
-        const uint32_t groups_u2 = (rows + 2 * g - 1) / (2 * g);
-        uint32_t min_groups = cus * kWaves * kStreamWgsPerCu;
-#ifdef OBJETA_TUNE
-        if (const char* e = getenv("OBJETA_TUNE_U")) {
-            if (atoi(e) == 2) return launch_stream_u<R, 1, 2>(ctx, s, rm, x, y, rows, cols, lpr, lds);
-            return launch_stream_u<R, 1, 1>(ctx, s, rm, x, y, rows, cols, lpr, lds);
-        }
-#endif
-        (void)groups_u2;
-        (void)min_groups;
-        return launch_stream_u<R, 1, 1>(ctx, s, rm, x, y, rows, cols, lpr, lds);
-    } else {
-        return launch_stream_u<R, NT, 1>(ctx, s, rm, x, y, rows, cols, lpr, lds);
-    }
+    return launch_stream_u<R, NT, 1>(ctx, s, rm, x, y, rows, cols, lpr, lds);
 }
 
 template <int F>
@@ -217,13 +197,7 @@ int32_t launch_qgemv(objeta_hip_context* ctx, int32_t format, hipStream_t s, con
         int nt;
         if (fast) {
             const uint32_t pairs = c / 64;
-            uint32_t lpr = pick_lpr(pairs);
-#ifdef OBJETA_TUNE
-            if (const char* e = getenv("OBJETA_TUNE_LPR")) {
-                const uint32_t l = static_cast<uint32_t>(atoi(e));
-                if (l && pairs % l == 0 && l <= 64) lpr = l;
-            }
-#endif
+            const uint32_t lpr = pick_lpr(pairs);
             const size_t per_token = static_cast<size_t>(pairs) * kPad * sizeof(float);
             nt = max_nt_for_lds(per_token, lds_limit, rem);
             if (nt == 0) OBJ_FAIL(kUnsupported, action, strf("cols %u exceed the LDS activation stage", c));

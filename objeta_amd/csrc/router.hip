@@ -252,7 +252,7 @@ static_assert(kMaxRouterExperts == static_cast<uint64_t>(kMaxExperts), "router w
 
 int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, const float* bias,
                       const float* x, uint64_t n_tokens, uint64_t n_experts, uint64_t hidden, uint64_t k,
-                      int32_t renormalize, uint32_t* ids, float* weights, uint64_t* ws,
+                      int32_t renormalize, uint32_t* ids, float* weights,
                       const objeta_hip_expert_ptrs* table, objeta_hip_expert_ptrs** sel_tab) {
     const char* action = "launch router_topk";
     if (n_experts == 0 || n_experts > kMaxExperts)
@@ -262,11 +262,19 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
                  strf("top_k %llu must be in 1..=min(num_experts, %d)", (unsigned long long)k, kMaxTopK));
     if (hidden == 0 || hidden > (1u << 24)) OBJ_FAIL(kInvalidInput, action, "hidden must be in 1..=2^24");
     if (n_tokens == 0) return 0;
-    if (n_tokens > ctx->counter_words) OBJ_FAIL(kInvalidInput, action, strf("n_tokens > %zu", ctx->counter_words));
+    if (n_tokens > kEpochWords) OBJ_FAIL(kInvalidInput, action, strf("n_tokens > %zu", kEpochWords));
     if (!w_r || !x || !ids || !weights) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    // the epoch words and counters of this stream's router scratch
+    StreamScratch* sc = nullptr;
+    OBJ_TRY(stream_scratch(ctx, s, &sc));
+    void* wsv = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsRouter, static_cast<size_t>(n_tokens) * kMaxRouterExperts * 2 * sizeof(uint64_t),
+                             &wsv));
+    uint64_t* ws = static_cast<uint64_t*>(wsv);
+    uint32_t* counters = sc->epochs;
     const dim3 grid(static_cast<uint32_t>((n_experts + kRWaves - 1) / kRWaves), static_cast<uint32_t>(n_tokens));
     const bool vec = hidden % 4 == 0 && reinterpret_cast<uintptr_t>(w_r) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
-    uint32_t* err = ctx->counters + ctx->counter_words;
+    uint32_t* err = ctx->err_word;
     const bool lanes = vec && hidden % 256 == 0 && hidden <= 256u * 32u;
     const bool split = vec && hidden % 1024 == 0 && hidden <= 1024u * 8u;
     // table resolution (split kernel, up to kSelTabMaxExperts experts) or none
@@ -279,31 +287,31 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
         if (hidden <= 1024u * 2u)
             hipLaunchKernelGGL(router_split_kernel<2>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err,
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err,
                                st ? table : nullptr, st);
         else
             hipLaunchKernelGGL(router_split_kernel<8>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err,
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err,
                                st ? table : nullptr, st);
     } else if (lanes) {
         const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
         if (hidden <= 256u * 8u)
             hipLaunchKernelGGL(router_lanes_kernel<8>, grid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err);
         else
             hipLaunchKernelGGL(router_lanes_kernel<32>, grid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, ctx->counters, err);
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err);
     } else if (vec)
         hipLaunchKernelGGL(router_kernel<true>, grid, dim3(kRThreads), 0, s, w_r, bias, x,
                            static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden), static_cast<uint32_t>(k),
-                           renormalize, ids, weights, ws, ctx->counters, err);
+                           renormalize, ids, weights, ws, counters, err);
     else
         hipLaunchKernelGGL(router_kernel<false>, grid, dim3(kRThreads), 0, s, w_r, bias, x,
                            static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden), static_cast<uint32_t>(k),
-                           renormalize, ids, weights, ws, ctx->counters, err);
+                           renormalize, ids, weights, ws, counters, err);
     OBJ_HIP(hipGetLastError(), action);
     return 0;
 }
@@ -321,10 +329,7 @@ extern "C" int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta
     OBJ_TRY(check_ctx(ctx, "router_topk_device"));
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     hipStream_t s = resolve_stream(ctx, stream);
-    const size_t need = static_cast<size_t>(n_tokens) * kMaxExperts * 2 * sizeof(uint64_t);
-    void* ws = nullptr;
-    OBJ_TRY(ensure_workspace(ctx, s, kWsRouter, need, &ws));
     return launch_router(ctx, s, d_w_r, d_bias, d_x, n_tokens, n_experts, hidden, k, renormalize, d_ids,
-                         d_weights, static_cast<uint64_t*>(ws), nullptr, nullptr);
+                         d_weights, nullptr, nullptr);
     OBJ_GUARD_END
 }

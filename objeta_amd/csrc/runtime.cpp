@@ -54,25 +54,54 @@ hipStream_t resolve_stream(objeta_hip_context* ctx, objeta_hip_stream s) {
     return s ? static_cast<hipStream_t>(s) : ctx->streams[0];
 }
 
+static int32_t fail_if_capturing(hipStream_t stream, const char* action, const std::string& what) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    OBJ_HIP(hipStreamIsCapturing(stream, &st), "query stream capture status");
+    if (st != hipStreamCaptureStatusNone)
+        OBJ_FAIL(kUnsupported, action, what + " needed while capturing; run the call once outside capture first");
+    return 0;
+}
+
+int32_t stream_scratch(objeta_hip_context* ctx, hipStream_t stream, StreamScratch** out) {
+    for (StreamScratch* sc : ctx->scratch)
+        if (sc->stream == stream) {
+            *out = sc;
+            return 0;
+        }
+    OBJ_TRY(fail_if_capturing(stream, "create stream scratch", "scratch for a new stream"));
+    auto* sc = new StreamScratch();
+    sc->stream = stream;
+    const size_t bytes = kEpochWords * sizeof(uint32_t);
+    hipError_t e = hipMalloc(&sc->epochs, bytes);
+    // cleared on the caller's stream and waited for: a clear on the null stream is
+    // not ordered before kernels on the context's non-blocking streams
+    if (e == hipSuccess) e = hipMemsetAsync(sc->epochs, 0, bytes, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        if (sc->epochs) (void)hipFree(sc->epochs);
+        delete sc;
+        OBJ_FAIL(kDriver, "allocate router epoch counters", hipGetErrorString(e));
+    }
+    ctx->scratch.push_back(sc);
+    *out = sc;
+    return 0;
+}
+
 int32_t ensure_workspace(objeta_hip_context* ctx, hipStream_t stream, int slot, size_t bytes, void** out) {
-    Workspace& ws = ctx->ws[slot];
+    StreamScratch* sc = nullptr;
+    OBJ_TRY(stream_scratch(ctx, stream, &sc));
+    Workspace& ws = sc->ws[slot];
     if (ws.bytes >= bytes) {
         *out = ws.ptr;
         return 0;
     }
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    OBJ_HIP(hipStreamIsCapturing(stream, &st), "query stream capture status");
-    if (st != hipStreamCaptureStatusNone)
-        OBJ_FAIL(kUnsupported, "grow workspace",
-                 strf("workspace of %zu bytes needed while capturing (have %zu); run the "
-                      "call once outside capture first",
-                      bytes, ws.bytes));
+    OBJ_TRY(fail_if_capturing(stream, "grow workspace",
+                              strf("workspace of %zu bytes (have %zu)", bytes, ws.bytes)));
     size_t grow = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
     void* p = nullptr;
     OBJ_HIP(hipMalloc(&p, grow), "allocate workspace");
-    // cleared on the caller's stream and waited for: a clear on the null stream is
-    // not ordered before kernels on the context's non-blocking streams, and the
-    // epoch-tagged words and counters in a workspace must start at zero
+    // epoch-tagged words in a workspace must start at zero
     OBJ_HIP(hipMemsetAsync(p, 0, grow, stream), "clear workspace");
     OBJ_HIP(hipStreamSynchronize(stream), "clear workspace");
     if (ws.ptr) ctx->retired_ws.push_back(ws.ptr);
@@ -206,7 +235,6 @@ int32_t objeta_hip_init(const objeta_hip_init_options* opts, objeta_hip_context*
     auto* ctx = new objeta_hip_context();
     ctx->device = static_cast<int>(o.device_ordinal);
     ctx->info = info;
-    if (const char* v = std::getenv("OBJETA_HIP_EXPERTS_XCD")) ctx->experts_xcd = std::strcmp(v, "1") == 0;
     auto fail_cleanup = [&](int32_t rc) {
         objeta_hip_destroy(ctx);
         return rc;
@@ -231,13 +259,11 @@ int32_t objeta_hip_init(const objeta_hip_init_options* opts, objeta_hip_context*
         int32_t rc = set_error(kDriver, __FILE__, __LINE__, __func__, "create copy stream", hipGetErrorString(e));
         return fail_cleanup(rc);
     }
-    ctx->counter_words = 4096;
-    // counter_words self-resetting tickets, then the device error word
-    e = hipMalloc(&ctx->counters, (ctx->counter_words + 64) * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(ctx->counters, 0, (ctx->counter_words + 64) * sizeof(uint32_t));
+    e = hipMalloc(&ctx->err_word, 64 * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(ctx->err_word, 0, 64 * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
-        int32_t rc = set_error(kDriver, __FILE__, __LINE__, __func__, "allocate device counters", hipGetErrorString(e));
+        int32_t rc = set_error(kDriver, __FILE__, __LINE__, __func__, "allocate device error word", hipGetErrorString(e));
         return fail_cleanup(rc);
     }
     *out = ctx;
@@ -255,11 +281,16 @@ int32_t objeta_hip_destroy(objeta_hip_context* ctx) {
     objeta::detach_caches(ctx);
     for (hipStream_t s : ctx->streams) (void)hipStreamDestroy(s);
     if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
-    for (auto& w : ctx->ws)
-        if (w.ptr) (void)hipFree(w.ptr);
+    for (StreamScratch* sc : ctx->scratch) {
+        for (auto& w : sc->ws)
+            if (w.ptr) (void)hipFree(w.ptr);
+        if (sc->epochs) (void)hipFree(sc->epochs);
+        delete sc;
+    }
+    ctx->scratch.clear();
     for (void* p : ctx->retired_ws) (void)hipFree(p);
     if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
-    if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->err_word) (void)hipFree(ctx->err_word);
     (void)hipGetLastError();
     delete ctx;
     return 0;

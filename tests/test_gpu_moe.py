@@ -236,3 +236,40 @@ def test_moe_layer_router_then_experts(backend, fmt, hidden, inter, n, k, T, bia
         ref = orc.selected_moe(fmt, oracle_experts(fmt, experts), sel, xs[t], hidden, inter, hidden)
         assert_moe_close(out[t] - xs[t], ref)
     del keep
+
+
+def test_moe_layer_two_streams_in_flight(backend):
+    """Two layer calls on two streams of one context, both enqueued before one
+    synchronize: each stream has its own router epochs and workspaces, so each
+    result equals the oracle's for its own input."""
+    fmt, hidden, inter, n, k, T = Q4, 2048, 768, 64, 8, 2
+    pool = make_experts(fmt, 12, hidden, inter, hidden, 23, gen="gauss")
+    experts = [pool[i % len(pool)] for i in range(n)]
+    table, keep = device_table(backend, fmt, experts)
+    w_r = orc.gauss(n * hidden, 41, 0.02)
+    d_wr = backend.to_device(w_r)
+    moe = MoeExecutor(backend)
+    runs = []
+    for si in range(2):
+        xs = np.stack([orc.gauss(hidden, 300 + 10 * si + t, 1.0) for t in range(T)])
+        bufs = dict(x=backend.to_device(xs.ravel()), out=backend.alloc(4 * T * hidden), ids=backend.alloc(4 * T * k),
+                    w=backend.alloc(4 * T * k))
+        runs.append((xs, bufs))
+    backend.synchronize()
+    for rep in range(3):
+        for si, (xs, b) in enumerate(runs):
+            moe.layer_device(fmt, table, d_wr, None, k, T, b["x"], b["x"], b["out"], b["ids"], b["w"], hidden, inter,
+                             hidden, stream=backend.stream(si))
+        for si in range(2):
+            backend.synchronize(backend.stream(si))
+        for si, (xs, b) in enumerate(runs):
+            ids = b["ids"].download(np.uint32, T * k).reshape(T, k)
+            out = b["out"].download(np.float32, T * hidden).reshape(T, hidden)
+            for t in range(T):
+                rid, rw, _, _ = orc.router(w_r, xs[t], n, hidden, k, renormalize=True)
+                assert np.array_equal(ids[t], rid), (rep, si, t)
+                sel = [(int(i), float(v)) for i, v in zip(rid, rw)]
+                ref = orc.selected_moe(fmt, oracle_experts(fmt, experts), sel, xs[t], hidden, inter, hidden)
+                assert_moe_close(out[t] - xs[t], ref)
+    assert moe.device_error() == 0
+    del keep
