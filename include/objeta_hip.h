@@ -263,6 +263,21 @@ int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, 
                                        uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
                                        float swiglu_limit);
 
+/* objeta_hip_moe_selected_device without any allocation, for callers that cannot
+ * allocate device memory (code under graph capture before a first eager call,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Same arguments and results as objeta_hip_moe_selected_device (the
+ * same kernels); the activations [n_tokens * k][intermediate] live in a static
+ * device array of 2^20 floats (4 MiB) per device, held until the process ends.
+ * n_tokens * k * intermediate > 2^20 fails with InvalidInput. Every call on a
+ * device shares that array: calls that overlap on one device race. */
+int32_t objeta_hip_moe_selected_device_noalloc(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                               const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                               const uint32_t* d_ids, const float* d_weights, uint64_t n_tokens,
+                                               uint64_t k, const float* d_x, const float* d_residual, float* d_out,
+                                               uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                               float swiglu_limit);
+
 /* objeta_hip_moe_selected_device for a batch whose tokens share experts: the
  * (token, slot) assignments are grouped by expert on the device and every selected
  * expert's gate, up and down matrices are read once for all of its tokens, with

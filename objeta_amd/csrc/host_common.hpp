@@ -105,6 +105,7 @@ struct objeta_hip_context {
     std::vector<void*> caches;                    // live caches created on this context
     size_t host_stage_bytes = 0;
     uint32_t* err_word = nullptr;  // device error word (bits set by kernels, read by objeta_hip_device_error)
+    float* static_act = nullptr;   // device address of this device's static activation scratch
     std::mutex mu;
 };
 

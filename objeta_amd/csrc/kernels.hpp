@@ -43,6 +43,12 @@ int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, 
                         const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim,
                         const objeta_hip_expert_ptrs* sel = nullptr);
 
+// Looks up (once per device, with the context's device current) the device address
+// of the static activation scratch of objeta_hip_moe_selected_device_noalloc and
+// keeps it in ctx->static_act.
+constexpr uint64_t kStaticActFloats = uint64_t(1) << 20;
+int32_t bind_static_scratch(objeta_hip_context* ctx);
+
 int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
                         float** out);
 

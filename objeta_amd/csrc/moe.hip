@@ -616,6 +616,38 @@ int32_t launch_moe_selected(objeta_hip_context* ctx, int32_t format, hipStream_t
                            sel);
 }
 
+// ------------------------------------------------ static activation scratch
+// The activations [n_tokens * k][intermediate] of objeta_hip_moe_selected_device_noalloc
+// live in this file-scope array (4 MiB on every device the library runs on, held
+// until the process ends) instead of a context workspace. In host code `scratch`
+// names a host-side stand-in, not the device array: only the address that
+// hipGetSymbolAddress returns (per device, with that device current) is passed to
+// kernels. Every call on a device shares the array; calls that overlap on one
+// device race. Nothing in it needs clearing: gate/up writes every activation that
+// down reads.
+static __device__ __align__(256) float scratch[kStaticActFloats];
+
+namespace {
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int32_t bind_static_scratch(objeta_hip_context* ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        OBJ_FAIL(kUnsupported, "bind static scratch", strf("device ordinal %d >= %d", ctx->device, kMaxDevices));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[ctx->device]) {
+        void* p = nullptr;
+        OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+        OBJ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(static activation scratch)");
+        if (!p) OBJ_FAIL(kDriver, "bind static scratch", "hipGetSymbolAddress returned NULL");
+        g_scratch_ptr[ctx->device] = p;
+    }
+    ctx->static_act = static_cast<float*>(g_scratch_ptr[ctx->device]);
+    return 0;
+}
+
 int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
                         float** out) {
     void* p = nullptr;
@@ -645,6 +677,29 @@ int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, 
     OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k ? k : 1, intermediate ? intermediate : 1, &act));
     return launch_moe_selected(ctx, format, s, d_table, n_table, d_ids, d_weights, n_tokens, k, d_x, d_residual,
                                d_out, hidden, intermediate, out_dim, swiglu_limit, act, nullptr);
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_moe_selected_device_noalloc(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                               const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                               const uint32_t* d_ids, const float* d_weights, uint64_t n_tokens,
+                                               uint64_t k, const float* d_x, const float* d_residual, float* d_out,
+                                               uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                               float swiglu_limit) {
+    OBJ_GUARD_BEGIN
+    const char* action = "moe_selected_device_noalloc";
+    OBJ_TRY(check_ctx(ctx, action));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, hidden, intermediate, out_dim));
+    if (n_tokens == 0 || out_dim == 0) return 0;
+    if (n_tokens * k * intermediate > kStaticActFloats)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("n_tokens * k * intermediate = %llu exceeds the static scratch of %llu floats",
+                      (unsigned long long)(n_tokens * k * intermediate), (unsigned long long)kStaticActFloats));
+    if (!ctx->static_act) OBJ_FAIL(kInternal, action, "static scratch not bound");
+    return launch_moe_selected(ctx, format, s, d_table, n_table, d_ids, d_weights, n_tokens, k, d_x, d_residual,
+                               d_out, hidden, intermediate, out_dim, swiglu_limit, ctx->static_act, nullptr);
     OBJ_GUARD_END
 }
 

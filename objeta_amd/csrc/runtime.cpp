@@ -6,6 +6,7 @@
 #include <string>
 
 #include "host_common.hpp"
+#include "kernels.hpp"
 
 namespace objeta {
 
@@ -258,6 +259,11 @@ int32_t objeta_hip_init(const objeta_hip_init_options* opts, objeta_hip_context*
     if (e != hipSuccess) {
         int32_t rc = set_error(kDriver, __FILE__, __LINE__, __func__, "create copy stream", hipGetErrorString(e));
         return fail_cleanup(rc);
+    }
+    {
+        // the device address of the no-allocation entry point's scratch array
+        const int32_t rc = bind_static_scratch(ctx);
+        if (rc != 0) return fail_cleanup(rc);
     }
     e = hipMalloc(&ctx->err_word, 64 * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(ctx->err_word, 0, 64 * sizeof(uint32_t));
