@@ -40,16 +40,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBPS = 8000.0
 
-
-def zipf_bias(n_experts: int, s: float, seed: int) -> np.ndarray:
-    """ln of the Zipf(s) pmf over ranks 1..n, assigned to experts by a seeded permutation."""
-    ranks = np.arange(1, n_experts + 1, dtype=np.float64)
-    pmf = ranks ** (-s)
-    pmf /= pmf.sum()
-    perm = np.random.default_rng(seed).permutation(n_experts)
-    bias = np.empty(n_experts, np.float64)
-    bias[perm] = np.log(pmf)
-    return bias.astype(np.float32)
+from objeta_amd.workloads import zipf_bias  # noqa: E402
 
 
 def cpu_model() -> str:

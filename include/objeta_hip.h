@@ -226,6 +226,13 @@ int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta_hip_stream
                                       uint64_t k, int32_t renormalize, uint32_t* d_ids,
                                       float* d_weights);
 
+/* y[i] = exp(x[i]) as the router's softmax evaluates it on the device: glibc's
+ * expf (the f32::exp of the reference's cpu_router, deepseek_single_layer_moe.rs:
+ * 687-743), bit for bit. Exposed so that tests can compare it with the host's
+ * expf; no reference counterpart. n <= 2^32. */
+int32_t objeta_hip_router_softmax_exp_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                             const float* d_x, float* d_y, uint64_t n);
+
 /* --------------------------------------------------------------- MoE path */
 /* Device addresses of one expert's projections: ExpertWeights (moe.rs:13-18) for
  * the block formats, DeepSeekFp4ExpertWeights (moe.rs:27-35) for FP4. gate and up
@@ -262,6 +269,20 @@ int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, 
                                        uint64_t k, const float* d_x, const float* d_residual, float* d_out,
                                        uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
                                        float swiglu_limit);
+
+/* objeta_hip_moe_selected_device plus a shared expert: d_shared (a device pointer to
+ * one objeta_hip_expert_ptrs, or NULL for none) is applied to every token with
+ * weight 1.0 after the routed sum,
+ *   out_t = residual_t + sum_j d_weights[t*k + j] * down_j(act_j) + down_s(act_s),
+ * as execute_selected_moe_official_routed_fp4_cuda adds its shared expert
+ * (moe.rs:1552-1600: weighted_accum with weight 1.0 after the routed experts). Same
+ * format, shapes and limits as the routed experts. */
+int32_t objeta_hip_moe_selected_shared_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                              const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                              const objeta_hip_expert_ptrs* d_shared, const uint32_t* d_ids,
+                                              const float* d_weights, uint64_t n_tokens, uint64_t k, const float* d_x,
+                                              const float* d_residual, float* d_out, uint64_t hidden,
+                                              uint64_t intermediate, uint64_t out_dim, float swiglu_limit);
 
 /* objeta_hip_moe_selected_device without any allocation, for callers that cannot
  * allocate device memory (code under graph capture before a first eager call,
@@ -325,6 +346,16 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
                                     const float* d_residual, float* d_out, uint32_t* d_ids_out,
                                     float* d_weights_out, uint64_t hidden, uint64_t intermediate,
                                     uint64_t out_dim, float swiglu_limit);
+
+/* objeta_hip_moe_layer_device with the shared expert of
+ * objeta_hip_moe_selected_shared_device (d_shared NULL: none). */
+int32_t objeta_hip_moe_layer_shared_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                           const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
+                                           const objeta_hip_expert_ptrs* d_shared, const float* d_router_w,
+                                           const float* d_router_bias, uint64_t k, int32_t renormalize,
+                                           uint64_t n_tokens, const float* d_x, const float* d_residual, float* d_out,
+                                           uint32_t* d_ids_out, float* d_weights_out, uint64_t hidden,
+                                           uint64_t intermediate, uint64_t out_dim, float swiglu_limit);
 
 /* Reads and clears the context's device error word (non-zero after a kernel met
  * an expert id outside its table). Synchronises the context's streams. */

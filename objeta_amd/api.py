@@ -152,6 +152,38 @@ class DeviceBuffer:
         return out
 
 
+class PinnedHostBuffer:
+    """PinnedHostBuffer (memory.rs:31-80): page-locked host memory of the backend's
+    device, so that copies from it run asynchronously at PCIe rate. `array(dtype)`
+    views it as a numpy array; free it (or let it be collected) before the backend
+    closes."""
+
+    def __init__(self, backend: "HipBackend", nbytes: int):
+        self.backend = backend
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(backend.L.objeta_hip_alloc_pinned_host(backend.ctx, self.nbytes, C.byref(p)))
+        self.ptr = p.value or 0
+
+    def array(self, dtype=np.uint8, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = (self.nbytes - offset) // dt.itemsize if count is None else int(count)
+        assert offset + n * dt.itemsize <= self.nbytes
+        buf = (C.c_uint8 * (n * dt.itemsize)).from_address(self.ptr + offset)
+        return np.frombuffer(buf, dtype=dt, count=n)
+
+    def free(self) -> None:
+        if self.ptr and self.backend.ctx:
+            check(self.backend.L.objeta_hip_free_pinned_host(self.backend.ctx, C.c_void_p(self.ptr)))
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class HipBackend:
     """CudaBackend (context.rs:72-165): one device, a pool of streams."""
 
@@ -326,11 +358,13 @@ class MoeExecutor:
 
     def selected_device(self, fmt, table: ExpertTable, d_ids, d_weights, n_tokens: int, k: int, d_x,
                         d_residual, d_out, hidden: int, inter: int, out_dim: int,
-                        swiglu_limit: float = 0.0, stream=None) -> None:
-        check(self.L.objeta_hip_moe_selected_device(
-            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr_or_none(d_ids),
-            _addr(d_weights), n_tokens, k, _addr(d_x), _addr_or_none(d_residual), _addr(d_out), hidden,
-            inter, out_dim, swiglu_limit))
+                        swiglu_limit: float = 0.0, stream=None, shared: "ExpertTable | None" = None) -> None:
+        """shared: a one-entry ExpertTable applied to every token with weight 1.0 after
+        the routed sum (moe.rs:1552-1600)."""
+        check(self.L.objeta_hip_moe_selected_shared_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, None if shared is None else shared.addr(),
+            _addr_or_none(d_ids), _addr(d_weights), n_tokens, k, _addr(d_x), _addr_or_none(d_residual),
+            _addr(d_out), hidden, inter, out_dim, swiglu_limit))
 
     def grouped_device(self, fmt, table: ExpertTable, d_ids, d_weights, n_tokens: int, k: int, d_x,
                        d_residual, d_out, hidden: int, inter: int, out_dim: int,
@@ -358,10 +392,10 @@ class MoeExecutor:
     def layer_device(self, fmt, table: ExpertTable, d_router_w, d_router_bias, k: int, n_tokens: int,
                      d_x, d_residual, d_out, d_ids_out, d_weights_out, hidden: int, inter: int,
                      out_dim: int, renormalize: bool = True, swiglu_limit: float = 0.0,
-                     stream=None) -> None:
-        check(self.L.objeta_hip_moe_layer_device(
-            self.backend.ctx, int(fmt), stream, table.addr(), table.n, _addr(d_router_w),
-            _addr_or_none(d_router_bias), k, 1 if renormalize else 0, n_tokens, _addr(d_x),
+                     stream=None, shared: "ExpertTable | None" = None) -> None:
+        check(self.L.objeta_hip_moe_layer_shared_device(
+            self.backend.ctx, int(fmt), stream, table.addr(), table.n, None if shared is None else shared.addr(),
+            _addr(d_router_w), _addr_or_none(d_router_bias), k, 1 if renormalize else 0, n_tokens, _addr(d_x),
             _addr_or_none(d_residual), _addr(d_out), _addr(d_ids_out), _addr(d_weights_out), hidden,
             inter, out_dim, swiglu_limit))
 

@@ -34,14 +34,16 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
                            float* act, uint64_t hidden, uint64_t inter, float limit,
-                           const objeta_hip_expert_ptrs* sel = nullptr);
+                           const objeta_hip_expert_ptrs* sel = nullptr, const objeta_hip_expert_ptrs* shared = nullptr);
 
 // sel (optional): the assignments' table entries as the router resolved them; the
-// kernels then skip the id and table lookups.
+// kernels then skip the id and table lookups. shared (optional, a device pointer to
+// one table entry): the shared expert, an extra slot per token with weight 1 added
+// after the routed sum; act then holds k + 1 slots per token.
 int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                         uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                         const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim,
-                        const objeta_hip_expert_ptrs* sel = nullptr);
+                        const objeta_hip_expert_ptrs* sel = nullptr, const objeta_hip_expert_ptrs* shared = nullptr);
 
 // Looks up (once per device, with the context's device current) the device address
 // of the static activation scratch of objeta_hip_moe_selected_device_noalloc and

@@ -64,28 +64,33 @@ __device__ __forceinline__ void stage_vec_wave(float* __restrict__ dst, const fl
 // ------------------------------------------------------------------ gate/up
 // grid.x = n_assign * blocks_per_assign, block = 256 (4 waves). A wave owns
 // g = 64 / lpr row slots (lpr lanes each) times U rows; lane lp of a slot owns
-// pairs lp + c * lpr, c < CH (pairs == CH * lpr).
+// pairs lp + c * lpr, c < CH (pairs == CH * lpr). A token has kk slots: k routed
+// ones (ids, sel and wts have stride k) and, when kk > k, the shared expert in
+// slot k; assignment a = t * kk + j indexes the activations.
 template <class R, int U, int CH>
 __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
     uint32_t lpr, uint32_t blocks_per_assign, float limit, uint32_t* __restrict__ err,
-    const objeta_hip_expert_ptrs* __restrict__ sel) {
+    const objeta_hip_expert_ptrs* __restrict__ sel, uint32_t kk, const objeta_hip_expert_ptrs* __restrict__ shared) {
     extern __shared__ float lds[];
     const uint32_t a = blockIdx.x / blocks_per_assign;
     const uint32_t rb = blockIdx.x - a * blocks_per_assign;
-    const uint32_t t = a / k;
+    const uint32_t t = a / kk;
+    const uint32_t j = a - t * kk;
+    const bool is_shared = j >= k;
+    const uint32_t ar = t * k + (is_shared ? 0u : j);  // routed index into ids / sel
     // The expert id and table entry come through scalar loads, issued first; the
     // activations are requested while they are in flight and before the weights,
     // so that writing them to LDS waits for them alone.
     // sel: the router resolved the assignments to table entries (valid ids)
     uint32_t e = 0;
-    const bool ok = sel ? true : expert_of(ids, a, n_table, err, e);
+    const bool ok = (is_shared || sel) ? true : expert_of(ids, ar, n_table, err, e);
     constexpr int kXV = 8;
     const bool x_regs = hidden <= 4u * kXV * kThreads;
     XRegs<kXV> xr;
     if (x_regs) stage_x_issue<1, kXV>(x + static_cast<size_t>(t) * hidden, hidden, xr);
-    const objeta_hip_expert_ptrs P = sel ? sel[a] : table[e];
+    const objeta_hip_expert_ptrs P = is_shared ? *shared : (sel ? sel[ar] : table[e]);
     const R gm = RowsOf<R>::make(P.gate, P.gate_scale, hidden);
     const R um = RowsOf<R>::make(P.up, P.up_scale, hidden);
 
@@ -142,15 +147,19 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
 }
 
 // -------------------------------------------------------------------- down
-// grid.x = n_tokens * blocks_per_token, block = ceil(k / JW) waves. All waves of
+// grid.x = n_tokens * blocks_per_token, block = ceil(kk / JW) waves. All waves of
 // a block cover the same g * U output rows; wave w takes slots [w*JW, w*JW+JW).
-// LDS: red [k][g*U] row sums, then one padded activation slot per (wave, jj).
+// Slots j < k are routed (ids, sel, wts with stride k); slot k, when kk > k, is the
+// shared expert with weight 1, combined last as the reference adds it after the
+// routed sum. LDS: red [kk][g*U] row sums, then one padded activation slot per
+// (wave, jj).
 template <class R, int U, int CH, int JW>
 __global__ __launch_bounds__(1024) void moe_down_kernel(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ wts, const float* __restrict__ act, const float* resid, float* out,
     uint32_t inter, uint32_t out_dim, uint32_t k, uint32_t lpr, uint32_t blocks_per_token,
-    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ sel) {
+    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ sel, uint32_t kk,
+    const objeta_hip_expert_ptrs* __restrict__ shared) {
     extern __shared__ float lds[];
     const uint32_t t = blockIdx.x / blocks_per_token;
     const uint32_t rb = blockIdx.x - t * blocks_per_token;
@@ -162,7 +171,7 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
     const uint32_t rows_blk = gs * U;
     const uint32_t row0 = rb * rows_blk;
     float* red = lds;
-    float* xst = lds + ((k * rows_blk + 3u) & ~3u) + wave * JW * pairs * kPad;
+    float* xst = lds + ((kk * rows_blk + 3u) & ~3u) + wave * JW * pairs * kPad;
 
     // the wave's activation slots are requested before the weights (loads complete
     // in order, so the LDS writes below then wait for the activations alone): lane l
@@ -176,8 +185,8 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
 #pragma unroll
         for (int jj = 0; jj < JW; ++jj) {
             const uint32_t j = wave * JW + jj;
-            const uint32_t jc = j < k ? j : k - 1;
-            const gptr<f32x4> src = as_global(reinterpret_cast<const f32x4*>(act + (static_cast<size_t>(t) * k + jc) * inter));
+            const uint32_t jc = j < kk ? j : kk - 1;
+            const gptr<f32x4> src = as_global(reinterpret_cast<const f32x4*>(act + (static_cast<size_t>(t) * kk + jc) * inter));
 #pragma unroll
             for (int q = 0; q < kAV; ++q) {
                 const uint32_t i = lane + static_cast<uint32_t>(q) * 64;
@@ -194,11 +203,13 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
     // every slot's id, then every slot's table entry, then the weights: one scalar
     // round trip per step rather than per slot
     uint32_t es[JW];
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) es[jj] = 0;
     if (sel) {  // the router resolved the assignments to table entries (valid ids)
 #pragma unroll
         for (int jj = 0; jj < JW; ++jj) {
             const uint32_t j = wave * JW + jj;
-            const objeta_hip_expert_ptrs* f = sel + (t * k + (j < k ? j : k - 1));
+            const objeta_hip_expert_ptrs* f = (j >= k && j < kk) ? shared : sel + (t * k + (j < k ? j : k - 1));
             ok[jj] = true;
             m[jj] = RowsOf<R>::make(f->down, f->down_scale, inter);
         }
@@ -207,11 +218,15 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
         for (int jj = 0; jj < JW; ++jj) {
             const uint32_t j = wave * JW + jj;
             const uint32_t jc = j < k ? j : k - 1;
-            ok[jj] = expert_of(ids, t * k + jc, n_table, err, es[jj]);
+            ok[jj] = (j >= k && j < kk) ? true : expert_of(ids, t * k + jc, n_table, err, es[jj]);
             es[jj] = __builtin_amdgcn_readfirstlane(es[jj]);
         }
 #pragma unroll
-        for (int jj = 0; jj < JW; ++jj) m[jj] = RowsOf<R>::make(table[es[jj]].down, table[es[jj]].down_scale, inter);
+        for (int jj = 0; jj < JW; ++jj) {
+            const uint32_t j = wave * JW + jj;
+            const objeta_hip_expert_ptrs* f = (j >= k && j < kk) ? shared : table + es[jj];
+            m[jj] = RowsOf<R>::make(f->down, f->down_scale, inter);
+        }
     }
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
@@ -236,8 +251,8 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
             }
         } else {
             const uint32_t j = wave * JW + jj;
-            const uint32_t jc = j < k ? j : k - 1;
-            stage_vec_wave(xst + jj * pairs * kPad, act + (static_cast<size_t>(t) * k + jc) * inter, inter, lane);
+            const uint32_t jc = j < kk ? j : kk - 1;
+            stage_vec_wave(xst + jj * pairs * kPad, act + (static_cast<size_t>(t) * kk + jc) * inter, inter, lane);
         }
     }
     __syncthreads();
@@ -266,7 +281,7 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const float v = row_reduce(acc[u][0], lp, lpr);
-            if (slot < gs && lp == 0 && j < k)
+            if (slot < gs && lp == 0 && j < kk)
                 red[j * rows_blk + static_cast<uint32_t>(u) * gs + slot] = ok[jj] ? v : __builtin_nanf("");
         }
     }
@@ -278,6 +293,7 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
             const size_t o = static_cast<size_t>(t) * out_dim + r;
             float acc = resid ? resid[o] : 0.0f;
             for (uint32_t j = 0; j < k; ++j) acc = __builtin_fmaf(wts[t * k + j], red[j * rows_blk + threadIdx.x], acc);
+            if (kk > k) acc += red[k * rows_blk + threadIdx.x];  // the shared expert, weight 1
             out[o] = acc;
         }
     }
@@ -332,20 +348,23 @@ __device__ __forceinline__ float row_dot_general(const uint8_t* __restrict__ w, 
     return wave_reduce(acc);
 }
 
-// grid.x = ceil(n_assign * inter / 4); one wave per (assignment, row).
+// grid.x = ceil(n_assign * inter / 4); one wave per (assignment, row). Slots as
+// in moe_gate_up_kernel (kk per token, the shared expert in slot k when kk > k).
 template <int F>
 __global__ __launch_bounds__(kThreads) void moe_gate_up_general(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
-    uint32_t n_assign, float limit, uint32_t* __restrict__ err) {
+    uint32_t n_assign, float limit, uint32_t* __restrict__ err, uint32_t kk,
+    const objeta_hip_expert_ptrs* __restrict__ shared) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t item = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (item >= n_assign * inter) return;
     const uint32_t a = item / inter, r = item - a * inter;
-    uint32_t e;
-    const bool ok = expert_of(ids, a, n_table, err, e);
-    const objeta_hip_expert_ptrs P = table[e];
-    const float* xt = x + static_cast<size_t>(a / k) * hidden;
+    const uint32_t t = a / kk, j = a - t * kk;
+    uint32_t e = 0;
+    const bool ok = j >= k ? true : expert_of(ids, t * k + j, n_table, err, e);
+    const objeta_hip_expert_ptrs P = j >= k ? *shared : table[e];
+    const float* xt = x + static_cast<size_t>(t) * hidden;
     const float g = row_dot_general<F>(static_cast<const uint8_t*>(P.gate), static_cast<const uint8_t*>(P.gate_scale),
                                        r, hidden, xt, lane);
     const float u = row_dot_general<F>(static_cast<const uint8_t*>(P.up), static_cast<const uint8_t*>(P.up_scale), r,
@@ -358,21 +377,23 @@ template <int F>
 __global__ __launch_bounds__(kThreads) void moe_down_general(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ wts, const float* __restrict__ act, const float* resid, float* out, uint32_t inter,
-    uint32_t out_dim, uint32_t k, uint32_t n_tokens, uint32_t* __restrict__ err) {
+    uint32_t out_dim, uint32_t k, uint32_t n_tokens, uint32_t* __restrict__ err, uint32_t kk,
+    const objeta_hip_expert_ptrs* __restrict__ shared) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t item = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (item >= n_tokens * out_dim) return;
     const uint32_t t = item / out_dim, r = item - t * out_dim;
     const size_t o = static_cast<size_t>(t) * out_dim + r;
     float acc = resid ? resid[o] : 0.0f;
-    for (uint32_t j = 0; j < k; ++j) {
-        uint32_t e;
-        const bool ok = expert_of(ids, t * k + j, n_table, err, e);
-        const objeta_hip_expert_ptrs P = table[e];
+    for (uint32_t j = 0; j < kk; ++j) {
+        uint32_t e = 0;
+        const bool ok = j >= k ? true : expert_of(ids, t * k + j, n_table, err, e);
+        const objeta_hip_expert_ptrs P = j >= k ? *shared : table[e];
         const float v = row_dot_general<F>(static_cast<const uint8_t*>(P.down),
                                            static_cast<const uint8_t*>(P.down_scale), r, inter,
-                                           act + (static_cast<size_t>(t) * k + j) * inter, lane);
-        acc = __builtin_fmaf(wts[t * k + j], ok ? v : __builtin_nanf(""), acc);
+                                           act + (static_cast<size_t>(t) * kk + j) * inter, lane);
+        const float w = j >= k ? 1.0f : wts[t * k + j];
+        acc = __builtin_fmaf(w, ok ? v : __builtin_nanf(""), acc);
     }
     if (lane == 0) out[o] = acc;
 }
@@ -386,8 +407,12 @@ using namespace dev;
 
 constexpr uint32_t kMaxK = 32;  // selection slots per token (router's top-k bound)
 
+// k routed slots per token plus, when `shared` is set, the shared expert in slot k:
+// kk = k + (shared != nullptr) slots in all.
 struct MoeShape {
     uint32_t n_table, n_tokens, k, hidden, inter, out_dim;
+    const objeta_hip_expert_ptrs* shared = nullptr;
+    uint32_t kk() const { return k + (shared ? 1u : 0u); }
 };
 
 size_t max_lds(const objeta_hip_context* ctx) {
@@ -402,10 +427,11 @@ hipError_t gate_up_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, cons
     const uint32_t gs = 64 / lpr;
     const uint32_t rows_blk = kWaves * gs * U;
     const uint32_t bpa = (sh.inter + rows_blk - 1) / rows_blk;
-    const uint32_t n_assign = sh.n_tokens * sh.k;
+    const uint32_t n_assign = sh.n_tokens * sh.kk();
     const size_t lds = static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 4 * sizeof(float);
     hipLaunchKernelGGL((moe_gate_up_kernel<R, U, CH>), dim3(n_assign * bpa), dim3(kThreads), lds, s, table,
-                       sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k, lpr, bpa, limit, err, sel);
+                       sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k, lpr, bpa, limit, err, sel, sh.kk(),
+                       sh.shared);
     return hipGetLastError();
 }
 
@@ -416,19 +442,20 @@ hipError_t down_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, const u
     const uint32_t gs = 64 / lpr;
     const uint32_t rows_blk = gs * U;
     const uint32_t bpt = (sh.out_dim + rows_blk - 1) / rows_blk;
-    const uint32_t waves = (sh.k + JW - 1) / JW;
-    const size_t lds = (((sh.k * rows_blk + 3u) & ~3u) + static_cast<size_t>(waves) * JW * (sh.inter >> 6) * kPad) *
+    const uint32_t waves = (sh.kk() + JW - 1) / JW;
+    const size_t lds = (((sh.kk() * rows_blk + 3u) & ~3u) + static_cast<size_t>(waves) * JW * (sh.inter >> 6) * kPad) *
                        sizeof(float);
     hipLaunchKernelGGL((moe_down_kernel<R, U, CH, JW>), dim3(sh.n_tokens * bpt), dim3(waves * 64), lds, s, table,
-                       sh.n_table, ids, wts, act, resid, out, sh.inter, sh.out_dim, sh.k, lpr, bpt, err, sel);
+                       sh.n_table, ids, wts, act, resid, out, sh.inter, sh.out_dim, sh.k, lpr, bpt, err, sel, sh.kk(),
+                       sh.shared);
     return hipGetLastError();
 }
 
 size_t down_lds_bytes(const MoeShape& sh, uint32_t jw, uint32_t u) {
     const uint32_t lpr = pick_lpr(sh.inter >> 6);
     const uint32_t rows_blk = (64 / lpr) * u;
-    const uint32_t waves = (sh.k + jw - 1) / jw;
-    return (((sh.k * rows_blk + 3u) & ~3u) + static_cast<size_t>(waves) * jw * (sh.inter >> 6) * kPad) * sizeof(float);
+    const uint32_t waves = (sh.kk() + jw - 1) / jw;
+    return (((sh.kk() * rows_blk + 3u) & ~3u) + static_cast<size_t>(waves) * jw * (sh.inter >> 6) * kPad) * sizeof(float);
 }
 
 // Dispatch on chunks per lane (pairs / lpr).
@@ -441,7 +468,7 @@ hipError_t launch_gate_up_rows(hipStream_t s, const objeta_hip_expert_ptrs* tabl
     const uint32_t ch = pairs / lpr;
     // two rows per slot when that still leaves a few workgroups per CU
     const uint32_t gs = 64 / lpr;
-    const uint64_t blocks_u2 = static_cast<uint64_t>(sh.n_tokens) * sh.k * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2));
+    const uint64_t blocks_u2 = static_cast<uint64_t>(sh.n_tokens) * sh.kk() * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2));
     const bool u2 = blocks_u2 >= 2ull * cus && ch <= 2;
     switch (ch) {
         case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel)
@@ -481,15 +508,15 @@ hipError_t launch_general(hipStream_t s, const objeta_hip_expert_ptrs* table, co
                           const float* x, float* act, const float* resid, float* out, const MoeShape& sh,
                           float limit, uint32_t* err, int phase) {
     if (phase == 0) {
-        const uint64_t items = static_cast<uint64_t>(sh.n_tokens) * sh.k * sh.inter;
+        const uint64_t items = static_cast<uint64_t>(sh.n_tokens) * sh.kk() * sh.inter;
         hipLaunchKernelGGL((moe_gate_up_general<F>), dim3(static_cast<uint32_t>((items + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, s, table, sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k,
-                           sh.n_tokens * sh.k, limit, err);
+                           sh.n_tokens * sh.kk(), limit, err, sh.kk(), sh.shared);
     } else {
         const uint64_t items = static_cast<uint64_t>(sh.n_tokens) * sh.out_dim;
         hipLaunchKernelGGL((moe_down_general<F>), dim3(static_cast<uint32_t>((items + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, s, table, sh.n_table, ids, wts, act, resid, out, sh.inter, sh.out_dim,
-                           sh.k, sh.n_tokens, err);
+                           sh.k, sh.n_tokens, err, sh.kk(), sh.shared);
     }
     return hipGetLastError();
 }
@@ -532,13 +559,14 @@ MoeShape shape_of(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidd
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
                            float* act, uint64_t hidden, uint64_t inter, float limit,
-                           const objeta_hip_expert_ptrs* sel) {
+                           const objeta_hip_expert_ptrs* sel, const objeta_hip_expert_ptrs* shared) {
     const char* action = "launch MoE gate/up";
     OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, hidden, inter, 1));
     if (n_tokens == 0) return 0;
     if (!table || !x || !act) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     if (reinterpret_cast<uintptr_t>(x) % 16) OBJ_FAIL(kInvalidInput, action, "x must be 16-byte aligned");
-    const MoeShape sh = shape_of(n_table, n_tokens, k, hidden, inter, 1);
+    MoeShape sh = shape_of(n_table, n_tokens, k, hidden, inter, 1);
+    sh.shared = shared;
     uint32_t* err = ctx->err_word;
     const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
     const bool fast = fast_shape(sh.hidden) && static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 16 <= max_lds(ctx);
@@ -565,21 +593,22 @@ int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t 
 int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                         uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                         const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim,
-                        const objeta_hip_expert_ptrs* sel) {
+                        const objeta_hip_expert_ptrs* sel, const objeta_hip_expert_ptrs* shared) {
     const char* action = "launch MoE down + combine";
     OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, 32, inter, out_dim));
     if (n_tokens == 0 || out_dim == 0) return 0;
     if (!table || !wts || !act || !out) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     if (reinterpret_cast<uintptr_t>(act) % 16) OBJ_FAIL(kInvalidInput, action, "act must be 16-byte aligned");
-    const MoeShape sh = shape_of(n_table, n_tokens, k, 32, inter, out_dim);
+    MoeShape sh = shape_of(n_table, n_tokens, k, 32, inter, out_dim);
+    sh.shared = shared;
     uint32_t* err = ctx->err_word;
     uint32_t jw = 0;
     if (fast_shape(sh.inter)) {
         // one token: one selection slot per wave (k waves per workgroup), measured
         // 0.2 us faster per Qwen3-A3B layer; batches: two slots per wave (16 tokens:
         // 4.3 against 4.7 ms per 48-layer step)
-        const bool jw1 = down_lds_bytes(sh, 1, 1) <= max_lds(ctx) && sh.k <= 16;
-        const bool jw2 = down_lds_bytes(sh, 2, 1) <= max_lds(ctx) && (sh.k + 1) / 2 <= 16;
+        const bool jw1 = down_lds_bytes(sh, 1, 1) <= max_lds(ctx) && sh.kk() <= 16;
+        const bool jw2 = down_lds_bytes(sh, 2, 1) <= max_lds(ctx) && (sh.kk() + 1) / 2 <= 16;
         if (sh.n_tokens == 1 && jw1) jw = 1;
         else if (jw2) jw = 2;
         else if (jw1) jw = 1;
@@ -608,12 +637,13 @@ int32_t launch_moe_selected(objeta_hip_context* ctx, int32_t format, hipStream_t
                             const objeta_hip_expert_ptrs* table, uint64_t n_table, const uint32_t* ids,
                             const float* wts, uint64_t n_tokens, uint64_t k, const float* x, const float* resid,
                             float* out, uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit, float* act,
-                            const objeta_hip_expert_ptrs* sel) {
+                            const objeta_hip_expert_ptrs* sel, const objeta_hip_expert_ptrs* shared) {
     OBJ_TRY(validate_moe("launch selected-expert MoE", format, n_table, n_tokens, k, hidden, inter, out_dim));
     if (n_tokens == 0 || out_dim == 0) return 0;
-    OBJ_TRY(launch_moe_gate_up(ctx, format, s, table, n_table, ids, n_tokens, k, x, act, hidden, inter, limit, sel));
+    OBJ_TRY(launch_moe_gate_up(ctx, format, s, table, n_table, ids, n_tokens, k, x, act, hidden, inter, limit, sel,
+                               shared));
     return launch_moe_down(ctx, format, s, table, n_table, ids, wts, n_tokens, k, act, resid, out, inter, out_dim,
-                           sel);
+                           sel, shared);
 }
 
 // ------------------------------------------------ static activation scratch
@@ -662,22 +692,34 @@ using namespace objeta;
 
 extern "C" {
 
-int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
-                                       const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
-                                       const uint32_t* d_ids, const float* d_weights, uint64_t n_tokens,
-                                       uint64_t k, const float* d_x, const float* d_residual, float* d_out,
-                                       uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
-                                       float swiglu_limit) {
+int32_t objeta_hip_moe_selected_shared_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                              const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                              const objeta_hip_expert_ptrs* d_shared, const uint32_t* d_ids,
+                                              const float* d_weights, uint64_t n_tokens, uint64_t k, const float* d_x,
+                                              const float* d_residual, float* d_out, uint64_t hidden,
+                                              uint64_t intermediate, uint64_t out_dim, float swiglu_limit) {
     OBJ_GUARD_BEGIN
     OBJ_TRY(check_ctx(ctx, "moe_selected_device"));
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     hipStream_t s = resolve_stream(ctx, stream);
     if (n_tokens == 0 || out_dim == 0) return 0;
     float* act = nullptr;
-    OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k ? k : 1, intermediate ? intermediate : 1, &act));
+    const uint64_t kk = (k ? k : 1) + (d_shared ? 1 : 0);
+    OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, kk, intermediate ? intermediate : 1, &act));
     return launch_moe_selected(ctx, format, s, d_table, n_table, d_ids, d_weights, n_tokens, k, d_x, d_residual,
-                               d_out, hidden, intermediate, out_dim, swiglu_limit, act, nullptr);
+                               d_out, hidden, intermediate, out_dim, swiglu_limit, act, nullptr, d_shared);
     OBJ_GUARD_END
+}
+
+int32_t objeta_hip_moe_selected_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                       const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                       const uint32_t* d_ids, const float* d_weights, uint64_t n_tokens,
+                                       uint64_t k, const float* d_x, const float* d_residual, float* d_out,
+                                       uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                       float swiglu_limit) {
+    return objeta_hip_moe_selected_shared_device(ctx, format, stream, d_table, n_table, nullptr, d_ids, d_weights,
+                                                 n_tokens, k, d_x, d_residual, d_out, hidden, intermediate, out_dim,
+                                                 swiglu_limit);
 }
 
 int32_t objeta_hip_moe_selected_device_noalloc(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
@@ -699,7 +741,7 @@ int32_t objeta_hip_moe_selected_device_noalloc(objeta_hip_context* ctx, int32_t 
                       (unsigned long long)(n_tokens * k * intermediate), (unsigned long long)kStaticActFloats));
     if (!ctx->static_act) OBJ_FAIL(kInternal, action, "static scratch not bound");
     return launch_moe_selected(ctx, format, s, d_table, n_table, d_ids, d_weights, n_tokens, k, d_x, d_residual,
-                               d_out, hidden, intermediate, out_dim, swiglu_limit, ctx->static_act, nullptr);
+                               d_out, hidden, intermediate, out_dim, swiglu_limit, ctx->static_act, nullptr, nullptr);
     OBJ_GUARD_END
 }
 
@@ -711,7 +753,7 @@ int32_t objeta_hip_moe_gate_up_device(objeta_hip_context* ctx, int32_t format, o
     OBJ_TRY(check_ctx(ctx, "moe_gate_up_device"));
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     return launch_moe_gate_up(ctx, format, resolve_stream(ctx, stream), d_table, n_table, d_ids, n_tokens, k, d_x,
-                              d_act, hidden, intermediate, swiglu_limit);
+                              d_act, hidden, intermediate, swiglu_limit, nullptr, nullptr);
     OBJ_GUARD_END
 }
 
@@ -723,17 +765,17 @@ int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, obje
     OBJ_TRY(check_ctx(ctx, "moe_down_device"));
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     return launch_moe_down(ctx, format, resolve_stream(ctx, stream), d_table, n_table, d_ids, d_weights, n_tokens, k,
-                           d_act, d_residual, d_out, intermediate, out_dim);
+                           d_act, d_residual, d_out, intermediate, out_dim, nullptr, nullptr);
     OBJ_GUARD_END
 }
 
-int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
-                                    const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
-                                    const float* d_router_w, const float* d_router_bias, uint64_t k,
-                                    int32_t renormalize, uint64_t n_tokens, const float* d_x,
-                                    const float* d_residual, float* d_out, uint32_t* d_ids_out,
-                                    float* d_weights_out, uint64_t hidden, uint64_t intermediate,
-                                    uint64_t out_dim, float swiglu_limit) {
+int32_t objeta_hip_moe_layer_shared_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                           const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
+                                           const objeta_hip_expert_ptrs* d_shared, const float* d_router_w,
+                                           const float* d_router_bias, uint64_t k, int32_t renormalize,
+                                           uint64_t n_tokens, const float* d_x, const float* d_residual, float* d_out,
+                                           uint32_t* d_ids_out, float* d_weights_out, uint64_t hidden,
+                                           uint64_t intermediate, uint64_t out_dim, float swiglu_limit) {
     OBJ_GUARD_BEGIN
     OBJ_TRY(check_ctx(ctx, "moe_layer_device"));
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
@@ -749,10 +791,22 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
                           d_ids_out, d_weights_out, d_table, &sel));
     if (out_dim == 0) return 0;
     float* act = nullptr;
-    OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k, intermediate ? intermediate : 1, &act));
+    OBJ_TRY(moe_act_scratch(ctx, s, n_tokens, k + (d_shared ? 1 : 0), intermediate ? intermediate : 1, &act));
     return launch_moe_selected(ctx, format, s, d_table, n_experts, d_ids_out, d_weights_out, n_tokens, k, d_x,
-                               d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit, act, sel);
+                               d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit, act, sel, d_shared);
     OBJ_GUARD_END
+}
+
+int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                    const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
+                                    const float* d_router_w, const float* d_router_bias, uint64_t k,
+                                    int32_t renormalize, uint64_t n_tokens, const float* d_x,
+                                    const float* d_residual, float* d_out, uint32_t* d_ids_out,
+                                    float* d_weights_out, uint64_t hidden, uint64_t intermediate,
+                                    uint64_t out_dim, float swiglu_limit) {
+    return objeta_hip_moe_layer_shared_device(ctx, format, stream, d_table, n_experts, nullptr, d_router_w,
+                                              d_router_bias, k, renormalize, n_tokens, d_x, d_residual, d_out,
+                                              d_ids_out, d_weights_out, hidden, intermediate, out_dim, swiglu_limit);
 }
 
 int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out) {

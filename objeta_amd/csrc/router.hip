@@ -246,6 +246,12 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
                   sel_tab ? sel_tab + static_cast<size_t>(t) * k : nullptr);
 }
 
+__global__ __launch_bounds__(256) void softmax_exp_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                          uint64_t n) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    if (i < n) y[i] = expf_glibc(x[i]);
+}
+
 }  // namespace
 
 static_assert(kMaxRouterExperts == static_cast<uint64_t>(kMaxExperts), "router workspace layout");
@@ -331,5 +337,20 @@ extern "C" int32_t objeta_hip_router_topk_device(objeta_hip_context* ctx, objeta
     hipStream_t s = resolve_stream(ctx, stream);
     return launch_router(ctx, s, d_w_r, d_bias, d_x, n_tokens, n_experts, hidden, k, renormalize, d_ids,
                          d_weights, nullptr, nullptr);
+    OBJ_GUARD_END
+}
+
+extern "C" int32_t objeta_hip_router_softmax_exp_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                                        const float* d_x, float* d_y, uint64_t n) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "router_softmax_exp_device"));
+    if (n == 0) return 0;
+    if (!d_x || !d_y) OBJ_FAIL(kInvalidInput, "router_softmax_exp_device", "NULL device pointer");
+    if (n > (uint64_t(1) << 32)) OBJ_FAIL(kInvalidInput, "router_softmax_exp_device", "n exceeds 2^32");
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    hipLaunchKernelGGL(softmax_exp_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, d_x, d_y, n);
+    OBJ_HIP(hipGetLastError(), "launch softmax exp");
+    return 0;
     OBJ_GUARD_END
 }

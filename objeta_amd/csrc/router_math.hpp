@@ -1,5 +1,5 @@
-// router_math.hpp — the router's arithmetic, shared by the router kernel and the
-// persistent decode-stack kernel.
+// router_math.hpp — the router's arithmetic (exact logit sums with error bounds,
+// the reference's softmax and stable top-k).
 //
 // Reference semantics: cpu_router (crates/objeta-cuda/src/bin/
 // deepseek_single_layer_moe.rs:687-743) takes each logit as a sequential fp32 sum
@@ -24,6 +24,51 @@ constexpr int kRWaves = kRThreads / 64;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kChunkBatch = 8;  // 256-element chunks loaded per batch (8 float4 per lane)
+
+// The reference's softmax calls Rust's f32::exp, which is glibc's expf on Linux.
+// glibc (2.28 and later) evaluates it with the method of Arm's optimized-routines
+// (Szabolcs Nagy, 2017): in double, x * 32/ln2 = k + r with k the nearest integer
+// (through the 1.5 * 2^52 shift), 2^(k/32) from a table of 2^(i/32), 2^(r/32)
+// from a degree-3 polynomial, one final rounding to float; on x86-64 with FMA it
+// runs the build with every product fused into the add that consumes it. This is
+// that form, operation for operation (fused where glibc fuses, separate products
+// elsewhere), so the device gets glibc's float on every argument; the same
+// restatement in the oracle agrees with glibc on all of [-110, 0] (exhaustively)
+// and double exp rounded once to float differs from it on 97,052 of those
+// arguments. Table entry i: the correctly rounded double 2^(i/32) minus i << 47.
+__device__ __forceinline__ float expf_glibc(float x) {
+    constexpr uint64_t kTab[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {  // |x| >= 88, inf or nan
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32, kShift = 0x1.8p+52;
+    constexpr double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                     kC2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = static_cast<double>(x);
+    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd = __dsub_rn(kd, kShift);
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    const double sc = __builtin_bit_cast(double, kTab[ki % 32] + (ki << 47));
+    const double z = __builtin_fma(kC0, r, kC1);
+    const double r2 = __dmul_rn(r, r);
+    double y = __builtin_fma(kC2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return static_cast<float>(__dmul_rn(y, sc));
+}
 
 // Wave-wide double scans through DPP row shifts and lane reads, not shuffles: a
 // shuffle goes through the LDS crossbar (over 100 cycles a step, 12 dependent
@@ -512,11 +557,11 @@ __device__ bool select_certain(SelectLds<MAXE>& s, uint32_t n, uint32_t k, int r
     float z = 1.0f;
     if (!renormalize) {
         float part = 0.0f;
-        for (uint32_t j = tid; j < n; j += kRThreads) part += expf(s.val[j] - mx);
+        for (uint32_t j = tid; j < n; j += kRThreads) part += expf_glibc(__fsub_rn(s.val[j], mx));
         z = block_sum(part, s.red);
     }
     if (tid < k) {
-        const float ev = expf(__fsub_rn(s.sv[tid], mx));
+        const float ev = expf_glibc(__fsub_rn(s.sv[tid], mx));
         s.e[tid] = renormalize ? ev : __fdiv_rn(ev, z);
     }
     __syncthreads();
@@ -640,12 +685,12 @@ __device__ __noinline__ bool select_refine(SelectLds<MAXE>& s, const float* __re
 
 // The reference's order throughout (cpu_router): logits[e] = sum_h fl(W[e,h] * x[h])
 // accumulated left to right in fp32 (+ bias); probs = exp(l - max) / sum with the
-// sum taken in expert order; stable descending sort of the probs. exp is evaluated
-// in double and rounded once, which agrees with glibc's expf on all but ~0.03% of
-// arguments (only a probability tie could expose that). Fills s.sel and s.e (the
-// probabilities). xat(h) returns x[h]. Block-wide; 256 threads.
+// sum taken in expert order; stable descending sort of the probs, with exp as
+// glibc's expf (expf_glibc, bit-identical), so equal probabilities tie exactly where
+// the reference's tie. Fills s.sel and s.e (the probabilities). xat(h) returns x[h].
+// Block-wide; 256 threads.
 // With s.val holding the logits the reference computes (or -inf where its exp
-// is exactly 0): the reference's softmax in fp32 (exp through double, the sum in
+// is exactly 0): the reference's softmax in fp32 (glibc's expf, the sum in
 // expert order, one division each) and its stable descending sort of the
 // probabilities; the top k ids go to s.sel, their probabilities to s.e. Block-wide.
 template <int MAXE>
@@ -655,7 +700,7 @@ __device__ void softmax_rank(SelectLds<MAXE>& s, uint32_t n, uint32_t k) {
     for (uint32_t j = threadIdx.x; j < n; j += kRThreads) mx = fmaxf(mx, s.val[j]);
     mx = block_max(mx, s.red);
     for (uint32_t j = threadIdx.x; j < n; j += kRThreads)
-        s.bnd[j] = static_cast<float>(exp(static_cast<double>(__fsub_rn(s.val[j], mx))));
+        s.bnd[j] = expf_glibc(__fsub_rn(s.val[j], mx));
     __syncthreads();
     if (threadIdx.x == 0) {
         float sum = 0.0f;

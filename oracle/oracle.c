@@ -582,3 +582,102 @@ float orc_gauss(uint64_t seed, uint64_t i, float sigma) {
 void orc_gauss_fill(uint64_t seed, uint64_t first, float sigma, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = orc_gauss(seed, first + i, sigma);
 }
+
+/* ------------------------------------------------------------- expf restated
+ * glibc (2.28 and later) computes expf with the method of Arm's optimized-routines
+ * (Szabolcs Nagy, 2017): in double, x * 32/ln2 = k + r with k the nearest integer
+ * (through the 1.5 * 2^52 shift), 2^(k/32) from a 32-entry table of 2^(i/32),
+ * 2^(r/32) from a degree-3 polynomial, one final rounding to float. On x86-64 with
+ * FMA (the GPU hosts' CPUs) glibc selects the build of it with the products fused
+ * into the adds that consume them, which is the form below: it agrees with glibc's
+ * expf on every argument (tests/test_oracle_crosscheck.py checks all of
+ * [-110, 0] and samples of the rest). Table entry i is the correctly rounded double
+ * 2^(i/32) with i << 47 subtracted, so that adding k << 47 yields 2^(k/32). */
+static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+static uint32_t f32_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, sizeof u);
+    return u;
+}
+static float bits_f32(uint32_t u) {
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+static double bits_f64(uint64_t u) {
+    double d;
+    memcpy(&d, &u, sizeof d);
+    return d;
+}
+static uint64_t f64_bits(double d) {
+    uint64_t u;
+    memcpy(&u, &d, sizeof u);
+    return u;
+}
+
+float orc_expf_restated(float x) {
+    const uint32_t ux = f32_bits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) { /* |x| >= 88, inf or nan */
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = f64_bits(kd);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    const double s = bits_f64(kExp2Tab[ki % 32] + (ki << 47));
+    const double z = fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float)(y * s);
+}
+
+void orc_expf_glibc(const float* in, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = expf(in[i]);
+}
+
+void orc_expf_range_check(uint32_t lo_bits, uint32_t hi_bits, uint64_t* restated_mismatch,
+                          uint64_t* double_mismatch) {
+    uint64_t a = 0, b = 0;
+#pragma omp parallel for reduction(+ : a, b) schedule(static)
+    for (int64_t u = (int64_t)lo_bits; u <= (int64_t)hi_bits; ++u) {
+        const float x = bits_f32((uint32_t)u);
+        const uint32_t g = f32_bits(expf(x));
+        if (f32_bits(orc_expf_restated(x)) != g) ++a;
+        if (f32_bits((float)exp((double)x)) != g) ++b;
+    }
+    *restated_mismatch = a;
+    *double_mismatch = b;
+}
+
+size_t orc_expf_double_disagreements(uint32_t lo_bits, uint32_t hi_bits, float* out, size_t cap) {
+    size_t n = 0;
+#pragma omp parallel for schedule(static)
+    for (int64_t u = (int64_t)lo_bits; u <= (int64_t)hi_bits; ++u) {
+        const float x = bits_f32((uint32_t)u);
+        if (f32_bits((float)exp((double)x)) != f32_bits(expf(x))) {
+            size_t slot;
+#pragma omp atomic capture
+            slot = n++;
+            if (slot < cap) out[slot] = x;
+        }
+    }
+    return n;
+}

@@ -102,6 +102,21 @@ int orc_router(const float* w_r, const float* bias, const float* x, size_t n_exp
 /* compare_outputs (quant.rs:676-723): out[0]=cosine, out[1]=rel_l2, out[2]=max_abs. */
 int orc_compare(const float* ref, const float* act, size_t n, float* out3);
 
+/* glibc's expf (Rust's f32::exp on Linux), element-wise: the value the reference's
+ * softmax uses (deepseek_single_layer_moe.rs:687-743). */
+void orc_expf_glibc(const float* in, float* out, size_t n);
+/* The restatement of glibc's expf method that the device router evaluates (see
+ * oracle.c). */
+float orc_expf_restated(float x);
+/* Over every float whose bits lie in [lo_bits, hi_bits]: the number of arguments
+ * where the restatement, and where exp in double rounded once to float, differ
+ * from glibc's expf. */
+void orc_expf_range_check(uint32_t lo_bits, uint32_t hi_bits, uint64_t* restated_mismatch,
+                          uint64_t* double_mismatch);
+/* The arguments (up to cap, in no particular order) where exp in double rounded once
+ * to float differs from glibc's expf; returns how many there are. */
+size_t orc_expf_double_disagreements(uint32_t lo_bits, uint32_t hi_bits, float* out, size_t cap);
+
 /* seeded_f32s LCG (crates/objeta-cuda/src/bin/bench_qgemv.rs:39-49, quant.rs:1610-1620). */
 void orc_seeded_f32s(uint64_t seed, float* out, size_t n);
 

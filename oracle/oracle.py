@@ -76,6 +76,12 @@ def _declare(L):
     L.orc_gauss_fill.argtypes = [C.c_uint64, C.c_uint64, C.c_float, P, SZ]
     L.orc_splitmix64.argtypes = [C.c_uint64]
     L.orc_splitmix64.restype = C.c_uint64
+    L.orc_expf_glibc.argtypes = [P, P, SZ]
+    L.orc_expf_restated.argtypes = [C.c_float]
+    L.orc_expf_restated.restype = C.c_float
+    L.orc_expf_range_check.argtypes = [C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+    L.orc_expf_double_disagreements.argtypes = [C.c_uint32, C.c_uint32, P, SZ]
+    L.orc_expf_double_disagreements.restype = SZ
 
 
 class OracleError(Exception):
@@ -199,10 +205,16 @@ def split_interleaved_fp4(interleaved, rows: int, cols: int):
 
 
 # ---------------------------------------------------------------- MoE
-def selected_moe(fmt: int, experts, selected, x, hidden: int, inter: int, out_dim: int):
+def selected_moe(fmt: int, experts, selected, x, hidden: int, inter: int, out_dim: int, shared=None):
     """experts: list of (gate, up, down) arrays (bytes for block formats / f32 for
     fmt=-1) or, for FP4, (gate_w, gate_s, up_w, up_s, down_w, down_s).
-    selected: list of (expert_id, weight)."""
+    selected: list of (expert_id, weight). shared: one more expert in the same form,
+    added with weight 1.0 after the routed sum, as execute_selected_moe_official_routed_fp4_cuda
+    does (moe.rs:1552-1600: weighted_accum(shared_down, out, 1.0) after the routed loop),
+    which is the routed loop of orc_selected_moe run over one more slot."""
+    if shared is not None:
+        experts = list(experts) + [shared]
+        selected = list(selected) + [(len(experts) - 1, 1.0)]
     n = len(experts)
     keep = []
 
@@ -249,6 +261,35 @@ def router(w_r, x, n_experts: int, hidden: int, k: int, bias=None, renormalize=T
                           _ptr(probs), err, 256)
     _check(rc, err)
     return ids, ws, logits, probs
+
+
+def expf_glibc(x) -> np.ndarray:
+    """glibc's expf element-wise (the f32::exp of the reference's softmax)."""
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    lib().orc_expf_glibc(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def expf_restated(x) -> np.ndarray:
+    """The oracle's restatement of glibc's expf method (the device router's form)."""
+    x = _f32(x).ravel()
+    return np.array([lib().orc_expf_restated(float(v)) for v in x], np.float32)
+
+
+def expf_range_check(lo_bits: int, hi_bits: int):
+    """(restated mismatches, double-rounded mismatches) against glibc's expf over every
+    float with bits in [lo_bits, hi_bits]."""
+    a, b = C.c_uint64(), C.c_uint64()
+    lib().orc_expf_range_check(lo_bits, hi_bits, C.byref(a), C.byref(b))
+    return a.value, b.value
+
+
+def expf_double_disagreements(lo_bits: int, hi_bits: int, cap: int = 1 << 18) -> np.ndarray:
+    """Sorted arguments in [lo_bits, hi_bits] where double exp rounded to float != glibc expf."""
+    out = np.empty(cap, np.float32)
+    n = lib().orc_expf_double_disagreements(lo_bits, hi_bits, _ptr(out), cap)
+    return np.sort(out[:min(n, cap)])
 
 
 def compare(ref, act):

@@ -56,13 +56,17 @@ def device_table(backend, fmt, experts):
     return ExpertTable(backend, entries), keep
 
 
-def assert_moe_close(out, ref):
+def assert_moe_close(out, ref, abs_bar=1e-2):
+    """abs_bar: the reference's absolute max-abs threshold, meant for outputs of order
+    one; None skips it where outputs are orders of magnitude larger (the relative
+    per-element bound below still applies)."""
     out = np.asarray(out, np.float32)
     ref = np.asarray(ref, np.float32)
     c = orc.compare(ref, out)
     assert c["cosine_similarity"] >= 0.9999, c
     assert c["relative_l2_error"] <= 1e-4, c
-    assert c["max_abs_error"] <= 1e-2, c
+    if abs_bar is not None:
+        assert c["max_abs_error"] <= abs_bar, c
     scale = max(float(np.max(np.abs(ref))), 1e-30)
     err = float(np.max(np.abs(out.astype(np.float64) - ref.astype(np.float64))))
     assert err <= 1e-4 * scale, f"max rel err {err / scale:.3e}"

@@ -170,3 +170,110 @@ def test_gauss_generator_statistics_and_determinism():
     assert np.array_equal(g[500:600], orc.gauss(100, 7, 1.0, first=500))
     s = orc.gauss(1000, 7, 0.02)
     assert np.array_equal(s, (g[:1000] * np.float32(0.02)).astype(np.float32))
+
+
+_LIBM = None
+
+
+def _expf(v: np.ndarray) -> np.ndarray:
+    """glibc expf element-wise through its own symbol (Rust's f32::exp calls it on Linux)."""
+    global _LIBM
+    import ctypes
+    if _LIBM is None:
+        _LIBM = ctypes.CDLL("libm.so.6")
+        _LIBM.expf.restype = ctypes.c_float
+        _LIBM.expf.argtypes = [ctypes.c_float]
+    return np.array([_LIBM.expf(float(a)) for a in np.asarray(v, np.float32)], np.float32)
+
+
+def _np_split_fp4_gemv(w, s, x, rows, cols):
+    """Dense sequential row sums over the decoded split FP4 matrix (table value * 2^(raw-127))."""
+    table = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6], np.float32)
+    b = np.asarray(w, np.uint8).reshape(rows, cols // 2)
+    nib = np.empty((rows, cols), np.uint8)
+    nib[:, 0::2] = b & 15
+    nib[:, 1::2] = b >> 4
+    raw = np.asarray(s, np.uint8).reshape(rows, cols // 32).astype(np.uint32)
+    scale = np.where(raw == 0, np.float32(2.0 ** -127), (raw << 23).view(np.float32)).astype(np.float32)
+    dec = (table[nib] * np.repeat(scale, 32, axis=1)).astype(np.float32)
+    prod = (dec * np.asarray(x, np.float32)[None, :]).astype(np.float32)
+    return np.cumsum(prod, axis=1, dtype=np.float32)[:, -1]
+
+
+def _np_selected_moe(fmt, experts, sel, x, hidden, inter, out_dim):
+    """selected_moe_cpu (moe.rs:1283-1324) / selected_moe_cpu_native_fp4 (moe.rs:1665-1735)
+    composed from independent numpy parts: gate and up GEMVs, act = g / (1 + exp(-g)) * u
+    in float32 operations, down GEMV, out += w * down in selection order."""
+    out = np.zeros(out_dim, np.float32)
+    for e, wt in sel:
+        ex = experts[e]
+        if fmt == orc.FP4:
+            g = _np_split_fp4_gemv(ex[0], ex[1], x, inter, hidden)
+            u = _np_split_fp4_gemv(ex[2], ex[3], x, inter, hidden)
+        else:
+            g = nps.gemv(fmt, ex[0], x, inter, hidden)
+            u = nps.gemv(fmt, ex[1], x, inter, hidden)
+        act = ((g / (np.float32(1.0) + _expf(-g))).astype(np.float32) * u).astype(np.float32)
+        if fmt == orc.FP4:
+            d = _np_split_fp4_gemv(ex[4], ex[5], act, out_dim, inter)
+        else:
+            d = nps.gemv(fmt, ex[2], act, out_dim, inter)
+        out = (out + (np.float32(wt) * d).astype(np.float32)).astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("fmt", [orc.Q4_0, orc.Q5_0, orc.IQ3_0, orc.FP4])
+@pytest.mark.parametrize("with_shared", [False, True])
+def test_selected_moe_matches_numpy_composition(fmt, with_shared):
+    """orc_selected_moe pinned on its own: expert indexing, gate/up order, SiLU, the
+    slot-ordered combine and the shared expert (one more slot of weight 1.0 after the
+    routed ones, moe.rs:1552-1600) against a numpy composition, bit for bit. A swapped
+    gate/up, a dropped slot or a reordered combine changes the bits."""
+    hidden, inter, out_dim, n = 128, 96, 64, 5
+    experts = []
+    for e in range(n):
+        if fmt == orc.FP4:
+            rng = np.random.default_rng(40 + e)
+            mats = []
+            for r, c in ((inter, hidden), (inter, hidden), (out_dim, inter)):
+                mats += [rng.integers(0, 256, size=r * c // 2, dtype=np.uint8),
+                         rng.integers(119, 128, size=r * c // 32, dtype=np.uint8)]
+            experts.append(tuple(mats))
+        else:
+            experts.append(tuple(orc.quantize_matrix(fmt, orc.gauss(r * c, 100 * e + i, 0.05), r, c)
+                                 for i, (r, c) in enumerate(((inter, hidden), (inter, hidden), (out_dim, inter)))))
+    x = orc.gauss(hidden, 7, 1.0)
+    sel = [(3, 0.4), (1, 0.35), (3, 0.15), (0, 0.1)]
+    shared = experts[4] if with_shared else None
+    got = orc.selected_moe(fmt, experts[:4], sel, x, hidden, inter, out_dim, shared=shared)
+    want_sel = sel + ([(4, 1.0)] if with_shared else [])
+    want = _np_selected_moe(fmt, experts, want_sel, x, hidden, inter, out_dim)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a plausible mistake changes the bits: gate and up swapped
+    swapped = [(ex[1], ex[0], ex[2]) if fmt != orc.FP4 else (ex[2], ex[3], ex[0], ex[1], ex[4], ex[5])
+               for ex in experts]
+    assert not np.array_equal(_np_selected_moe(fmt, swapped, want_sel, x, hidden, inter, out_dim), want)
+
+
+def test_expf_restatement_matches_glibc_exhaustively_on_softmax_domain():
+    """The router's softmax evaluates exp(l - max) with l - max in [-inf, 0]. The
+    restatement of glibc's expf method (the device's form) agrees with glibc's expf on
+    every float in [-110, 0]; exp in double rounded once to float does not (the
+    disagreements exist, so a ranking built on it could break a probability tie
+    differently from the reference)."""
+    restated, dbl = orc.expf_range_check(0x80000000, 0xC2DC0000)  # -0 .. -110
+    assert restated == 0
+    assert dbl > 90000
+    # below -110 glibc underflows to exactly 0 (from below log(2^-150) ~ -103.97)
+    restated, _ = orc.expf_range_check(0xC2DC0001, 0xC3000000)  # -110 .. -128
+    assert restated == 0
+
+
+def test_expf_restatement_specials_and_positive_sample():
+    x = np.array([0.0, -0.0, -np.inf, np.inf, 88.72, 88.73, -103.97, -103.98, 1e-30, -1e-30, 1.0, -1.0, 10.0, 50.5],
+                 np.float32)
+    rng = np.random.default_rng(3)
+    x = np.concatenate([x, rng.uniform(-90, 88, 200000).astype(np.float32),
+                        rng.uniform(-1e-3, 1e-3, 50000).astype(np.float32)])
+    assert np.array_equal(orc.expf_restated(x).view(np.uint32), orc.expf_glibc(x).view(np.uint32))
+    assert np.isnan(orc.expf_restated(np.array([np.nan], np.float32))[0])
