@@ -207,6 +207,12 @@ int32_t objeta_hip_fill_gauss_quantized_device(objeta_hip_context* ctx, int32_t 
                                                objeta_hip_stream stream, void* d_out,
                                                uint64_t rows, uint64_t cols, uint64_t seed,
                                                float sigma);
+/* One split FP4 matrix of synthetic bytes (no reference counterpart; the reference's
+ * FP4 inputs come from checkpoints): d_w [rows][cols/2] nibbles uniform over the 16
+ * E2M1 codes, d_s [rows][cols/32] E8M0 scales uniform over raw 119..127 (2^-8 ..
+ * 2^0), from a counter-based splitmix64 recipe that the host reproduces. */
+int32_t objeta_hip_fill_fp4_split_device(objeta_hip_context* ctx, objeta_hip_stream stream, void* d_w, void* d_s,
+                                         uint64_t rows, uint64_t cols, uint64_t seed);
 /* The E8M0 exponent rule of the device FP4 quantizer (fp4_quantize_block,
  * quant.rs:913-918) evaluated on the host, element-wise over n block maxima. */
 int32_t objeta_hip_fp4_scale_raw_host(const float* amax, uint8_t* out, uint64_t n);

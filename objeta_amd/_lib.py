@@ -130,6 +130,7 @@ SIGNATURES = {
     "objeta_hip_fill_gauss_device": (I32, [P, P, P, U64, U64, U64, F32]),
     "objeta_hip_fill_gauss_quantized_device": (I32, [P, I32, P, P, U64, U64, U64, F32]),
     "objeta_hip_fp4_scale_raw_host": (I32, [P, P, U64]),
+    "objeta_hip_fill_fp4_split_device": (I32, [P, P, P, P, U64, U64, U64]),
     "objeta_hip_router_topk_device": (I32, [P, P, P, P, P, U64, U64, U64, U64, I32, P, P]),
     "objeta_hip_router_softmax_exp_device": (I32, [P, P, P, P, U64]),
     "objeta_hip_moe_selected_device": (I32, [P, I32, P, P, U64, P, P, U64, U64, P, P, P, U64, U64,

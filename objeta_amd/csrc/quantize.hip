@@ -81,6 +81,22 @@ __global__ __launch_bounds__(kThreads) void gauss_kernel(float* __restrict__ out
     out[i] = rules::gauss_from_key(key, first + i, sigma);
 }
 
+// One split FP4 matrix of synthetic bytes: weight byte i is byte (i mod 8) of
+// splitmix64(kw + i / 8) (nibbles uniform over the 16 E2M1 codes), scale byte i is
+// 119 + splitmix64(ks + i) mod 9 (E8M0 2^-8 .. 2^0). Thread t writes weight word t
+// and scale byte t.
+__global__ __launch_bounds__(kThreads) void fp4_split_random_kernel(uint8_t* __restrict__ w, uint8_t* __restrict__ sc,
+                                                                    uint64_t n_w, uint64_t n_s, uint64_t kw,
+                                                                    uint64_t ks) {
+    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const uint64_t i0 = t * 8;
+    if (i0 < n_w) {
+        const uint64_t v = rules::splitmix64(kw + t);
+        for (uint32_t b = 0; b < 8 && i0 + b < n_w; ++b) w[i0 + b] = static_cast<uint8_t>(v >> (8 * b));
+    }
+    if (t < n_s) sc[t] = static_cast<uint8_t>(119u + static_cast<uint32_t>(rules::splitmix64(ks + t) % 9u));
+}
+
 __global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ d, uint64_t words) {
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < words;
          i += static_cast<uint64_t>(gridDim.x) * kThreads)
@@ -209,6 +225,26 @@ int32_t objeta_hip_fill_gauss_quantized_device(objeta_hip_context* ctx, int32_t 
 
 // Host evaluation of the E8M0 exponent rule used by the device FP4 quantizer, so
 // the rule can be checked against the CPU reference over every float.
+int32_t objeta_hip_fill_fp4_split_device(objeta_hip_context* ctx, objeta_hip_stream stream, void* d_w, void* d_s,
+                                         uint64_t rows, uint64_t cols, uint64_t seed) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "fill_fp4_split_device"));
+    if (cols % 32 != 0)
+        OBJ_FAIL(kInvalidInput, "fill_fp4_split_device",
+                 strf("cols %llu must be a multiple of block_size 32", (unsigned long long)cols));
+    const uint64_t n_w = rows * cols / 2, n_s = rows * cols / 32;
+    if (n_w == 0) return 0;
+    if (!d_w || !d_s) OBJ_FAIL(kInvalidInput, "fill_fp4_split_device", "NULL device pointer");
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    const uint64_t threads = (n_w + 7) / 8 > n_s ? (n_w + 7) / 8 : n_s;
+    hipLaunchKernelGGL(fp4_split_random_kernel, grid_for(threads), dim3(kThreads), 0, resolve_stream(ctx, stream),
+                       static_cast<uint8_t*>(d_w), static_cast<uint8_t*>(d_s), n_w, n_s, rules::splitmix64(seed),
+                       rules::splitmix64(seed ^ 0x5CA1E5CA1E5CA1E5ull));
+    OBJ_HIP(hipGetLastError(), "launch fp4 split fill");
+    return 0;
+    OBJ_GUARD_END
+}
+
 int32_t objeta_hip_fp4_scale_raw_host(const float* amax, uint8_t* out, uint64_t n) {
     if (n && (!amax || !out)) OBJ_FAIL(kInvalidInput, "fp4_scale_raw_host", "NULL pointer");
     for (uint64_t i = 0; i < n; ++i) out[i] = rules::fp4_scale_raw(amax[i]);

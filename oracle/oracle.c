@@ -341,6 +341,14 @@ float orc_dot_row(int fmt, const uint8_t* row_q, const float* x, size_t cols) {
     return sum;
 }
 
+/* Threads of the row loops (GEMV rows, router logits, FP4 decode rows). Each row's
+ * sum stays one sequential loop, so the results do not depend on the count; the
+ * reference's CPU path is single-threaded (1, the default), more threads give the
+ * row-parallel CPU baseline. */
+static int g_threads = 1;
+void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int orc_get_threads(void) { return g_threads; }
+
 /* gemv_cpu, quant.rs:627-646; validate_quant_inputs, quant.rs:751-793 */
 int orc_gemv(int fmt, const uint8_t* q, size_t q_len, const float* x, size_t x_len,
              size_t rows, size_t cols, float* y, char* err, size_t err_len) {
@@ -355,6 +363,7 @@ int orc_gemv(int fmt, const uint8_t* q, size_t q_len, const float* x, size_t x_l
                     rows * row_bytes);
     if (x_len != cols)
         return fail(K_INVALID_INPUT, err, err_len, "x len %zu != cols %zu", x_len, cols);
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (size_t r = 0; r < rows; ++r) y[r] = orc_dot_row(fmt, q + r * row_bytes, x, cols);
     return 0;
 }
@@ -374,6 +383,7 @@ int orc_dense_gemv(const float* m, size_t m_len, const float* x, size_t x_len, s
                     rows * cols);
     if (x_len != cols)
         return fail(K_INVALID_INPUT, err, err_len, "vector len %zu != cols %zu", x_len, cols);
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (size_t r = 0; r < rows; ++r) y[r] = dense_row(m + r * cols, x, cols);
     return 0;
 }
@@ -382,6 +392,7 @@ int orc_dense_gemv(const float* m, size_t m_len, const float* x, size_t x_len, s
 void orc_decode_fp4_split(const uint8_t* w, const uint8_t* s, size_t rows, size_t cols,
                           float* out) {
     size_t phys = cols / 2, scols = cols / 32;
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (size_t r = 0; r < rows; ++r) {
         for (size_t g = 0; g < phys; ++g) {
             uint8_t b = w[r * phys + g];
@@ -488,6 +499,7 @@ int orc_router(const float* w_r, const float* bias, const float* x, size_t n_exp
     float* logits = (float*)malloc(n_experts * sizeof(float));
     float* probs = (float*)malloc(n_experts * sizeof(float));
     uint32_t* order = (uint32_t*)malloc(n_experts * sizeof(uint32_t));
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (size_t e = 0; e < n_experts; ++e) {
         float sum = 0.0f;
         const float* row = w_r + e * hidden;

@@ -102,6 +102,11 @@ int orc_router(const float* w_r, const float* bias, const float* x, size_t n_exp
 /* compare_outputs (quant.rs:676-723): out[0]=cosine, out[1]=rel_l2, out[2]=max_abs. */
 int orc_compare(const float* ref, const float* act, size_t n, float* out3);
 
+/* Threads of the row loops (default 1, the reference's single thread); results are
+ * identical for every count because each row's sum stays sequential. */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
 /* glibc's expf (Rust's f32::exp on Linux), element-wise: the value the reference's
  * softmax uses (deepseek_single_layer_moe.rs:687-743). */
 void orc_expf_glibc(const float* in, float* out, size_t n);

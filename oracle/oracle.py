@@ -76,6 +76,8 @@ def _declare(L):
     L.orc_gauss_fill.argtypes = [C.c_uint64, C.c_uint64, C.c_float, P, SZ]
     L.orc_splitmix64.argtypes = [C.c_uint64]
     L.orc_splitmix64.restype = C.c_uint64
+    L.orc_set_threads.argtypes = [C.c_int]
+    L.orc_get_threads.restype = C.c_int
     L.orc_expf_glibc.argtypes = [P, P, SZ]
     L.orc_expf_restated.argtypes = [C.c_float]
     L.orc_expf_restated.restype = C.c_float
@@ -261,6 +263,11 @@ def router(w_r, x, n_experts: int, hidden: int, k: int, bias=None, renormalize=T
                           _ptr(probs), err, 256)
     _check(rc, err)
     return ids, ws, logits, probs
+
+
+def set_threads(n: int) -> None:
+    """Threads of the oracle's row loops (1 = the reference's single thread)."""
+    lib().orc_set_threads(int(n))
 
 
 def expf_glibc(x) -> np.ndarray:

@@ -202,3 +202,17 @@ def test_router_softmax_exp_is_glibc_expf(backend):
     want = orc.expf_glibc(x)
     bad = np.nonzero(y.view(np.uint32) != want.view(np.uint32))[0]
     assert bad.size == 0, f"{bad.size} mismatches, first at x={x[bad[0]]!r}: {y[bad[0]]!r} != {want[bad[0]]!r}"
+
+
+def test_fill_fp4_split_device_matches_host_recipe(backend):
+    """The device FP4 generator writes the bytes of the host recipe (workloads.fp4_random_split)."""
+    import ctypes as C
+    from objeta_amd import check
+    from objeta_amd.workloads import fp4_random_split
+    for rows, cols, seed in ((7, 96, 3), (2048, 7168, 8001)):
+        w, s = fp4_random_split(rows, cols, seed)
+        dw, ds = backend.alloc(w.size), backend.alloc(s.size)
+        check(backend.L.objeta_hip_fill_fp4_split_device(backend.ctx, None, dw.addr(), ds.addr(), rows, cols, seed))
+        assert np.array_equal(dw.download(np.uint8, w.size), w)
+        assert np.array_equal(ds.download(np.uint8, s.size), s)
+        assert s.min() >= 119 and s.max() <= 127
