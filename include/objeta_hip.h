@@ -464,6 +464,65 @@ int32_t objeta_hip_cache_release_transient(objeta_hip_expert_cache* cache, const
 int32_t objeta_hip_cache_order(const objeta_hip_expert_cache* cache, objeta_hip_cache_key* keys, uint64_t cap,
                                uint64_t* n);
 
+/* ---------------------------------------- FP8-activation ("official") path */
+/* The DeepSeek official arithmetic: activations quantized to F8_E4M3 bytes with
+ * one F8_E8M0 scale per 128 elements, FP8 x FP4 and FP8 x FP8 GEMVs, and the
+ * routed / shared expert compositions. Results follow the reference's CPU
+ * definitions (crates/objeta-parser/src/deepseek.rs:1444-1716): act_quant bytes
+ * exactly; GEMV sums in another order (within 1e-4 relative). */
+
+/* cuda_act_quant_device (quant.rs:1229-1281) with cpu_act_quant's bytes
+ * (deepseek.rs:1484-1525), over rows x cols floats (cols % 128 == 0): d_values
+ * [rows][cols] F8_E4M3, d_scales [rows][cols/128] F8_E8M0, and, when d_dequant is
+ * set, the dequantized values act_v * act_s as floats (d_dequant may alias d_x).
+ * Each output is nullable; at least one is required. d_x and d_dequant 8-byte,
+ * d_values 2-byte aligned. */
+int32_t objeta_hip_act_quant_fp8_device(objeta_hip_context* ctx, objeta_hip_stream stream, const float* d_x,
+                                        uint64_t rows, uint64_t cols, uint8_t* d_values, uint8_t* d_scales,
+                                        float* d_dequant);
+
+/* cuda_fp8_act_fp4_weight_gemv_device (quant.rs:1284-1325), arithmetic of
+ * cpu_fp8_act_fp4_weight_gemv_f32 (deepseek.rs:1528-1566), for `batch`
+ * activation vectors: d_out[b][r] = sum_c act(b, c) * fp4(r, c) * ws(r, c / 32)
+ * with act = f8e4m3(d_act_values[b][c]) * e8m0(d_act_scales[b][c / 128]); weights
+ * in the split layout (nibbles [rows][k/2], E8M0 [rows][k/32]). k_logical % 128 == 0. */
+int32_t objeta_hip_fp8_act_fp4_weight_gemv_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                                  const uint8_t* d_act_values, const uint8_t* d_act_scales,
+                                                  const uint8_t* d_weight, const uint8_t* d_weight_scales,
+                                                  float* d_out, uint64_t rows, uint64_t k_logical, uint64_t batch);
+
+/* cuda_fp8_act_fp8_weight_gemv_device (quant.rs:1328-1362), arithmetic of
+ * cpu_fp8_act_fp8_weight_gemv (deepseek.rs:1630-1661): FP8 E4M3 weights
+ * [rows][k] with E8M0 scales on a 128 x 128 tile grid [ceil(rows/128)][k/128];
+ * products summed in f32 (the reference sums in f64). k_logical % 128 == 0;
+ * d_weight 16-byte aligned. */
+int32_t objeta_hip_fp8_act_fp8_weight_gemv_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                                  const uint8_t* d_act_values, const uint8_t* d_act_scales,
+                                                  const uint8_t* d_weight, const uint8_t* d_weight_scales,
+                                                  float* d_out, uint64_t rows, uint64_t k_logical, uint64_t batch);
+
+/* The device part of execute_selected_moe_official_routed_fp4_cuda
+ * (moe.rs:1393-1663) batched over tokens. For token t:
+ *   xq     = act_quant(x_t)                               (dequantized)
+ *   act_j  = swiglu(gate_e xq, up_e xq), e = d_table[d_ids[t*k + j]] (FP4 split)
+ *   act_s  = swiglu(gate_s xq, up_s xq)                   (d_shared_fp8, FP8 tiles)
+ *   out_t  = sum_j d_weights[t*k + j] * down_e(act_quant(act_j)) + down_s(act_quant(act_s))
+ * swiglu(g, u) = g / (1 + exp(-g)) * clamp(u, -L, L) (the CPU compositions,
+ * deepseek.rs:1680-1686, 1708-1713; the reference's CUDA silu_mul also clamps g
+ * to <= L). L = swiglu_limit >= 0. d_shared_fp8: a device pointer to one
+ * objeta_hip_expert_ptrs whose tensors are FP8 E4M3 with 128 x 128 E8M0 scale
+ * tiles, or NULL. k = 0 leaves the shared expert alone. hidden and intermediate
+ * are multiples of 128. d_inter_values [n_tokens*kk][intermediate] and
+ * d_inter_scales [n_tokens*kk][intermediate/128] (nullable; kk = k + 1 with a
+ * shared expert, else k) receive the intermediates' FP8 codes: rows t*k + j for
+ * the routed slots, then n_tokens*k + t for the shared expert. */
+int32_t objeta_hip_moe_official_fp4_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                           const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                           const objeta_hip_expert_ptrs* d_shared_fp8, const uint32_t* d_ids,
+                                           const float* d_weights, uint64_t n_tokens, uint64_t k, const float* d_x,
+                                           float* d_out, uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                           float swiglu_limit, uint8_t* d_inter_values, uint8_t* d_inter_scales);
+
 /* ------------------------------------------------ host-in/host-out executor */
 /* One expert's host tensors: gate/up/down bytes (and, for FP4, the E8M0 scale
  * arrays) with their lengths. Mirrors ExpertWeights (moe.rs:13-18) and
@@ -546,6 +605,24 @@ int32_t objeta_hip_moe_execute_selected(objeta_hip_context* ctx, int32_t format,
                                         const float* x, uint64_t x_len, uint64_t hidden, uint64_t intermediate,
                                         uint64_t out_dim, uint64_t layer_id, objeta_hip_expert_cache* cache,
                                         float* out, objeta_hip_moe_telemetry* tel);
+
+/* execute_selected_moe_official_routed_fp4_cuda (moe.rs:1393-1663): host x in,
+ * host out[out_dim] out, for one token; experts are FP4 split host tensors
+ * (gate/up/down weight and scale, cached under the reference's keys), shared_fp8
+ * (nullable) a host struct of device addresses of the FP8 shared expert (device
+ * resident, as DeepSeekFp8SharedExpertWeightsDevice). The reference passes 10.0
+ * as swiglu_limit. Telemetry follows the reference's official accounting:
+ * logical bytes = the unique selected experts' working set; routed_fp4_* and
+ * shared_fp8_* / total_* fields filled; resident-cache counters other than
+ * hit/miss/eviction 0; activation_ms = the intermediate act_quant; shared_expert_ms =
+ * the shared expert's launches. */
+int32_t objeta_hip_moe_execute_official_fp4(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                            const objeta_hip_host_expert* experts, uint64_t n_experts,
+                                            const uint64_t* sel_ids, const float* sel_weights, uint64_t n_selected,
+                                            const float* x, uint64_t x_len, uint64_t hidden, uint64_t intermediate,
+                                            uint64_t out_dim, uint64_t layer_id, objeta_hip_expert_cache* cache,
+                                            const objeta_hip_expert_ptrs* shared_fp8, float swiglu_limit, float* out,
+                                            objeta_hip_moe_telemetry* tel);
 
 #ifdef __cplusplus
 }

@@ -164,6 +164,13 @@ SIGNATURES = {
     "objeta_hip_cache_order": (I32, [P, P, U64, P]),
     "objeta_hip_moe_execute_selected": (I32, [P, I32, P, P, U64, P, P, U64, P, U64, U64, U64, U64, U64, P,
                                               P, P]),
+    "objeta_hip_act_quant_fp8_device": (I32, [P, P, P, U64, U64, P, P, P]),
+    "objeta_hip_fp8_act_fp4_weight_gemv_device": (I32, [P, P, P, P, P, P, P, U64, U64, U64]),
+    "objeta_hip_fp8_act_fp8_weight_gemv_device": (I32, [P, P, P, P, P, P, P, U64, U64, U64]),
+    "objeta_hip_moe_official_fp4_device": (I32, [P, P, P, U64, P, P, P, U64, U64, P, P, U64, U64, U64, F32,
+                                                 P, P]),
+    "objeta_hip_moe_execute_official_fp4": (I32, [P, P, P, U64, P, P, U64, P, U64, U64, U64, U64, U64, P, P,
+                                                  F32, P, P]),
 }
 
 

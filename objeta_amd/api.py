@@ -309,6 +309,41 @@ class QuantBackend:
         check(self.L.objeta_hip_fp4_gemv_split_device(self.backend.ctx, stream, _addr(d_w), _addr(d_s),
                                                       _addr(d_x), _addr(d_y), rows, cols, batch))
 
+    # ---- FP8-activation ("official arithmetic") kernels
+    def act_quant_device(self, stream, d_x, rows: int, cols: int, d_values=None, d_scales=None,
+                         d_dequant=None) -> None:
+        """cuda_act_quant_device (quant.rs:1229-1281) with cpu_act_quant's bytes: FP8 E4M3
+        values [rows][cols], E8M0 scales [rows][cols/128], optionally the dequantized floats."""
+        check(self.L.objeta_hip_act_quant_fp8_device(self.backend.ctx, stream, _addr(d_x), rows, cols,
+                                                     _addr_or_none(d_values), _addr_or_none(d_scales),
+                                                     _addr_or_none(d_dequant)))
+
+    def act_quant(self, stream, x: np.ndarray, rows: int, cols: int):
+        """cuda_act_quant (quant.rs:1119-1216): host floats in, (values, scales) bytes out."""
+        xv = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        if cols % 128 != 0:
+            raise ValueError(f"cuda_act_quant: cols {cols} not divisible by 128")
+        if xv.size != rows * cols:
+            raise ValueError(f"cuda_act_quant: input len {xv.size} != rows {rows} * cols {cols}")
+        dx = self.backend.to_device(xv)
+        dv, ds = self.backend.alloc(max(1, rows * cols)), self.backend.alloc(max(1, rows * cols // 128))
+        self.act_quant_device(stream, dx, rows, cols, dv, ds)
+        return dv.download(np.uint8, rows * cols, stream), ds.download(np.uint8, rows * cols // 128, stream)
+
+    def fp8_act_fp4_weight_gemv_device(self, stream, d_act_values, d_act_scales, d_weight, d_weight_scales,
+                                       d_out, rows: int, k_logical: int, batch: int = 1) -> None:
+        """cuda_fp8_act_fp4_weight_gemv_device (quant.rs:1284-1325), `batch` activation vectors."""
+        check(self.L.objeta_hip_fp8_act_fp4_weight_gemv_device(
+            self.backend.ctx, stream, _addr(d_act_values), _addr(d_act_scales), _addr(d_weight),
+            _addr(d_weight_scales), _addr(d_out), rows, k_logical, batch))
+
+    def fp8_act_fp8_weight_gemv_device(self, stream, d_act_values, d_act_scales, d_weight, d_weight_scales,
+                                       d_out, rows: int, k_logical: int, batch: int = 1) -> None:
+        """cuda_fp8_act_fp8_weight_gemv_device (quant.rs:1328-1362): FP8 weights, 128 x 128 scale tiles."""
+        check(self.L.objeta_hip_fp8_act_fp8_weight_gemv_device(
+            self.backend.ctx, stream, _addr(d_act_values), _addr(d_act_scales), _addr(d_weight),
+            _addr(d_weight_scales), _addr(d_out), rows, k_logical, batch))
+
 
 def _addr(v):
     if isinstance(v, DeviceBuffer):
@@ -398,6 +433,18 @@ class MoeExecutor:
             _addr(d_router_w), _addr_or_none(d_router_bias), k, 1 if renormalize else 0, n_tokens, _addr(d_x),
             _addr_or_none(d_residual), _addr(d_out), _addr(d_ids_out), _addr(d_weights_out), hidden,
             inter, out_dim, swiglu_limit))
+
+    def official_fp4_device(self, table: ExpertTable, d_ids, d_weights, n_tokens: int, k: int, d_x, d_out,
+                            hidden: int, inter: int, out_dim: int, swiglu_limit: float = 10.0, stream=None,
+                            shared_fp8: "ExpertTable | None" = None, d_inter_values=None,
+                            d_inter_scales=None) -> None:
+        """The device part of execute_selected_moe_official_routed_fp4_cuda (moe.rs:1393-1663),
+        batched over tokens: FP8 activations, FP4 split routed experts, an optional FP8
+        shared expert (a one-entry ExpertTable with 128 x 128 scale tiles)."""
+        check(self.L.objeta_hip_moe_official_fp4_device(
+            self.backend.ctx, stream, table.addr(), table.n, None if shared_fp8 is None else shared_fp8.addr(),
+            _addr(d_ids), _addr(d_weights), n_tokens, k, _addr(d_x), _addr(d_out), hidden, inter, out_dim,
+            swiglu_limit, _addr_or_none(d_inter_values), _addr_or_none(d_inter_scales)))
 
     def device_error(self) -> int:
         v = C.c_uint32(0)
@@ -556,8 +603,9 @@ def _telemetry_moe(t: MoeTelemetry) -> dict:
     return d
 
 
-def _execute(backend: HipBackend, fmt: int, stream, experts, selected, x, hidden, inter, out_dim, layer_id,
-             cache: ExpertCache | None):
+def _host_experts(experts):
+    """(HostExpert array, kept arrays) for [(gate, up, down)] or
+    [(gate_w, gate_s, up_w, up_s, down_w, down_s)] host tensors."""
     keep = []
     arr = (HostExpert * max(1, len(experts)))()
     for i, e in enumerate(experts):
@@ -572,6 +620,12 @@ def _execute(backend: HipBackend, fmt: int, stream, experts, selected, x, hidden
             v = [g.ctypes.data, g.nbytes, u.ctypes.data, u.nbytes, d.ctypes.data, d.nbytes,
                  gs.ctypes.data, gs.nbytes, us.ctypes.data, us.nbytes, ds.ctypes.data, ds.nbytes]
         arr[i] = HostExpert(*v)
+    return arr, keep
+
+
+def _execute(backend: HipBackend, fmt: int, stream, experts, selected, x, hidden, inter, out_dim, layer_id,
+             cache: ExpertCache | None):
+    arr, keep = _host_experts(experts)
     ids = np.array([s[0] for s in selected], np.uint64)
     ws = np.array([s[1] for s in selected], np.float32)
     xv = np.ascontiguousarray(x, dtype=np.float32).ravel()
@@ -600,6 +654,33 @@ def _moe_execute_native_fp4(self, quant, stream, experts, selected_experts, x, h
                     intermediate, out_dim, layer_id, cache)
 
 
+def _moe_execute_official_fp4(self, quant, stream, experts, selected_experts, hidden_state, hidden_size: int,
+                              intermediate_size: int, out_dim: int, layer_id: int,
+                              cache: ExpertCache | None = None, shared_expert=None, swiglu_limit: float = 10.0):
+    """execute_selected_moe_official_routed_fp4_cuda (moe.rs:1393-1663): experts =
+    [(gate_w, gate_s, up_w, up_s, down_w, down_s)] split-FP4 host bytes; shared_expert =
+    (gate_w, up_w, down_w, gate_s, up_s, down_s) device addresses of the FP8 shared
+    expert, or None. Returns (out, telemetry)."""
+    arr, keep = _host_experts(experts)
+    ids = np.array([s[0] for s in selected_experts], np.uint64)
+    ws = np.array([s[1] for s in selected_experts], np.float32)
+    xv = np.ascontiguousarray(hidden_state, dtype=np.float32).ravel()
+    out = np.zeros(max(out_dim, 1), np.float32)
+    tel = MoeTelemetry()
+    sh = None
+    if shared_expert is not None:
+        sh = ExpertPtrs(*[_ptr_int(p) for p in shared_expert])
+    check(self.L.objeta_hip_moe_execute_official_fp4(
+        self.backend.ctx, stream, arr, len(experts), ids.ctypes.data_as(C.c_void_p), ws.ctypes.data_as(C.c_void_p),
+        ids.size, xv.ctypes.data_as(C.c_void_p), xv.size, hidden_size, intermediate_size, out_dim, layer_id,
+        cache.h if cache is not None else None, None if sh is None else C.byref(sh), swiglu_limit,
+        out.ctypes.data_as(C.c_void_p), C.byref(tel)))
+    del keep
+    return out[:out_dim], _telemetry_moe(tel)
+
+
+MoeExecutor.execute_selected_moe_official_routed_fp4 = _moe_execute_official_fp4
+MoeExecutor.execute_selected_moe_official_routed_fp4_cuda = _moe_execute_official_fp4
 MoeExecutor.execute_selected_moe = _moe_execute_selected
 MoeExecutor.execute_selected_moe_cuda = _moe_execute_selected
 MoeExecutor.execute_selected_moe_native_fp4 = _moe_execute_native_fp4

@@ -609,6 +609,169 @@ float elapsed(hipEvent_t a, hipEvent_t b) {
     return ms;
 }
 
+// The tensors of one host expert in key order: w_gate / w_up / w_down for the
+// block formats, gate/up/down weight and scale for the FP4 split layout.
+int tensors_of(const objeta_hip_host_expert& e, bool fp4, TensorRef* t) {
+    if (!fp4) {
+        t[0] = {e.gate, e.gate_len, OBJETA_HIP_TENSOR_GATE, false};
+        t[1] = {e.up, e.up_len, OBJETA_HIP_TENSOR_UP, false};
+        t[2] = {e.down, e.down_len, OBJETA_HIP_TENSOR_DOWN, false};
+        return 3;
+    }
+    t[0] = {e.gate, e.gate_len, OBJETA_HIP_TENSOR_GATE_WEIGHT, false};
+    t[1] = {e.gate_scale, e.gate_scale_len, OBJETA_HIP_TENSOR_GATE_SCALE, true};
+    t[2] = {e.up, e.up_len, OBJETA_HIP_TENSOR_UP_WEIGHT, false};
+    t[3] = {e.up_scale, e.up_scale_len, OBJETA_HIP_TENSOR_UP_SCALE, true};
+    t[4] = {e.down, e.down_len, OBJETA_HIP_TENSOR_DOWN_WEIGHT, false};
+    t[5] = {e.down_scale, e.down_scale_len, OBJETA_HIP_TENSOR_DOWN_SCALE, true};
+    return 6;
+}
+
+// The selected experts' device tensors for one executor call: cache hits, or
+// copies of misses enqueued on the copy stream, with the byte accounting of the
+// reference's load closure (moe.rs:458-583, 1000-1100, 1451-1487). The blocks stay
+// referenced until release().
+struct StagedExperts {
+    std::vector<std::pair<Cache*, Block*>> held;  // (home, block) references of this call
+    std::vector<hipEvent_t> ready;                // per slot: its copies done (NULL: all hits)
+    uint64_t w_loaded = 0, w_reused = 0, s_loaded = 0, s_reused = 0, logical = 0;
+    uint64_t by_kind[3] = {0, 0, 0};
+    bool any_copy = false;
+
+    void release() {
+        for (auto& hb : held) {
+            hb.second->refs -= 1;
+            retire_block(hb.first, hb.second);
+        }
+        held.clear();
+    }
+    ~StagedExperts() {
+        for (hipEvent_t r : ready)
+            if (r) (void)hipEventDestroy(r);
+    }
+};
+
+// count_oversize: an expert larger than the capacity counts as an oversized-expert
+// bypass (bypass enabled) or a self-eviction risk, as the block-format and native
+// FP4 executors count them (moe.rs:485-492); the official executor counts neither.
+int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_host_expert* experts,
+                       const uint64_t* sel_ids, uint64_t k, int32_t format, uint64_t layer_id, bool count_oversize,
+                       hipStream_t s, objeta_hip_expert_ptrs* h_tab, StagedExperts& st) {
+    const bool fp4 = format == OBJETA_HIP_FP4_E2M1;
+    Cache* pool = transient_pool(ctx);
+    st.ready.assign(k, nullptr);
+    for (uint64_t j = 0; j < k; ++j) {
+        const uint64_t e = sel_ids[j];
+        TensorRef t[6];
+        const int nt = tensors_of(experts[e], fp4, t);
+        uint64_t eb = 0;
+        for (int q = 0; q < nt; ++q) eb += t[q].len;
+        st.logical += eb;
+        st.by_kind[0] += t[0].len + (fp4 ? t[1].len : 0);
+        st.by_kind[1] += fp4 ? t[2].len + t[3].len : t[1].len;
+        st.by_kind[2] += fp4 ? t[4].len + t[5].len : t[2].len;
+        bool bypass = false;
+        if (cache && eb > cache->st.capacity_bytes) {
+            if (cache->st.bypass_oversized_experts) {
+                bypass = true;
+                if (count_oversize) cache->st.oversized_expert_bypass_count += 1;
+            } else if (count_oversize) {
+                cache->st.self_eviction_risk_count += 1;
+            }
+        }
+        const void* dptr[6] = {};
+        bool copied = false;
+        for (int q = 0; q < nt; ++q) {
+            const Key key{layer_id, e, t[q].kind, format};
+            Block* b = nullptr;
+            bool hit = false;
+            if (bypass) {
+                cache->st.cache_insert_attempt_count += 1;
+                cache->st.cache_insert_bypass_count += 1;
+            } else if (cache) {
+                b = lookup(cache, key);
+                hit = b != nullptr;
+            }
+            Cache* home = cache && !bypass ? cache : pool;
+            if (!hit) {
+                OBJ_TRY(stage_tensor(home, t[q].h, t[q].len, s, &b));
+                copied = true;
+                if (cache && !bypass) (void)insert_block(cache, key, b, t[q].len);
+            }
+            b->refs += 1;
+            st.held.push_back({home, b});
+            dptr[q] = b->ptr;
+            if (hit) (t[q].scale ? st.s_reused : st.w_reused) += t[q].len;
+            else (t[q].scale ? st.s_loaded : st.w_loaded) += t[q].len;
+        }
+        if (copied) {
+            st.any_copy = true;
+            hipEvent_t r = nullptr;
+            if (hipEventCreateWithFlags(&r, hipEventDisableTiming) != hipSuccess ||
+                hipEventRecord(r, ctx->copy_stream) != hipSuccess) {
+                (void)hipGetLastError();
+                if (r) (void)hipEventDestroy(r);
+                OBJ_FAIL(kDriver, "record copy event", "event failure");
+            }
+            st.ready[j] = r;
+        }
+        objeta_hip_expert_ptrs& p = h_tab[j];
+        if (fp4) p = {dptr[0], dptr[2], dptr[4], dptr[1], dptr[3], dptr[5]};
+        else p = {dptr[0], dptr[1], dptr[2], nullptr, nullptr, nullptr};
+    }
+    return 0;
+}
+
+// Size checks of every selected expert's tensors (moe.rs:366-422, 830-925).
+int32_t validate_selected(const objeta_hip_host_expert* experts, uint64_t n_experts, const uint64_t* sel_ids,
+                          uint64_t k, bool fp4, uint64_t gu_w, uint64_t gu_s, uint64_t dn_w, uint64_t dn_s) {
+    for (uint64_t i = 0; i < k; ++i) {
+        const uint64_t e = sel_ids[i];
+        if (e >= n_experts)
+            OBJ_FAIL(kInvalidInput, "validate expert index",
+                     strf("expert index %llu out of bounds (len=%llu)", (unsigned long long)e,
+                          (unsigned long long)n_experts));
+        TensorRef t[6];
+        const int nt = tensors_of(experts[e], fp4, t);
+        for (int j = 0; j < nt; ++j) {
+            const uint64_t want = (j < 2 * (nt / 3)) ? (t[j].scale ? gu_s : gu_w) : (t[j].scale ? dn_s : dn_w);
+            if (t[j].len != want)
+                OBJ_FAIL(kInvalidInput, strf("validate expert %s size", tensor_label(t[j].kind)),
+                         strf("%s len %llu != expected %llu", tensor_label(t[j].kind), (unsigned long long)t[j].len,
+                              (unsigned long long)want));
+        }
+    }
+    return 0;
+}
+
+void copy_cache_counters(const Cache* cache, objeta_hip_moe_telemetry& t) {
+    if (!cache) return;
+    t.resident_cache_resident_bytes = cache->st.resident_bytes;
+    t.resident_cache_capacity_bytes = cache->st.capacity_bytes;
+    t.resident_cache_hit_count = cache->st.hit_count;
+    t.resident_cache_miss_count = cache->st.miss_count;
+    t.resident_cache_eviction_count = cache->st.eviction_count;
+    t.resident_cache_insert_attempt_count = cache->st.cache_insert_attempt_count;
+    t.resident_cache_insert_accept_count = cache->st.cache_insert_accept_count;
+    t.resident_cache_insert_bypass_count = cache->st.cache_insert_bypass_count;
+    t.resident_cache_oversized_tensor_bypass_count = cache->st.oversized_tensor_bypass_count;
+    t.resident_cache_oversized_expert_bypass_count = cache->st.oversized_expert_bypass_count;
+    t.resident_cache_self_eviction_risk_count = cache->st.self_eviction_risk_count;
+}
+
+struct EventSet {
+    std::vector<hipEvent_t> e;
+    explicit EventSet(size_t n) : e(n, nullptr) {}
+    int32_t create() {
+        for (auto& v : e) OBJ_HIP(hipEventCreate(&v), "create telemetry event");
+        return 0;
+    }
+    ~EventSet() {
+        for (hipEvent_t v : e)
+            if (v) (void)hipEventDestroy(v);
+    }
+};
+
 }  // namespace
 }  // namespace objeta
 
@@ -637,53 +800,17 @@ extern "C" int32_t objeta_hip_moe_execute_selected(
     const uint64_t gu_s = fp4 ? intermediate * (hidden / 32) : 0;
     const uint64_t dn_w = fp4 ? out_dim * (intermediate / 2) : out_dim * (intermediate / 32) * bb;
     const uint64_t dn_s = fp4 ? out_dim * (intermediate / 32) : 0;
-    auto tensors_of = [&](const objeta_hip_host_expert& e, TensorRef* t) -> int {
-        if (!fp4) {
-            t[0] = {e.gate, e.gate_len, OBJETA_HIP_TENSOR_GATE, false};
-            t[1] = {e.up, e.up_len, OBJETA_HIP_TENSOR_UP, false};
-            t[2] = {e.down, e.down_len, OBJETA_HIP_TENSOR_DOWN, false};
-            return 3;
-        }
-        t[0] = {e.gate, e.gate_len, OBJETA_HIP_TENSOR_GATE_WEIGHT, false};
-        t[1] = {e.gate_scale, e.gate_scale_len, OBJETA_HIP_TENSOR_GATE_SCALE, true};
-        t[2] = {e.up, e.up_len, OBJETA_HIP_TENSOR_UP_WEIGHT, false};
-        t[3] = {e.up_scale, e.up_scale_len, OBJETA_HIP_TENSOR_UP_SCALE, true};
-        t[4] = {e.down, e.down_len, OBJETA_HIP_TENSOR_DOWN_WEIGHT, false};
-        t[5] = {e.down_scale, e.down_scale_len, OBJETA_HIP_TENSOR_DOWN_SCALE, true};
-        return 6;
-    };
-    for (uint64_t i = 0; i < n_selected; ++i) {
-        const uint64_t e = sel_ids[i];
-        if (e >= n_experts)
-            OBJ_FAIL(kInvalidInput, "validate expert index",
-                     strf("expert index %llu out of bounds (len=%llu)", (unsigned long long)e,
-                          (unsigned long long)n_experts));
-        TensorRef t[6];
-        const int nt = tensors_of(experts[e], t);
-        for (int j = 0; j < nt; ++j) {
-            const uint64_t want = (j < 2 * (nt / 3)) ? (t[j].scale ? gu_s : gu_w) : (t[j].scale ? dn_s : dn_w);
-            if (t[j].len != want)
-                OBJ_FAIL(kInvalidInput, strf("validate expert %s size", tensor_label(t[j].kind)),
-                         strf("%s len %llu != expected %llu", tensor_label(t[j].kind), (unsigned long long)t[j].len,
-                              (unsigned long long)want));
-        }
-    }
+    OBJ_TRY(validate_selected(experts, n_experts, sel_ids, n_selected, fp4, gu_w, gu_s, dn_w, dn_s));
     if (n_selected > 32) OBJ_FAIL(kInvalidInput, "validate selection", "at most 32 selected experts per call");
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     hipStream_t s = resolve_stream(ctx, stream);
     const uint64_t k = n_selected;
 
     // ---- telemetry events
-    hipEvent_t ev[8] = {};
-    for (auto& e : ev) OBJ_HIP(hipEventCreate(&e), "create telemetry event");
-    struct EvGuard {
-        hipEvent_t* e;
-        ~EvGuard() {
-            for (int i = 0; i < 8; ++i)
-                if (e[i]) (void)hipEventDestroy(e[i]);
-        }
-    } evg{ev};
-    enum { T0, X0, X1, GU0, GU1, DN1, D2H0, T1 };
+    enum { T0, X0, X1, GU0, GU1, DN1, D2H0, T1, C0, C1, kEv };
+    EventSet evs(kEv);
+    OBJ_TRY(evs.create());
+    hipEvent_t* ev = evs.e.data();
     OBJ_HIP(hipEventRecord(ev[T0], s), "record event");
 
     // ---- device scratch: [x | out | weights | table] and host staging
@@ -710,109 +837,19 @@ extern "C" int32_t objeta_hip_moe_execute_selected(
     OBJ_HIP(hipEventRecord(ev[X1], s), "record event");
 
     // ---- weights: cache admission and copies (moe.rs:458-583, 1000-1100)
-    Cache* pool = transient_pool(ctx);
-    std::vector<std::pair<Cache*, Block*>> held;  // (home, block) references of this call
-    std::vector<hipEvent_t> ready(k, nullptr);
-    hipEvent_t c0 = nullptr, c1 = nullptr;  // copy stream span of this call's weight copies
-    OBJ_HIP(hipEventCreate(&c0), "create telemetry event");
-    struct CopyEvGuard {
-        hipEvent_t& a;
-        hipEvent_t& b;
-        ~CopyEvGuard() {
-            if (a) (void)hipEventDestroy(a);
-            if (b) (void)hipEventDestroy(b);
-        }
-    } cg{c0, c1};
-    OBJ_HIP(hipEventCreate(&c1), "create telemetry event");
-    OBJ_HIP(hipEventRecord(c0, ctx->copy_stream), "record event");
-    uint64_t w_loaded = 0, w_reused = 0, s_loaded = 0, s_reused = 0, logical = 0;
-    uint64_t by_kind[3] = {0, 0, 0};
+    StagedExperts st;
+    OBJ_HIP(hipEventRecord(ev[C0], ctx->copy_stream), "record event");
     std::vector<uint64_t> uniq(sel_ids, sel_ids + k);
     std::sort(uniq.begin(), uniq.end());
     uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
     const uint64_t single_expert_bytes = 2 * (gu_w + gu_s) + dn_w + dn_s;
-    bool any_copy = false;
-    int32_t rc = 0;
-    auto release_all = [&]() {
-        for (auto& hb : held) {
-            hb.second->refs -= 1;
-            retire_block(hb.first, hb.second);
-        }
-        held.clear();
-    };
-    for (uint64_t j = 0; j < k && rc == 0; ++j) {
-        const uint64_t e = sel_ids[j];
-        TensorRef t[6];
-        const int nt = tensors_of(experts[e], t);
-        uint64_t eb = 0;
-        for (int q = 0; q < nt; ++q) eb += t[q].len;
-        logical += eb;
-        by_kind[0] += t[0].len + (fp4 ? t[1].len : 0);
-        by_kind[1] += fp4 ? t[2].len + t[3].len : t[1].len;
-        by_kind[2] += fp4 ? t[4].len + t[5].len : t[2].len;
-        bool bypass = false;
-        if (cache && eb > cache->st.capacity_bytes) {
-            if (cache->st.bypass_oversized_experts) {
-                bypass = true;
-                cache->st.oversized_expert_bypass_count += 1;
-            } else {
-                cache->st.self_eviction_risk_count += 1;
-            }
-        }
-        const void* dptr[6] = {};
-        bool copied = false;
-        for (int q = 0; q < nt && rc == 0; ++q) {
-            const Key key{layer_id, e, t[q].kind, format};
-            Block* b = nullptr;
-            bool hit = false;
-            if (bypass) {
-                cache->st.cache_insert_attempt_count += 1;
-                cache->st.cache_insert_bypass_count += 1;
-            } else if (cache) {
-                b = lookup(cache, key);
-                hit = b != nullptr;
-            }
-            Cache* home = cache && !bypass ? cache : pool;
-            if (!hit) {
-                rc = stage_tensor(home, t[q].h, t[q].len, s, &b);
-                if (rc) break;
-                copied = true;
-                if (cache && !bypass) (void)insert_block(cache, key, b, t[q].len);
-            }
-            b->refs += 1;
-            held.push_back({home, b});
-            dptr[q] = b->ptr;
-            if (hit) (t[q].scale ? s_reused : w_reused) += t[q].len;
-            else (t[q].scale ? s_loaded : w_loaded) += t[q].len;
-        }
-        if (rc) break;
-        if (copied) {
-            any_copy = true;
-            hipEvent_t r = nullptr;
-            if (hipEventCreateWithFlags(&r, hipEventDisableTiming) != hipSuccess ||
-                hipEventRecord(r, ctx->copy_stream) != hipSuccess) {
-                (void)hipGetLastError();
-                rc = set_error(kDriver, __FILE__, __LINE__, __func__, "record copy event", "event failure");
-                if (r) (void)hipEventDestroy(r);
-                break;
-            }
-            ready[j] = r;
-        }
-        objeta_hip_expert_ptrs& p = h_tab[j];
-        if (fp4) p = {dptr[0], dptr[2], dptr[4], dptr[1], dptr[3], dptr[5]};
-        else p = {dptr[0], dptr[1], dptr[2], nullptr, nullptr, nullptr};
-    }
-    auto destroy_ready = [&]() {
-        for (hipEvent_t r : ready)
-            if (r) (void)hipEventDestroy(r);
-    };
+    int32_t rc = stage_selected(ctx, cache, experts, sel_ids, k, format, layer_id, true, s, h_tab, st);
     if (rc) {
         (void)hipStreamSynchronize(ctx->copy_stream);
-        release_all();
-        destroy_ready();
+        st.release();
         return rc;
     }
-    OBJ_HIP(hipEventRecord(c1, ctx->copy_stream), "record event");
+    OBJ_HIP(hipEventRecord(ev[C1], ctx->copy_stream), "record event");
 
     // ---- compute
     do {
@@ -830,7 +867,7 @@ extern "C" int32_t objeta_hip_moe_execute_selected(
         if (k == 0) {
             if ((rc = launch_zero(s, d_out, out_dim * 4))) break;
             (void)hipEventRecord(ev[GU1], s);
-        } else if (!any_copy) {
+        } else if (!st.any_copy) {
             if ((rc = launch_moe_gate_up(ctx, format, s, d_tab, k, nullptr, 1, k, d_x, act, hidden, intermediate, 0.f)))
                 break;
             (void)hipEventRecord(ev[GU1], s);
@@ -840,8 +877,8 @@ extern "C" int32_t objeta_hip_moe_execute_selected(
         } else {
             // expert by expert, each waiting only for its own copies
             for (uint64_t j = 0; j < k && rc == 0; ++j) {
-                if (ready[j]) {
-                    hipError_t e = hipStreamWaitEvent(s, ready[j], 0);
+                if (st.ready[j]) {
+                    hipError_t e = hipStreamWaitEvent(s, st.ready[j], 0);
                     if (e != hipSuccess) {
                         (void)hipGetLastError();
                         rc = set_error(kDriver, __FILE__, __LINE__, __func__, "wait expert copies", hipGetErrorString(e));
@@ -869,53 +906,195 @@ extern "C" int32_t objeta_hip_moe_execute_selected(
     if (rc) {
         (void)hipStreamSynchronize(s);
         (void)hipStreamSynchronize(ctx->copy_stream);
-        release_all();
-        destroy_ready();
+        st.release();
         return rc;
     }
     std::memcpy(out, h_out, out_dim * 4);
-    release_all();
-    destroy_ready();
+    st.release();
 
     // ---- telemetry (moe.rs:664-748)
-    const uint64_t loaded = w_loaded + s_loaded, reused = w_reused + s_reused;
-    if (logical != loaded + reused)
+    const uint64_t loaded = st.w_loaded + st.s_loaded, reused = st.w_reused + st.s_reused;
+    if (st.logical != loaded + reused)
         OBJ_FAIL(kInternal, "MoE byte invariant", "logical_expert_bytes_requested != loaded + reused");
     if (tel) {
         objeta_hip_moe_telemetry t{};
         t.selected_expert_count = k;
-        t.logical_expert_bytes_requested = logical;
+        t.logical_expert_bytes_requested = st.logical;
         t.actual_expert_bytes_loaded = loaded;
         t.resident_cache_bytes_reused = reused;
-        t.weight_bytes_loaded = w_loaded;
-        t.weight_bytes_reused = w_reused;
-        t.scale_bytes_loaded = s_loaded;
-        t.scale_bytes_reused = s_reused;
-        if (cache) {
-            t.resident_cache_resident_bytes = cache->st.resident_bytes;
-            t.resident_cache_capacity_bytes = cache->st.capacity_bytes;
-            t.resident_cache_hit_count = cache->st.hit_count;
-            t.resident_cache_miss_count = cache->st.miss_count;
-            t.resident_cache_eviction_count = cache->st.eviction_count;
-            t.resident_cache_insert_attempt_count = cache->st.cache_insert_attempt_count;
-            t.resident_cache_insert_accept_count = cache->st.cache_insert_accept_count;
-            t.resident_cache_insert_bypass_count = cache->st.cache_insert_bypass_count;
-            t.resident_cache_oversized_tensor_bypass_count = cache->st.oversized_tensor_bypass_count;
-            t.resident_cache_oversized_expert_bypass_count = cache->st.oversized_expert_bypass_count;
-            t.resident_cache_self_eviction_risk_count = cache->st.self_eviction_risk_count;
-        }
-        t.h2d_ms = elapsed(ev[X0], ev[X1]) + (any_copy ? elapsed(c0, c1) : 0.f);
+        t.weight_bytes_loaded = st.w_loaded;
+        t.weight_bytes_reused = st.w_reused;
+        t.scale_bytes_loaded = st.s_loaded;
+        t.scale_bytes_reused = st.s_reused;
+        copy_cache_counters(cache, t);
+        t.h2d_ms = elapsed(ev[X0], ev[X1]) + (st.any_copy ? elapsed(ev[C0], ev[C1]) : 0.f);
         t.gate_up_qgemv_ms = elapsed(ev[GU0], ev[GU1]);
         t.down_qgemv_ms = elapsed(ev[GU1], ev[DN1]);
         const float d2h = elapsed(ev[D2H0], ev[T1]);
         t.total_ms = elapsed(ev[T0], ev[T1]);
         const float un = t.total_ms - t.h2d_ms - t.gate_up_qgemv_ms - t.down_qgemv_ms - d2h;
         t.unaccounted_ms = un > 0.f ? un : 0.f;
-        t.bytes_by_tensor_kind_gate = by_kind[0];
-        t.bytes_by_tensor_kind_up = by_kind[1];
-        t.bytes_by_tensor_kind_down = by_kind[2];
+        t.bytes_by_tensor_kind_gate = st.by_kind[0];
+        t.bytes_by_tensor_kind_up = st.by_kind[1];
+        t.bytes_by_tensor_kind_down = st.by_kind[2];
         t.bytes_per_expert = single_expert_bytes;
         t.selected_working_set_bytes = uniq.size() * single_expert_bytes;
+        *tel = t;
+    }
+    return 0;
+    OBJ_GUARD_END
+}
+
+// execute_selected_moe_official_routed_fp4_cuda (moe.rs:1393-1663): FP4 split
+// routed experts through the FP8-activation path, plus an optional device-resident
+// FP8 shared expert, for one token. The launches are those of
+// objeta_hip_moe_official_fp4_device; misses are copied on the copy stream and the
+// layer waits for all of them. Telemetry follows the reference's official
+// accounting: logical bytes are the unique selected experts' working set, the
+// shared expert counts as loaded on every call, cache counters beyond
+// hit/miss/eviction stay 0, activation_ms is the intermediate act_quant and
+// shared_expert_ms the shared expert's two launches.
+extern "C" int32_t objeta_hip_moe_execute_official_fp4(
+    objeta_hip_context* ctx, objeta_hip_stream stream, const objeta_hip_host_expert* experts, uint64_t n_experts,
+    const uint64_t* sel_ids, const float* sel_weights, uint64_t n_selected, const float* x, uint64_t x_len,
+    uint64_t hidden, uint64_t intermediate, uint64_t out_dim, uint64_t layer_id, objeta_hip_expert_cache* cache,
+    const objeta_hip_expert_ptrs* shared_fp8, float swiglu_limit, float* out, objeta_hip_moe_telemetry* tel) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "execute_selected_moe_official_routed_fp4"));
+    const char* action = "validate execute_selected_moe_official_routed_fp4_cuda input";
+    if (cache && cache->ctx && cache->ctx != ctx)
+        OBJ_FAIL(kInvalidInput, "validate expert cache", "cache belongs to another context");
+    if (x_len != hidden)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("x len %llu != hidden %llu", (unsigned long long)x_len, (unsigned long long)hidden));
+    if (hidden % 128 != 0 || intermediate % 128 != 0)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("hidden %llu and intermediate %llu must be multiples of 128", (unsigned long long)hidden,
+                      (unsigned long long)intermediate));
+    if (n_selected && (!sel_ids || !sel_weights)) OBJ_FAIL(kInvalidInput, "validate selection", "NULL selection");
+    if ((hidden && !x) || (out_dim && !out)) OBJ_FAIL(kInvalidInput, "validate buffers", "NULL host pointer");
+    const uint64_t gu_w = intermediate * (hidden / 2), gu_s = intermediate * (hidden / 32);
+    const uint64_t dn_w = out_dim * (intermediate / 2), dn_s = out_dim * (intermediate / 32);
+    OBJ_TRY(validate_selected(experts, n_experts, sel_ids, n_selected, true, gu_w, gu_s, dn_w, dn_s));
+    if (n_selected > 32) OBJ_FAIL(kInvalidInput, "validate selection", "at most 32 selected experts per call");
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    const uint64_t k = n_selected;
+
+    enum { T0, X0, X1, GU1, SH1, AQ1, DN1, D2H0, T1, kEv };
+    EventSet evs(kEv);
+    OBJ_TRY(evs.create());
+    hipEvent_t* ev = evs.e.data();
+    OBJ_HIP(hipEventRecord(ev[T0], s), "record event");
+
+    // device scratch: [x | out | weights | ids | table | shared entry] and host staging
+    const size_t x_b = (hidden * 4 + 255) & ~size_t(255);
+    const size_t o_b = (out_dim * 4 + 255) & ~size_t(255);
+    const size_t w_b = 256, i_b = 256;
+    const size_t t_b = (k + 1) * sizeof(objeta_hip_expert_ptrs);
+    void* dws = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsMoeTable, x_b + o_b + w_b + i_b + t_b, &dws));
+    void* hst = nullptr;
+    OBJ_TRY(ensure_host_stage(ctx, x_b + o_b + w_b + i_b + t_b, &hst));
+    char* d0 = static_cast<char*>(dws);
+    char* h0 = static_cast<char*>(hst);
+    float* d_x = reinterpret_cast<float*>(d0);
+    float* d_out = reinterpret_cast<float*>(d0 + x_b);
+    float* h_out = reinterpret_cast<float*>(h0 + x_b);
+    const size_t tail = x_b + o_b;  // weights | ids | table, copied in one piece
+    float* d_w = reinterpret_cast<float*>(d0 + tail);
+    uint32_t* d_ids = reinterpret_cast<uint32_t*>(d0 + tail + w_b);
+    objeta_hip_expert_ptrs* d_tab = reinterpret_cast<objeta_hip_expert_ptrs*>(d0 + tail + w_b + i_b);
+    uint32_t* h_ids = reinterpret_cast<uint32_t*>(h0 + tail + w_b);
+    objeta_hip_expert_ptrs* h_tab = reinterpret_cast<objeta_hip_expert_ptrs*>(h0 + tail + w_b + i_b);
+    std::memcpy(h0, x, hidden * 4);
+    if (k) std::memcpy(h0 + tail, sel_weights, k * 4);
+    for (uint64_t j = 0; j < k; ++j) h_ids[j] = static_cast<uint32_t>(j);  // slot j reads table entry j
+    if (shared_fp8) h_tab[k] = *shared_fp8;
+    OBJ_HIP(hipEventRecord(ev[X0], s), "record event");
+    OBJ_HIP(hipMemcpyAsync(d_x, h0, hidden * 4, hipMemcpyHostToDevice, s), "official_h2d");
+    OBJ_HIP(hipEventRecord(ev[X1], s), "record event");
+
+    StagedExperts st;
+    int32_t rc = stage_selected(ctx, cache, experts, sel_ids, k, OBJETA_HIP_FP4_E2M1, layer_id, false, s, h_tab, st);
+    if (rc) {
+        (void)hipStreamSynchronize(ctx->copy_stream);
+        st.release();
+        return rc;
+    }
+    do {
+        hipError_t e = hipMemcpyAsync(d0 + tail, h0 + tail, w_b + i_b + t_b, hipMemcpyHostToDevice, s);
+        for (uint64_t j = 0; j < k && e == hipSuccess; ++j)
+            if (st.ready[j]) e = hipStreamWaitEvent(s, st.ready[j], 0);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            rc = set_error(kDriver, __FILE__, __LINE__, __func__, "official_table_h2d", hipGetErrorString(e));
+            break;
+        }
+        const OfficialMarks marks{ev[GU1], ev[SH1], ev[AQ1], ev[DN1]};
+        if ((rc = launch_moe_official_fp4(ctx, s, d_tab, k ? k : 1, shared_fp8 ? d_tab + k : nullptr, d_ids, d_w, 1, k,
+                                          d_x, d_out, hidden, intermediate, out_dim, swiglu_limit, nullptr, nullptr,
+                                          &marks)))
+            break;
+        (void)hipEventRecord(ev[D2H0], s);
+        e = hipMemcpyAsync(h_out, d_out, out_dim * 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipEventRecord(ev[T1], s);
+        if (e == hipSuccess) e = hipEventSynchronize(ev[T1]);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            rc = set_error(kDriver, __FILE__, __LINE__, __func__, "official_d2h", hipGetErrorString(e));
+        }
+    } while (false);
+    if (rc) {
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamSynchronize(ctx->copy_stream);
+        st.release();
+        return rc;
+    }
+    std::memcpy(out, h_out, out_dim * 4);
+    st.release();
+
+    if (tel) {
+        std::vector<uint64_t> uniq(sel_ids, sel_ids + k);
+        std::sort(uniq.begin(), uniq.end());
+        uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
+        const uint64_t single_expert_bytes = 2 * (gu_w + gu_s) + dn_w + dn_s;
+        const uint64_t working = uniq.size() * single_expert_bytes;
+        // the reference's shared byte formula (moe.rs:1618-1624), scales counted per 128
+        const uint64_t sh_total = shared_fp8 ? 2 * (intermediate * hidden) + out_dim * intermediate +
+                                                   2 * (intermediate * hidden / 128) + out_dim * intermediate / 128
+                                             : 0;
+        const uint64_t loaded = st.w_loaded + st.s_loaded, reused = st.w_reused + st.s_reused;
+        objeta_hip_moe_telemetry t{};
+        t.selected_expert_count = k;
+        t.logical_expert_bytes_requested = working;
+        t.actual_expert_bytes_loaded = loaded;
+        t.resident_cache_bytes_reused = reused;
+        t.weight_bytes_loaded = st.w_loaded;
+        t.weight_bytes_reused = st.w_reused;
+        t.scale_bytes_loaded = st.s_loaded;
+        t.scale_bytes_reused = st.s_reused;
+        if (cache) {
+            t.resident_cache_resident_bytes = cache->st.resident_bytes;
+            t.resident_cache_capacity_bytes = cache->st.capacity_bytes;
+            t.resident_cache_hit_count = cache->st.hit_count;
+            t.resident_cache_miss_count = cache->st.miss_count;
+            t.resident_cache_eviction_count = cache->st.eviction_count;
+        }
+        t.h2d_ms = elapsed(ev[X0], ev[X1]);
+        t.gate_up_qgemv_ms = elapsed(ev[X1], ev[GU1]);
+        t.activation_ms = elapsed(ev[SH1], ev[AQ1]);
+        t.down_qgemv_ms = elapsed(ev[AQ1], ev[DN1]);
+        t.shared_expert_ms = shared_fp8 ? elapsed(ev[GU1], ev[SH1]) + elapsed(ev[DN1], ev[D2H0]) : 0.f;
+        t.total_ms = elapsed(ev[T0], ev[T1]) - elapsed(ev[D2H0], ev[T1]);
+        t.bytes_per_expert = single_expert_bytes;
+        t.selected_working_set_bytes = working;
+        t.routed_fp4_bytes_loaded = loaded;
+        t.routed_fp4_bytes_reused = reused;
+        t.shared_fp8_bytes_loaded = sh_total;
+        t.total_logical_bytes = working + sh_total;
+        t.total_loaded_bytes = loaded + sh_total;
+        t.total_reused_bytes = reused;
         *tel = t;
     }
     return 0;

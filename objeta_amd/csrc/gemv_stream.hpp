@@ -10,6 +10,7 @@
 #pragma once
 
 #include "device_common.hpp"
+#include "quant_rules.hpp"
 
 namespace objeta {
 namespace dev {
@@ -99,6 +100,65 @@ struct Fp4Rows {
     }
 };
 
+// Rows of an FP8 E4M3 matrix (the DeepSeek shared expert): bytes [rows][cols] and
+// E8M0 scales on a 128 x 128 tile grid [ceil(rows/128)][ceil(cols/128)]
+// (deepseek.rs:1630-1661); a 64-weight pair lies inside one tile. Bytes decode with
+// the reference's f8e4m3_to_f32 (deepseek.rs:799-829). cols % 128 == 0.
+struct Fp8Rows {
+    static constexpr int kDw = 17;  // 16 weight dwords + the tile's scale byte
+    const uint8_t* __restrict__ w;
+    const uint8_t* __restrict__ s;
+    size_t wrow;     // bytes per row (cols)
+    uint32_t scols;  // scale tiles per row of tiles
+
+    __device__ __forceinline__ void load(uint32_t r, uint32_t p, uint32_t (&d)[kDw]) const {
+        uint32_t n[16];
+        load_dwords<16>(reinterpret_cast<const uint32_t*>(w + static_cast<size_t>(r) * wrow + p * 64u), n);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d[i] = n[i];
+        d[16] = *as_global(s + static_cast<size_t>(r >> 7) * scols + (p >> 1));
+    }
+    template <int NT>
+    __device__ __forceinline__ void dot(const uint32_t (&d)[kDw], const float* const (&xs)[NT],
+                                        float (&acc)[NT]) const {
+        dot<NT>(d, xs, acc, xs);
+    }
+    template <int NT>
+    __device__ __forceinline__ void dot(const uint32_t (&d)[kDw], const float* const (&xs)[NT],
+                                        float (&acc)[NT], const float* const (&xs_slow)[NT]) const {
+        const float scale = e8m0_to_f32(d[16] & 0xFFu);
+        const bool finite = __builtin_isfinite(scale);
+        float a[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) a[t] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            float wv[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) wv[b] = rules::f8e4m3_to_f32((d[q] >> (8 * b)) & 0xFFu);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float4 xv = *reinterpret_cast<const float4*>(xs[t] + 4 * q);
+                if (finite) {
+                    a[t] = __builtin_fmaf(wv[0], xv.x, a[t]);
+                    a[t] = __builtin_fmaf(wv[1], xv.y, a[t]);
+                    a[t] = __builtin_fmaf(wv[2], xv.z, a[t]);
+                    a[t] = __builtin_fmaf(wv[3], xv.w, a[t]);
+                } else {  // the reference's per-weight w * s (NaN / inf propagate as there)
+                    acc[t] = __builtin_fmaf(wv[0] * scale, xs_slow[t][4 * q], acc[t]);
+                    acc[t] = __builtin_fmaf(wv[1] * scale, xs_slow[t][4 * q + 1], acc[t]);
+                    acc[t] = __builtin_fmaf(wv[2] * scale, xs_slow[t][4 * q + 2], acc[t]);
+                    acc[t] = __builtin_fmaf(wv[3] * scale, xs_slow[t][4 * q + 3], acc[t]);
+                }
+            }
+        }
+        if (finite) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] = __builtin_fmaf(scale, a[t], acc[t]);
+        }
+    }
+};
+
 // A row accessor over one expert tensor: pointer(s) from an expert table entry and
 // the tensor's column count.
 template <class R>
@@ -107,6 +167,12 @@ template <int F>
 struct RowsOf<QRows<F>> {
     static __device__ __forceinline__ QRows<F> make(const void* w, const void*, uint32_t cols) {
         return QRows<F>{static_cast<const uint8_t*>(w), static_cast<size_t>(cols >> 5) * Fmt<F>::kBlockBytes};
+    }
+};
+template <>
+struct RowsOf<Fp8Rows> {
+    static __device__ __forceinline__ Fp8Rows make(const void* w, const void* s, uint32_t cols) {
+        return Fp8Rows{static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(s), cols, (cols + 127) >> 7};
     }
 };
 template <>

@@ -77,7 +77,8 @@ enum WsSlot : int {
     kWsMoeTable = 2,
     kWsGrouped = 3,
     kWsSelTab = 4,
-    kWsSlots = 5
+    kWsOfficial = 5,  // dequantized FP8 activations of the official path
+    kWsSlots = 6
 };
 
 // The scratch of one stream. Calls on different streams of a context may be in

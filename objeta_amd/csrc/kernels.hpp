@@ -19,6 +19,20 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
 
 int32_t launch_zero(hipStream_t s, void* d, uint64_t bytes);
 
+// GEMV over an FP8 E4M3 matrix with 128 x 128 E8M0 scale tiles (cols % 128 == 0).
+int32_t launch_fp8_rows(objeta_hip_context* ctx, hipStream_t s, const void* d_w, const void* d_s,
+                        const float* d_x, float* d_y, uint64_t rows, uint64_t cols, uint64_t batch);
+
+// act_quant (deepseek.rs:1484-1525) of `rows` vectors of `cols` floats (cols % 128
+// == 0): F8_E4M3 bytes to d_values, one E8M0 scale per 128 to d_scales, and when
+// d_deq is set the dequantized values act_v * act_s (the factors of the reference's
+// FP8 GEMVs) as floats. d_deq may alias d_x.
+int32_t launch_act_quant(hipStream_t s, const float* d_x, uint64_t rows, uint64_t cols, uint8_t* d_values,
+                         uint8_t* d_scales, float* d_deq);
+// act_v * act_s as floats for FP8 activations and their 128-element scales.
+int32_t launch_fp8_dequant(hipStream_t s, const uint8_t* d_values, const uint8_t* d_scales, uint64_t rows,
+                           uint64_t cols, float* d_out);
+
 // The router launch behind objeta_hip_router_topk_device (its epoch words and
 // counters are the scratch of stream `s`). With table and sel_tab given and *sel_tab non-null, the router also
 // writes the selected experts' table entries to (*sel_tab)[t * k + r] when it can
@@ -34,12 +48,25 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
                            float* act, uint64_t hidden, uint64_t inter, float limit,
-                           const objeta_hip_expert_ptrs* sel = nullptr, const objeta_hip_expert_ptrs* shared = nullptr);
+                           const objeta_hip_expert_ptrs* sel = nullptr, const objeta_hip_expert_ptrs* shared = nullptr,
+                           bool official = false);
 
 // sel (optional): the assignments' table entries as the router resolved them; the
 // kernels then skip the id and table lookups. shared (optional, a device pointer to
 // one table entry): the shared expert, an extra slot per token with weight 1 added
 // after the routed sum; act then holds k + 1 slots per token.
+// Events recorded after the phases of launch_moe_official_fp4 (each nullable).
+struct OfficialMarks {
+    hipEvent_t gate_up_end, shared_gate_up_end, act_quant_end, down_end;
+};
+// The official-arithmetic FP4 MoE layer (FP8 activations, FP4 split routed experts,
+// optional FP8 shared expert with 128 x 128 scale tiles).
+int32_t launch_moe_official_fp4(objeta_hip_context* ctx, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                                uint64_t n_table, const objeta_hip_expert_ptrs* shared, const uint32_t* ids,
+                                const float* wts, uint64_t n_tokens, uint64_t k, const float* x, float* out,
+                                uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit,
+                                uint8_t* inter_values, uint8_t* inter_scales, const OfficialMarks* marks);
+
 int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                         uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                         const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim,

@@ -23,6 +23,8 @@
 #include "gemv_stream.hpp"
 #include "host_common.hpp"
 #include "kernels.hpp"
+#include "quant_rules.hpp"
+#include "router_math.hpp"
 
 namespace objeta {
 namespace dev {
@@ -36,6 +38,19 @@ __device__ __forceinline__ float silu_mul(float g, float u, float limit) {
     }
     const float silu = g / (1.0f + expf(-g));
     return silu * u;
+}
+
+// The SwiGLU of the official compositions (crates/objeta-parser/src/deepseek.rs:
+// 1680-1686, 1708-1713): only the up projection is clamped, exp is glibc's expf
+// (Rust's f32::exp) and the division is IEEE.
+__device__ __forceinline__ float swiglu_official(float g, float u, float limit) {
+    if (u < -limit) u = -limit;
+    else if (u > limit) u = limit;
+    return rules::div_rn(g, 1.0f + rmath::expf_glibc(-g)) * u;
+}
+
+__device__ __forceinline__ float swiglu(float g, float u, float limit, uint32_t official) {
+    return official ? swiglu_official(g, u, limit) : silu_mul(g, u, limit);
 }
 
 // Expert id of assignment a; ids == nullptr means the identity. Returns false
@@ -72,7 +87,8 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
     uint32_t lpr, uint32_t blocks_per_assign, float limit, uint32_t* __restrict__ err,
-    const objeta_hip_expert_ptrs* __restrict__ sel, uint32_t kk, const objeta_hip_expert_ptrs* __restrict__ shared) {
+    const objeta_hip_expert_ptrs* __restrict__ sel, uint32_t kk, const objeta_hip_expert_ptrs* __restrict__ shared,
+    uint32_t official) {
     extern __shared__ float lds[];
     const uint32_t a = blockIdx.x / blocks_per_assign;
     const uint32_t rb = blockIdx.x - a * blocks_per_assign;
@@ -142,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
         const float v = row_reduce(au[0], lp, lpr);
         const uint32_t r = row0 + static_cast<uint32_t>(u) * gs + slot;
         if (slot < gs && lp == 0 && r < inter)
-            act[static_cast<size_t>(a) * inter + r] = ok ? silu_mul(g, v, limit) : __builtin_nanf("");
+            act[static_cast<size_t>(a) * inter + r] = ok ? swiglu(g, v, limit, official) : __builtin_nanf("");
     }
 }
 
@@ -355,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_general(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
     uint32_t n_assign, float limit, uint32_t* __restrict__ err, uint32_t kk,
-    const objeta_hip_expert_ptrs* __restrict__ shared) {
+    const objeta_hip_expert_ptrs* __restrict__ shared, uint32_t official) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t item = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (item >= n_assign * inter) return;
@@ -369,7 +385,7 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_general(
                                        r, hidden, xt, lane);
     const float u = row_dot_general<F>(static_cast<const uint8_t*>(P.up), static_cast<const uint8_t*>(P.up_scale), r,
                                        hidden, xt, lane);
-    if (lane == 0) act[static_cast<size_t>(a) * inter + r] = ok ? silu_mul(g, u, limit) : __builtin_nanf("");
+    if (lane == 0) act[static_cast<size_t>(a) * inter + r] = ok ? swiglu(g, u, limit, official) : __builtin_nanf("");
 }
 
 // grid.x = ceil(n_tokens * out_dim / 4); one wave per (token, row), slots in order.
@@ -412,6 +428,7 @@ constexpr uint32_t kMaxK = 32;  // selection slots per token (router's top-k bou
 struct MoeShape {
     uint32_t n_table, n_tokens, k, hidden, inter, out_dim;
     const objeta_hip_expert_ptrs* shared = nullptr;
+    bool official = false;  // gate/up applies the official SwiGLU
     uint32_t kk() const { return k + (shared ? 1u : 0u); }
 };
 
@@ -431,7 +448,7 @@ hipError_t gate_up_fast(hipStream_t s, const objeta_hip_expert_ptrs* table, cons
     const size_t lds = static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 4 * sizeof(float);
     hipLaunchKernelGGL((moe_gate_up_kernel<R, U, CH>), dim3(n_assign * bpa), dim3(kThreads), lds, s, table,
                        sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k, lpr, bpa, limit, err, sel, sh.kk(),
-                       sh.shared);
+                       sh.shared, sh.official ? 1u : 0u);
     return hipGetLastError();
 }
 
@@ -469,7 +486,8 @@ hipError_t launch_gate_up_rows(hipStream_t s, const objeta_hip_expert_ptrs* tabl
     // two rows per slot when that still leaves a few workgroups per CU
     const uint32_t gs = 64 / lpr;
     const uint64_t blocks_u2 = static_cast<uint64_t>(sh.n_tokens) * sh.kk() * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2));
-    const bool u2 = blocks_u2 >= 2ull * cus && ch <= 2;
+    // (FP8 rows carry 17 dwords each: two row slots of them would spill)
+    const bool u2 = blocks_u2 >= 2ull * cus && ch <= 2 && R::kDw <= 9;
     switch (ch) {
         case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel)
                           : gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel);
@@ -511,7 +529,7 @@ hipError_t launch_general(hipStream_t s, const objeta_hip_expert_ptrs* table, co
         const uint64_t items = static_cast<uint64_t>(sh.n_tokens) * sh.kk() * sh.inter;
         hipLaunchKernelGGL((moe_gate_up_general<F>), dim3(static_cast<uint32_t>((items + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, s, table, sh.n_table, ids, x, act, sh.hidden, sh.inter, sh.k,
-                           sh.n_tokens * sh.kk(), limit, err, sh.kk(), sh.shared);
+                           sh.n_tokens * sh.kk(), limit, err, sh.kk(), sh.shared, sh.official ? 1u : 0u);
     } else {
         const uint64_t items = static_cast<uint64_t>(sh.n_tokens) * sh.out_dim;
         hipLaunchKernelGGL((moe_down_general<F>), dim3(static_cast<uint32_t>((items + kWaves - 1) / kWaves)),
@@ -559,7 +577,7 @@ MoeShape shape_of(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidd
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
                            float* act, uint64_t hidden, uint64_t inter, float limit,
-                           const objeta_hip_expert_ptrs* sel, const objeta_hip_expert_ptrs* shared) {
+                           const objeta_hip_expert_ptrs* sel, const objeta_hip_expert_ptrs* shared, bool official) {
     const char* action = "launch MoE gate/up";
     OBJ_TRY(validate_moe(action, format, n_table, n_tokens, k, hidden, inter, 1));
     if (n_tokens == 0) return 0;
@@ -567,6 +585,7 @@ int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t 
     if (reinterpret_cast<uintptr_t>(x) % 16) OBJ_FAIL(kInvalidInput, action, "x must be 16-byte aligned");
     MoeShape sh = shape_of(n_table, n_tokens, k, hidden, inter, 1);
     sh.shared = shared;
+    sh.official = official;
     uint32_t* err = ctx->err_word;
     const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
     const bool fast = fast_shape(sh.hidden) && static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 16 <= max_lds(ctx);
@@ -644,6 +663,83 @@ int32_t launch_moe_selected(objeta_hip_context* ctx, int32_t format, hipStream_t
                                shared));
     return launch_moe_down(ctx, format, s, table, n_table, ids, wts, n_tokens, k, act, resid, out, inter, out_dim,
                            sel, shared);
+}
+
+// ------------------------------------------------------- official FP4 layer
+// execute_selected_moe_official_routed_fp4_cuda (moe.rs:1393-1663) for a batch of
+// tokens, in six launches: act_quant(x) dequantized; the routed gate/up (FP4 split
+// weights, official SwiGLU) of every (token, slot); the shared expert's gate/up
+// (FP8 weights) into the rows after them; act_quant of all intermediates,
+// dequantized in place; the routed down with the weighted combine from zero
+// (d_out += w * down in selection order); the shared down added with weight 1.
+// Workspace: x dequantized [n_tokens][hidden], then the intermediates
+// [n_tokens * k routed rows | n_tokens shared rows][inter]. inter_values /
+// inter_scales (nullable) receive the intermediates' FP8 bytes and scales in that
+// row order.
+int32_t launch_moe_official_fp4(objeta_hip_context* ctx, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                                uint64_t n_table, const objeta_hip_expert_ptrs* shared, const uint32_t* ids,
+                                const float* wts, uint64_t n_tokens, uint64_t k, const float* x, float* out,
+                                uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit,
+                                uint8_t* inter_values, uint8_t* inter_scales, const OfficialMarks* marks) {
+    const char* action = "launch official FP4 MoE";
+    // k = 0 (an empty selection) leaves the shared expert alone, over zeros
+    OBJ_TRY(validate_moe(action, OBJETA_HIP_FP4_E2M1, n_table, n_tokens, k ? k : 1, hidden, inter, out_dim));
+    if (hidden % 128 != 0 || inter % 128 != 0)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("hidden %llu and intermediate %llu must be multiples of the act_quant block 128",
+                      (unsigned long long)hidden, (unsigned long long)inter));
+    if (!(limit >= 0.0f)) OBJ_FAIL(kInvalidInput, action, "swiglu_limit must be a number >= 0 (clamp(-l, l))");
+    if (n_tokens == 0 || out_dim == 0) return 0;
+    if ((k && (!table || !ids || !wts)) || !x || !out) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    const uint64_t kk = k + (shared ? 1 : 0);
+    MoeShape ssh = shape_of(1, n_tokens, 0, hidden, inter, out_dim);
+    ssh.shared = shared;
+    ssh.official = true;
+    if (shared) {
+        const bool fits = fast_shape(ssh.hidden) && fast_shape(ssh.inter) &&
+                          static_cast<size_t>(ssh.hidden >> 6) * kPad * sizeof(float) + 16 <= max_lds(ctx) &&
+                          down_lds_bytes(ssh, 1, 1) <= max_lds(ctx);
+        if (!fits)
+            OBJ_FAIL(kUnsupported, action,
+                     strf("FP8 shared expert needs hidden %llu and intermediate %llu with a streaming lane split",
+                          (unsigned long long)hidden, (unsigned long long)inter));
+    }
+    const size_t xb = (static_cast<size_t>(n_tokens * hidden) * sizeof(float) + 255) & ~size_t(255);
+    const size_t ab = static_cast<size_t>(n_tokens * kk * inter) * sizeof(float);
+    void* ws = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsOfficial, xb + ab + 64, &ws));
+    float* xd = static_cast<float*>(ws);
+    float* act = reinterpret_cast<float*>(static_cast<char*>(ws) + xb);
+    float* act_sh = act + n_tokens * k * inter;
+    uint32_t* err = ctx->err_word;
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    auto mark = [&](hipEvent_t e) -> int32_t {
+        if (e) OBJ_HIP(hipEventRecord(e, s), "record event");
+        return 0;
+    };
+    OBJ_TRY(launch_act_quant(s, x, n_tokens, hidden, nullptr, nullptr, xd));
+    if (k)
+        OBJ_TRY(launch_moe_gate_up(ctx, OBJETA_HIP_FP4_E2M1, s, table, n_table, ids, n_tokens, k, xd, act, hidden,
+                                   inter, limit, nullptr, nullptr, true));
+    OBJ_TRY(mark(marks ? marks->gate_up_end : nullptr));
+    if (shared) {
+        const hipError_t e = launch_gate_up_rows<Fp8Rows>(s, shared, nullptr, xd, act_sh, ssh, limit, err, cus, nullptr);
+        if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+    }
+    OBJ_TRY(mark(marks ? marks->shared_gate_up_end : nullptr));
+    if (kk) OBJ_TRY(launch_act_quant(s, act, n_tokens * kk, inter, inter_values, inter_scales, act));
+    OBJ_TRY(mark(marks ? marks->act_quant_end : nullptr));
+    if (k)
+        OBJ_TRY(launch_moe_down(ctx, OBJETA_HIP_FP4_E2M1, s, table, n_table, ids, wts, n_tokens, k, act, nullptr, out,
+                                inter, out_dim));
+    else
+        OBJ_TRY(launch_zero(s, out, n_tokens * out_dim * sizeof(float)));
+    OBJ_TRY(mark(marks ? marks->down_end : nullptr));
+    if (shared) {
+        const hipError_t e = launch_down_rows<Fp8Rows>(s, shared, nullptr, nullptr, act_sh, out, out, ssh, 1, err, nullptr);
+        if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+    }
+    return 0;
 }
 
 // ------------------------------------------------ static activation scratch
@@ -807,6 +903,21 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
     return objeta_hip_moe_layer_shared_device(ctx, format, stream, d_table, n_experts, nullptr, d_router_w,
                                               d_router_bias, k, renormalize, n_tokens, d_x, d_residual, d_out,
                                               d_ids_out, d_weights_out, hidden, intermediate, out_dim, swiglu_limit);
+}
+
+int32_t objeta_hip_moe_official_fp4_device(objeta_hip_context* ctx, objeta_hip_stream stream,
+                                           const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
+                                           const objeta_hip_expert_ptrs* d_shared_fp8, const uint32_t* d_ids,
+                                           const float* d_weights, uint64_t n_tokens, uint64_t k, const float* d_x,
+                                           float* d_out, uint64_t hidden, uint64_t intermediate, uint64_t out_dim,
+                                           float swiglu_limit, uint8_t* d_inter_values, uint8_t* d_inter_scales) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_ctx(ctx, "moe_official_fp4_device"));
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    return launch_moe_official_fp4(ctx, resolve_stream(ctx, stream), d_table, n_table, d_shared_fp8, d_ids, d_weights,
+                                   n_tokens, k, d_x, d_out, hidden, intermediate, out_dim, swiglu_limit,
+                                   d_inter_values, d_inter_scales, nullptr);
+    OBJ_GUARD_END
 }
 
 int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out) {

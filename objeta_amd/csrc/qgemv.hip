@@ -284,6 +284,42 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
     return 0;
 }
 
+int32_t launch_fp8_rows(objeta_hip_context* ctx, hipStream_t s, const void* d_w, const void* d_s,
+                        const float* d_x, float* d_y, uint64_t rows, uint64_t cols, uint64_t batch) {
+    const char* action = "launch fp8_act_fp8_weight_gemv";
+    if (cols % 128 != 0)
+        OBJ_FAIL(kInvalidInput, action, strf("cols %llu must be a multiple of 128", (unsigned long long)cols));
+    if (rows == 0 || batch == 0) return 0;
+    if (!d_w || !d_s || !d_x || !d_y) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
+    if (rows > 0x7FFFFFFFull || cols > 0x7FFFFFFFull) OBJ_FAIL(kInvalidInput, action, "rows/cols exceed 2^31");
+    if (reinterpret_cast<uintptr_t>(d_w) % 16 != 0 || reinterpret_cast<uintptr_t>(d_x) % 16 != 0)
+        OBJ_FAIL(kInvalidInput, action, "weights and activations must be 16-byte aligned");
+    const uint32_t r = static_cast<uint32_t>(rows), c = static_cast<uint32_t>(cols);
+    const uint32_t pairs = c / 64;
+    const uint32_t lpr = pick_lpr(pairs);
+    if (lpr == 0) OBJ_FAIL(kUnsupported, action, strf("cols %u has no lane split", c));
+    const Fp8Rows rm{static_cast<const uint8_t*>(d_w), static_cast<const uint8_t*>(d_s), c, (c + 127) / 128};
+    const size_t per_token = static_cast<size_t>(pairs) * kPad * sizeof(float);
+    uint64_t done = 0;
+    while (done < batch) {
+        const int nt = max_nt_for_lds(per_token, 65536, batch - done);
+        if (nt == 0) OBJ_FAIL(kUnsupported, action, strf("cols %u exceed the LDS activation stage", c));
+        const size_t lds = per_token * nt + 4 * sizeof(float);
+        const float* xb = d_x + done * cols;
+        float* yb = d_y + done * rows;
+        hipError_t e;
+        switch (nt) {
+            case 8: e = launch_stream<Fp8Rows, 8>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
+            case 4: e = launch_stream<Fp8Rows, 4>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
+            case 2: e = launch_stream<Fp8Rows, 2>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
+            default: e = launch_stream<Fp8Rows, 1>(ctx, s, rm, xb, yb, r, c, lpr, lds); break;
+        }
+        if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+        done += static_cast<uint64_t>(nt);
+    }
+    return 0;
+}
+
 }  // namespace objeta
 
 using namespace objeta;

@@ -3,13 +3,19 @@
 // quantize_matrix_cpu (crates/objeta-cuda/src/quant.rs:506-926).
 #pragma once
 
-#include <hip/hip_runtime.h>
 #include <stdint.h>
+
+// Under hipcc the rules are host and device functions; a plain C++ compiler sees
+// ordinary inline functions (the host checks of the scale rules build that way).
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define OBJ_HD __host__ __device__ __forceinline__
+#else
+#define OBJ_HD inline
+#endif
 
 namespace objeta {
 namespace rules {
-
-#define OBJ_HD __host__ __device__ __forceinline__
 
 OBJ_HD uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 OBJ_HD float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -190,6 +196,85 @@ OBJ_HD void fp4_block(const float* src, uint8_t* dst) {
         const uint8_t q1 = fp4_quantize_val(src[2 * i + 1], s);
         dst[1 + i] = static_cast<uint8_t>(q0 | (q1 << 4));
     }
+}
+
+// ------------------------------------------- FP8 official arithmetic (DeepSeek)
+// f8e4m3_to_f32 (crates/objeta-parser/src/deepseek.rs:799-829): exponent field 0
+// decodes as mant * 2^-5 (the reference's subnormal rule), 15 as +-448, the rest as
+// normals (sign, exponent + 120, mantissa << 20).
+OBJ_HD float f8e4m3_to_f32(uint32_t raw) {
+    const uint32_t sign = (raw & 0x80u) << 24;
+    const uint32_t exp = (raw >> 3) & 0x0Fu, mant = raw & 0x07u;
+    if (exp == 0) return u2f(f2u(static_cast<float>(mant) * 0.03125f) | sign);
+    if (exp == 15) return u2f(f2u(448.0f) | sign);
+    return u2f(sign | ((exp + 120u) << 23) | (mant << 20));
+}
+
+// f32_to_f8e4m3_exact (deepseek.rs:1444-1473). Below 1/128 the reference rounds
+// |v| * 16 (always < 0.125, so the code is a signed zero); at or above 448 it
+// saturates to 0x7E / 0xFE; otherwise the exponent is biased by 7 (clamped at 0),
+// the mantissa rounded half-up to 3 bits, and exponents above 14 saturate to 0x77.
+OBJ_HD uint8_t f32_to_f8e4m3_exact(float v) {
+    const uint32_t bits = f2u(v);
+    const uint32_t abits = bits & 0x7FFFFFFFu;
+    const float a = u2f(abits);
+    const bool neg = v < 0.0f;  // false for NaN, as in the reference
+    if (a < 1.0f / 128.0f) {
+        const float q = __builtin_roundf(a * 16.0f);
+        const uint32_t quant = q >= 7.0f ? 7u : static_cast<uint32_t>(q);
+        return static_cast<uint8_t>((neg ? 0x80u : 0u) | quant);
+    }
+    if (a >= 448.0f) return neg ? 0xFEu : 0x7Eu;
+    int32_t exp_f8 = static_cast<int32_t>((abits >> 23) & 0xFFu) - 127 + 7;
+    if (exp_f8 < 0) exp_f8 = 0;
+    uint32_t mant3 = ((abits & 0x7FFFFFu) + (1u << 19)) >> 20;
+    uint32_t exp_final = static_cast<uint32_t>(exp_f8) & 0xFFu;
+    if (mant3 >= 8) {
+        mant3 = 0;
+        exp_final = exp_final == 255 ? 255 : exp_final + 1;
+    }
+    if (exp_final > 14) {
+        exp_final = 14;
+        mant3 = 7;
+    }
+    return static_cast<uint8_t>((neg ? 0x80u : 0u) | (exp_final << 3) | (mant3 & 7u));
+}
+
+// The block exponent of cpu_act_quant (deepseek.rs:1494-1513) for a block maximum
+// amax (NaN already ignored): ceil(log2(max(amax, 1e-4) * (1 / 448))) with glibc's
+// log2f (ceil_log2_cr); the scale is 2^result and its E8M0 byte result + 127.
+OBJ_HD int32_t fp8_act_log2_scale(float amax) {
+    const float m = amax > 1e-4f ? amax : 1e-4f;
+    return ceil_log2_cr(m * (1.0f / 448.0f));
+}
+OBJ_HD uint8_t fp8_act_scale_raw(int32_t log2_scale) {
+    const int32_t e = log2_scale + 127;
+    return static_cast<uint8_t>(e < 0 ? 0 : (e > 255 ? 255 : e));
+}
+
+// The whole block scale of cpu_act_quant: its E8M0 byte and the factor that turns
+// x / scale into one exact multiplication. For finite amax the exponent lies in
+// [-22, 120], so 2^-exponent is a normal float and x * 2^-exponent rounds exactly
+// as x / 2^exponent does. For amax = +inf the reference's `log2().ceil() as i32`
+// saturates to i32::MAX: the byte `e = log2 + 127` wraps negative and clamps to 0,
+// 2^i32::MAX is +inf and x / inf is x * 0 (+-0 for finite x, NaN for +-inf).
+struct Fp8ActScale {
+    uint8_t raw;
+    float inv;
+};
+OBJ_HD Fp8ActScale fp8_act_scale(float amax) {
+    if (amax == __builtin_inff()) return Fp8ActScale{0, 0.0f};
+    const int32_t l = fp8_act_log2_scale(amax);
+    return Fp8ActScale{fp8_act_scale_raw(l), u2f(static_cast<uint32_t>(127 - l) << 23)};
+}
+
+// One element of cpu_act_quant: clamp(x / scale, -448, 448) encoded (NaN stays NaN
+// through the clamp, as f32::clamp keeps it).
+OBJ_HD uint8_t fp8_act_code(float x, float inv) {
+    float v = x * inv;
+    if (v < -448.0f) v = -448.0f;
+    else if (v > 448.0f) v = 448.0f;
+    return f32_to_f8e4m3_exact(v);
 }
 
 // Counter-based synthetic generator: element i of stream `seed` is

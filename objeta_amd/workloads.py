@@ -55,3 +55,26 @@ def fp4_random_expert(hidden: int, inter: int, out_dim: int, seed: int):
     uw, us = fp4_random_split(inter, hidden, seed + 1)
     dw, ds = fp4_random_split(out_dim, inter, seed + 2)
     return gw, gs, uw, us, dw, ds
+
+
+def fp8_random_tiles(rows: int, cols: int, seed: int):
+    """(weights [rows * cols] u8, scales [ceil(rows/128) * ceil(cols/128)] u8): random
+    F8_E4M3 bytes with E8M0 128 x 128 tile scales in [119, 127], the layout of the
+    DeepSeek FP8 shared expert. Weight byte i is byte i mod 8 of splitmix64(kw + i / 8)."""
+    with np.errstate(over="ignore"):
+        kw = splitmix64(np.array([seed ^ 0xF8F8F8F8], np.uint64))[0]
+        ks = splitmix64(np.array([seed ^ 0x5CA1E5CA1E5CA1E5 ^ 0xF8], np.uint64))[0]
+        n_w = rows * cols
+        n_s = ((rows + 127) // 128) * ((cols + 127) // 128)
+        words = splitmix64(kw + np.arange((n_w + 7) // 8, dtype=np.uint64))
+        w = words.view(np.uint8)[:n_w].copy()
+        sc = (np.uint64(119) + splitmix64(ks + np.arange(n_s, dtype=np.uint64)) % np.uint64(9)).astype(np.uint8)
+    return w, sc
+
+
+def fp8_random_expert(hidden: int, inter: int, out_dim: int, seed: int):
+    """(gate_w, gate_s, up_w, up_s, down_w, down_s) of one FP8 shared expert."""
+    gw, gs = fp8_random_tiles(inter, hidden, seed)
+    uw, us = fp8_random_tiles(inter, hidden, seed + 1)
+    dw, ds = fp8_random_tiles(out_dim, inter, seed + 2)
+    return gw, gs, uw, us, dw, ds

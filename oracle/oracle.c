@@ -693,3 +693,183 @@ size_t orc_expf_double_disagreements(uint32_t lo_bits, uint32_t hi_bits, float* 
     }
     return n;
 }
+
+/* ------------------------------------------------------ FP8 official arithmetic
+ * The DeepSeek "official arithmetic" CPU path of crates/objeta-parser/src/deepseek.rs:
+ * activations quantized to F8_E4M3 bytes with one F8_E8M0 scale per 128 elements,
+ * FP8 x FP4 and FP8 x FP8 GEMVs, and the routed / shared expert compositions. */
+
+/* f8e4m3_to_f32, deepseek.rs:799-829: exponent field 0 decodes as mant * 2^-5 (the
+ * reference's subnormal rule), 15 as +-448, the rest as IEEE-style normals. */
+float orc_f8e4m3_to_f32(uint8_t raw) {
+    const uint32_t sign = raw >> 7, exp = (raw >> 3) & 0x0Fu, mant = raw & 0x07u;
+    if (exp == 0) {
+        if (mant == 0) return u2f(sign << 31);
+        return (float)mant * 0.03125f * (sign == 0 ? 1.0f : -1.0f); /* 2f32.powi(1 - 6) = 2^-5 */
+    }
+    if (exp == 15) return sign == 0 ? 448.0f : -448.0f;
+    return u2f((sign << 31) | ((exp + 120u) << 23) | (mant << 20));
+}
+
+/* f32_to_f8e4m3_exact, deepseek.rs:1444-1473. */
+uint8_t orc_f32_to_f8e4m3_exact(float v) {
+    if (fabsf(v) < 1.0f / 128.0f) { /* below min normal */
+        const uint8_t sign = v < 0.0f ? 0x80u : 0u;
+        const float scaled = fabsf(v) * 16.0f;
+        float q = roundf(scaled); /* f32::round, half away from zero; `as u8` saturates */
+        uint8_t quant = q >= 255.0f ? 255u : (uint8_t)q;
+        return (uint8_t)(sign | (quant < 7 ? quant : 7));
+    }
+    if (fabsf(v) >= 448.0f) return v < 0.0f ? 0xFEu : 0x7Eu;
+    const uint8_t sign = v < 0.0f ? 0x80u : 0u;
+    const uint32_t bits = f2u(fabsf(v));
+    const int32_t exp32 = (int32_t)((bits >> 23) & 0xFFu) - 127;
+    int32_t exp_f8 = exp32 + 7;
+    if (exp_f8 < 0) exp_f8 = 0;
+    const uint32_t mant_bits = bits & 0x7FFFFFu;
+    uint8_t mant3 = (uint8_t)((mant_bits + (1u << 19)) >> 20);
+    uint8_t exp_final = (uint8_t)exp_f8;
+    if (mant3 >= 8) {
+        mant3 = 0;
+        exp_final = exp_final == 255 ? 255 : (uint8_t)(exp_final + 1);
+    }
+    if (exp_final > 14) {
+        exp_final = 14;
+        mant3 = 7;
+    }
+    return (uint8_t)(sign | (exp_final << 3) | (mant3 & 7));
+}
+
+/* cpu_act_quant, deepseek.rs:1484-1525: per block, amax = max |x| (NaN ignored) and at
+ * least 1e-4; scale = 2^ceil(log2(amax * (1/448))); y = f32_to_f8e4m3_exact(clamp(x /
+ * scale, -448, 448)); s = clamp(log2 scale + 127, 0, 255). n % block == 0. */
+void orc_act_quant(const float* x, size_t n, size_t block, uint8_t* y, uint8_t* s) {
+    const float fp8_max = 448.0f, fp8_max_inv = 1.0f / 448.0f;
+    for (size_t b = 0; b < n / block; ++b) {
+        const size_t start = b * block, end = start + block;
+        float amax = 0.0f;
+        for (size_t i = start; i < end; ++i) {
+            const float a = fabsf(x[i]);
+            if (a > amax) amax = a;
+        }
+        amax = fmaxf(amax, 1e-4f);
+        const float raw = amax * fp8_max_inv;
+        float scale;
+        if (isinf(raw)) {
+            /* `inf.log2().ceil() as i32` saturates to i32::MAX; e = MAX + 127 wraps
+             * negative in a release build (byte 0) and 2f32.powi(MAX) is +inf */
+            scale = INFINITY;
+            s[b] = 0;
+        } else {
+            const int32_t log2_ceil = raw > 0.0f ? (int32_t)ceilf(log2f(raw)) : -127;
+            /* 2.0f32.powi(log2_ceil): an exact power of two over the range raw can take */
+            scale = ldexpf(1.0f, log2_ceil);
+            const int32_t e = log2_ceil + 127;
+            s[b] = (uint8_t)(e < 0 ? 0 : (e > 255 ? 255 : e));
+        }
+        for (size_t i = start; i < end; ++i) {
+            float v = x[i] / scale;
+            if (v < -fp8_max) v = -fp8_max;
+            else if (v > fp8_max) v = fp8_max;
+            y[i] = orc_f32_to_f8e4m3_exact(v);
+        }
+    }
+}
+
+/* cpu_fp8_act_fp4_weight_gemv_f32, deepseek.rs:1528-1566: per row, over byte
+ * col_group, the low then the high nibble, sum += act_v * act_s * fp4 * ws in f32. */
+void orc_fp8_act_fp4_weight_gemv_f32(const uint8_t* act_v, const uint8_t* act_s, const uint8_t* w,
+                                     const uint8_t* ws, size_t rows, size_t cols, float* out) {
+    const size_t phys = cols / 2, scols = cols / 32;
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
+    for (size_t r = 0; r < rows; ++r) {
+        float sum = 0.0f;
+        for (size_t g = 0; g < phys; ++g) {
+            const uint8_t bv = w[r * phys + g];
+            const size_t lo = g * 2, hi = lo + 1;
+            const float fp4_lo = FP4_E2M1FN_TABLE[bv & 0x0F], fp4_hi = FP4_E2M1FN_TABLE[(bv >> 4) & 0x0F];
+            const float ws_lo = orc_f8e8m0_to_f32(ws[r * scols + lo / 32]);
+            const float ws_hi = orc_f8e8m0_to_f32(ws[r * scols + hi / 32]);
+            const float av_lo = orc_f8e4m3_to_f32(act_v[lo]), av_hi = orc_f8e4m3_to_f32(act_v[hi]);
+            const float as_lo = orc_f8e8m0_to_f32(act_s[lo / 128]), as_hi = orc_f8e8m0_to_f32(act_s[hi / 128]);
+            sum = sum + av_lo * as_lo * fp4_lo * ws_lo;
+            sum = sum + av_hi * as_hi * fp4_hi * ws_hi;
+        }
+        out[r] = sum;
+    }
+}
+
+/* cpu_fp8_act_fp8_weight_gemv, deepseek.rs:1630-1661: weight scales on a 128 x 128
+ * tile grid [ceil(rows/128)][ceil(cols/128)], products and sum in f64, result
+ * rounded to f32. */
+void orc_fp8_act_fp8_weight_gemv(const uint8_t* act_v, const uint8_t* act_s, const uint8_t* w,
+                                 const uint8_t* ws, size_t rows, size_t cols, float* out) {
+    const size_t wt_scale_cols = (cols + 127) / 128;
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
+    for (size_t r = 0; r < rows; ++r) {
+        const size_t srow = r / 128;
+        double sum = 0.0;
+        for (size_t c = 0; c < cols; ++c) {
+            const float av = orc_f8e4m3_to_f32(act_v[c]);
+            const float as = orc_f8e8m0_to_f32(act_s[c / 128]);
+            const float wv = orc_f8e4m3_to_f32(w[r * cols + c]);
+            const float wsv = orc_f8e8m0_to_f32(ws[srow * wt_scale_cols + c / 128]);
+            sum += (double)av * (double)as * (double)wv * (double)wsv;
+        }
+        out[r] = (float)sum;
+    }
+}
+
+/* The SwiGLU of the official compositions (deepseek.rs:1680-1686, 1708-1713): only the
+ * up projection is clamped; act = g / (1 + exp(-g)) * clamp(u). */
+static void official_swiglu(const float* g, const float* u, float* act, size_t n, float limit) {
+    for (size_t i = 0; i < n; ++i) {
+        float uc = u[i];
+        if (uc < -limit) uc = -limit;
+        else if (uc > limit) uc = limit;
+        act[i] = g[i] / (1.0f + expf(-g[i])) * uc;
+    }
+}
+
+/* cpu_routed_expert_fp4_official_f32 (deepseek.rs:1694-1716) with FP4 split weights,
+ * and cpu_shared_expert_fp8_official (deepseek.rs:1664-1692) with FP8 weights on a
+ * 128 x 128 scale tile grid. act_pre (nullable, [inter]) receives the activation
+ * before its act_quant, act_q / act_qs (nullable) its FP8 bytes and scales. */
+int orc_expert_official(int fp8_weights, const uint8_t* gw, const uint8_t* gs, const uint8_t* uw,
+                        const uint8_t* us, const uint8_t* dw, const uint8_t* ds, const float* x,
+                        size_t dim, size_t inter, float swiglu_limit, float* out, float* act_pre,
+                        uint8_t* act_q, uint8_t* act_qs, char* err, size_t err_len) {
+    if (dim % 128 != 0 || inter % 128 != 0)
+        return fail(K_INVALID_INPUT, err, err_len, "dim %zu and inter %zu must be multiples of 128", dim, inter);
+    uint8_t* xq = (uint8_t*)malloc(dim);
+    uint8_t* xs = (uint8_t*)malloc(dim / 128);
+    float* g = (float*)malloc(inter * sizeof(float));
+    float* u = (float*)malloc(inter * sizeof(float));
+    float* a = (float*)malloc(inter * sizeof(float));
+    uint8_t* aq = (uint8_t*)malloc(inter);
+    uint8_t* as = (uint8_t*)malloc(inter / 128);
+    orc_act_quant(x, dim, 128, xq, xs);
+    if (fp8_weights) {
+        orc_fp8_act_fp8_weight_gemv(xq, xs, gw, gs, inter, dim, g);
+        orc_fp8_act_fp8_weight_gemv(xq, xs, uw, us, inter, dim, u);
+    } else {
+        orc_fp8_act_fp4_weight_gemv_f32(xq, xs, gw, gs, inter, dim, g);
+        orc_fp8_act_fp4_weight_gemv_f32(xq, xs, uw, us, inter, dim, u);
+    }
+    official_swiglu(g, u, a, inter, swiglu_limit);
+    orc_act_quant(a, inter, 128, aq, as);
+    if (fp8_weights) orc_fp8_act_fp8_weight_gemv(aq, as, dw, ds, dim, inter, out);
+    else orc_fp8_act_fp4_weight_gemv_f32(aq, as, dw, ds, dim, inter, out);
+    if (act_pre) memcpy(act_pre, a, inter * sizeof(float));
+    if (act_q) memcpy(act_q, aq, inter);
+    if (act_qs) memcpy(act_qs, as, inter / 128);
+    free(xq); free(xs); free(g); free(u); free(a); free(aq); free(as);
+    return 0;
+}
+
+void orc_f8e4m3_to_f32_n(const uint8_t* raw, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f8e4m3_to_f32(raw[i]);
+}
+void orc_f32_to_f8e4m3_exact_n(const float* v, uint8_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f32_to_f8e4m3_exact(v[i]);
+}

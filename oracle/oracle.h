@@ -102,6 +102,24 @@ int orc_router(const float* w_r, const float* bias, const float* x, size_t n_exp
 /* compare_outputs (quant.rs:676-723): out[0]=cosine, out[1]=rel_l2, out[2]=max_abs. */
 int orc_compare(const float* ref, const float* act, size_t n, float* out3);
 
+/* FP8 official arithmetic (crates/objeta-parser/src/deepseek.rs): F8_E4M3 decode and
+ * encode, act_quant (128-element E8M0 blocks), the FP8 x FP4 (f32 sums) and FP8 x FP8
+ * (f64 sums) GEMVs, and one expert of the official routed (fp8_weights = 0, FP4 split
+ * weights) or shared (fp8_weights = 1) composition. */
+float orc_f8e4m3_to_f32(uint8_t raw);
+uint8_t orc_f32_to_f8e4m3_exact(float v);
+void orc_act_quant(const float* x, size_t n, size_t block, uint8_t* y, uint8_t* s);
+void orc_f8e4m3_to_f32_n(const uint8_t* raw, float* out, size_t n);
+void orc_f32_to_f8e4m3_exact_n(const float* v, uint8_t* out, size_t n);
+void orc_fp8_act_fp4_weight_gemv_f32(const uint8_t* act_v, const uint8_t* act_s, const uint8_t* w,
+                                     const uint8_t* ws, size_t rows, size_t cols, float* out);
+void orc_fp8_act_fp8_weight_gemv(const uint8_t* act_v, const uint8_t* act_s, const uint8_t* w,
+                                 const uint8_t* ws, size_t rows, size_t cols, float* out);
+int orc_expert_official(int fp8_weights, const uint8_t* gw, const uint8_t* gs, const uint8_t* uw,
+                        const uint8_t* us, const uint8_t* dw, const uint8_t* ds, const float* x,
+                        size_t dim, size_t inter, float swiglu_limit, float* out, float* act_pre,
+                        uint8_t* act_q, uint8_t* act_qs, char* err, size_t err_len);
+
 /* Threads of the row loops (default 1, the reference's single thread); results are
  * identical for every count because each row's sum stays sequential. */
 void orc_set_threads(int n);

@@ -76,6 +76,17 @@ def _declare(L):
     L.orc_gauss_fill.argtypes = [C.c_uint64, C.c_uint64, C.c_float, P, SZ]
     L.orc_splitmix64.argtypes = [C.c_uint64]
     L.orc_splitmix64.restype = C.c_uint64
+    L.orc_f8e4m3_to_f32.argtypes = [C.c_uint8]
+    L.orc_f8e4m3_to_f32.restype = C.c_float
+    L.orc_f32_to_f8e4m3_exact.argtypes = [C.c_float]
+    L.orc_f32_to_f8e4m3_exact.restype = C.c_uint8
+    L.orc_f8e4m3_to_f32_n.argtypes = [P, P, SZ]
+    L.orc_f32_to_f8e4m3_exact_n.argtypes = [P, P, SZ]
+    L.orc_act_quant.argtypes = [P, SZ, SZ, P, P]
+    L.orc_fp8_act_fp4_weight_gemv_f32.argtypes = [P, P, P, P, SZ, SZ, P]
+    L.orc_fp8_act_fp8_weight_gemv.argtypes = [P, P, P, P, SZ, SZ, P]
+    L.orc_expert_official.argtypes = [C.c_int, P, P, P, P, P, P, P, SZ, SZ, C.c_float, P, P, P, P, C.c_char_p,
+                                      SZ]
     L.orc_set_threads.argtypes = [C.c_int]
     L.orc_get_threads.restype = C.c_int
     L.orc_expf_glibc.argtypes = [P, P, SZ]
@@ -263,6 +274,69 @@ def router(w_r, x, n_experts: int, hidden: int, k: int, bias=None, renormalize=T
                           _ptr(probs), err, 256)
     _check(rc, err)
     return ids, ws, logits, probs
+
+
+# ------------------------------------------------------ FP8 official arithmetic
+def f8e4m3_to_f32(raw) -> np.ndarray:
+    """f8e4m3_to_f32 (deepseek.rs:799-829) element-wise."""
+    r = _u8(raw).ravel()
+    out = np.empty(r.size, np.float32)
+    lib().orc_f8e4m3_to_f32_n(_ptr(r), _ptr(out), r.size)
+    return out
+
+
+def f32_to_f8e4m3(v) -> np.ndarray:
+    """f32_to_f8e4m3_exact (deepseek.rs:1444-1473) element-wise."""
+    x = _f32(v).ravel()
+    out = np.empty(x.size, np.uint8)
+    lib().orc_f32_to_f8e4m3_exact_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def act_quant(x, block: int = 128):
+    """cpu_act_quant (deepseek.rs:1484-1525): (F8_E4M3 bytes, F8_E8M0 scales)."""
+    x = _f32(x).ravel()
+    assert x.size % block == 0
+    y = np.empty(x.size, np.uint8)
+    sc = np.empty(x.size // block, np.uint8)
+    lib().orc_act_quant(_ptr(x), x.size, block, _ptr(y), _ptr(sc))
+    return y, sc
+
+
+def fp8_act_fp4_gemv(act_v, act_s, w, ws, rows: int, cols: int) -> np.ndarray:
+    """cpu_fp8_act_fp4_weight_gemv_f32 (deepseek.rs:1528-1566)."""
+    a, s_, w, ws = _u8(act_v), _u8(act_s), _u8(w), _u8(ws)
+    out = np.empty(rows, np.float32)
+    lib().orc_fp8_act_fp4_weight_gemv_f32(_ptr(a), _ptr(s_), _ptr(w), _ptr(ws), rows, cols, _ptr(out))
+    return out
+
+
+def fp8_act_fp8_gemv(act_v, act_s, w, ws, rows: int, cols: int) -> np.ndarray:
+    """cpu_fp8_act_fp8_weight_gemv (deepseek.rs:1630-1661), f64 sums."""
+    a, s_, w, ws = _u8(act_v), _u8(act_s), _u8(w), _u8(ws)
+    out = np.empty(rows, np.float32)
+    lib().orc_fp8_act_fp8_weight_gemv(_ptr(a), _ptr(s_), _ptr(w), _ptr(ws), rows, cols, _ptr(out))
+    return out
+
+
+def expert_official(fp8_weights: bool, ex, x, dim: int, inter: int, swiglu_limit: float = 10.0):
+    """One expert of the official composition: cpu_routed_expert_fp4_official_f32
+    (deepseek.rs:1694-1716; ex = FP4 split (gw, gs, uw, us, dw, ds)) or
+    cpu_shared_expert_fp8_official (deepseek.rs:1664-1692; ex = FP8 weights with
+    128 x 128 tile scales). dim is both the input and the output length, as in the
+    reference's compositions. Returns (out, act before its act_quant, act bytes, act
+    scales)."""
+    parts = [_u8(a) for a in ex]
+    x = _f32(x).ravel()
+    out = np.empty(dim, np.float32)
+    pre = np.empty(inter, np.float32)
+    aq = np.empty(inter, np.uint8)
+    asc = np.empty(inter // 128, np.uint8)
+    err = C.create_string_buffer(256)
+    rc = lib().orc_expert_official(1 if fp8_weights else 0, *[_ptr(p) for p in parts], _ptr(x), dim, inter,
+                                   swiglu_limit, _ptr(out), _ptr(pre), _ptr(aq), _ptr(asc), err, 256)
+    _check(rc, err)
+    return out, pre, aq, asc
 
 
 def set_threads(n: int) -> None:
