@@ -415,6 +415,25 @@ typedef struct {
     int32_t reserved;
 } objeta_hip_cache_stats;
 
+/* One expert's host tensors: gate/up/down bytes (and, for FP4, the E8M0 scale
+ * arrays) with their lengths. Mirrors ExpertWeights (moe.rs:13-18) and
+ * DeepSeekFp4ExpertWeights (moe.rs:27-35). Pinned host memory
+ * (objeta_hip_alloc_pinned_host) lets cache misses overlap compute. */
+typedef struct {
+    const void* gate;
+    uint64_t gate_len;
+    const void* up;
+    uint64_t up_len;
+    const void* down;
+    uint64_t down_len;
+    const void* gate_scale;
+    uint64_t gate_scale_len;
+    const void* up_scale;
+    uint64_t up_scale_len;
+    const void* down_scale;
+    uint64_t down_scale_len;
+} objeta_hip_host_expert;
+
 /* A single-GPU VRAM expert cache: LRU over tensors, pinned (never evicted) entries,
  * admission by size. Device memory comes from blocks that are recycled after an
  * eviction only once every stream of the context has passed the point of the
@@ -460,6 +479,25 @@ int32_t objeta_hip_cache_clear(objeta_hip_expert_cache* cache);
 int32_t objeta_hip_cache_reset_counters(objeta_hip_expert_cache* cache);
 /* Returns a transient copy made by insert/get_or_insert with *cached == 0. */
 int32_t objeta_hip_cache_release_transient(objeta_hip_expert_cache* cache, const void* d_ptr);
+/* Cross-layer prefetch: starts the copies of host tensors into the cache on the
+ * context's copy stream and returns without waiting, so that a later call finds
+ * them resident (executor calls order their kernels after the copy; cache_get waits
+ * for it on the host). Keys already resident, and tensors larger than the capacity,
+ * are skipped; the others are admitted as insert admits them (counted as inserts,
+ * evicting least recent entries). Not a get: hit and miss counters are unchanged.
+ * No counterpart in the reference, whose executor copies misses synchronously.
+ * *issued (nullable) = copies started. h_srcs must stay valid until the copies end
+ * (pinned host memory lets them run asynchronously). */
+int32_t objeta_hip_cache_prefetch(objeta_hip_expert_cache* cache, const objeta_hip_cache_key* keys,
+                                  const void* const* h_srcs, const uint64_t* nbytes, uint64_t n, uint64_t* issued);
+/* The shared-expert preload of deepseek_single_layer_moe.rs:1698-1730: for each of
+ * n_layers layers, insert_pinned of the six FP8 shared tensors (gate weight/scale,
+ * up weight/scale, down weight/scale of shared[l]) under the keys (first_layer + l,
+ * 0, OBJETA_HIP_TENSOR_SHARED_*, OBJETA_HIP_FP4_E2M1). *bytes / *ms (nullable): the
+ * bytes preloaded and the host time including the copies. */
+int32_t objeta_hip_cache_preload_shared(objeta_hip_expert_cache* cache, const objeta_hip_host_expert* shared,
+                                        uint64_t n_layers, uint64_t first_layer, objeta_hip_stream stream,
+                                        uint64_t* bytes, float* ms);
 /* The keys in LRU order (least recent first), up to cap of them; *n = count. */
 int32_t objeta_hip_cache_order(const objeta_hip_expert_cache* cache, objeta_hip_cache_key* keys, uint64_t cap,
                                uint64_t* n);
@@ -524,24 +562,6 @@ int32_t objeta_hip_moe_official_fp4_device(objeta_hip_context* ctx, objeta_hip_s
                                            float swiglu_limit, uint8_t* d_inter_values, uint8_t* d_inter_scales);
 
 /* ------------------------------------------------ host-in/host-out executor */
-/* One expert's host tensors: gate/up/down bytes (and, for FP4, the E8M0 scale
- * arrays) with their lengths. Mirrors ExpertWeights (moe.rs:13-18) and
- * DeepSeekFp4ExpertWeights (moe.rs:27-35). Pinned host memory
- * (objeta_hip_alloc_pinned_host) lets cache misses overlap compute. */
-typedef struct {
-    const void* gate;
-    uint64_t gate_len;
-    const void* up;
-    uint64_t up_len;
-    const void* down;
-    uint64_t down_len;
-    const void* gate_scale;
-    uint64_t gate_scale_len;
-    const void* up_scale;
-    uint64_t up_scale_len;
-    const void* down_scale;
-    uint64_t down_scale_len;
-} objeta_hip_host_expert;
 
 /* MoeTelemetry (moe.rs:236-276); bytes_by_tensor_kind flattened. The fused
  * kernels report their time under gate_up_qgemv_ms (gate + up + SiLU) and
@@ -615,14 +635,19 @@ int32_t objeta_hip_moe_execute_selected(objeta_hip_context* ctx, int32_t format,
  * logical bytes = the unique selected experts' working set; routed_fp4_* and
  * shared_fp8_* / total_* fields filled; resident-cache counters other than
  * hit/miss/eviction 0; activation_ms = the intermediate act_quant; shared_expert_ms =
- * the shared expert's launches. */
+ * the shared expert's launches. shared_from_cache != 0 (with a cache) first resolves
+ * the shared expert from the cache's entries (layer_id, 0, OBJETA_HIP_TENSOR_SHARED_*,
+ * OBJETA_HIP_FP4_E2M1), as objeta_hip_cache_preload_shared leaves them, by get in
+ * key order stopping at the first miss (the sketch in
+ * crates/objeta-cuda/src/moe_tmp.txt:1-35); shared_fp8 is the fallback. A shared
+ * expert from the cache counts its resident bytes under shared_fp8_bytes_reused. */
 int32_t objeta_hip_moe_execute_official_fp4(objeta_hip_context* ctx, objeta_hip_stream stream,
                                             const objeta_hip_host_expert* experts, uint64_t n_experts,
                                             const uint64_t* sel_ids, const float* sel_weights, uint64_t n_selected,
                                             const float* x, uint64_t x_len, uint64_t hidden, uint64_t intermediate,
                                             uint64_t out_dim, uint64_t layer_id, objeta_hip_expert_cache* cache,
-                                            const objeta_hip_expert_ptrs* shared_fp8, float swiglu_limit, float* out,
-                                            objeta_hip_moe_telemetry* tel);
+                                            const objeta_hip_expert_ptrs* shared_fp8, int32_t shared_from_cache,
+                                            float swiglu_limit, float* out, objeta_hip_moe_telemetry* tel);
 
 #ifdef __cplusplus
 }

@@ -5,9 +5,9 @@ this package is the Python mirror of the reference API used by tests and the
 benchmark.
 """
 from .api import (DeviceBuffer, ExpertCache, ExpertCacheKey, ExpertTable, ExpertTensorKind, HipBackend,
-                  HipBackendBuilder, HipError, MoeExecutor, PinnedHostBuffer, QGemvShape, QuantBackend, QuantFormat, check,
+                  HipBackendBuilder, HipError, HostExpertSet, MoeExecutor, PinnedHostBuffer, QGemvShape, QuantBackend, QuantFormat, check,
                   discover_devices)
 
 __all__ = ["DeviceBuffer", "ExpertCache", "ExpertCacheKey", "ExpertTable", "ExpertTensorKind", "HipBackend",
-           "HipBackendBuilder", "HipError", "MoeExecutor", "PinnedHostBuffer", "QGemvShape", "QuantBackend", "QuantFormat", "check",
+           "HipBackendBuilder", "HipError", "HostExpertSet", "MoeExecutor", "PinnedHostBuffer", "QGemvShape", "QuantBackend", "QuantFormat", "check",
            "discover_devices"]

@@ -170,7 +170,9 @@ SIGNATURES = {
     "objeta_hip_moe_official_fp4_device": (I32, [P, P, P, U64, P, P, P, U64, U64, P, P, U64, U64, U64, F32,
                                                  P, P]),
     "objeta_hip_moe_execute_official_fp4": (I32, [P, P, P, U64, P, P, U64, P, U64, U64, U64, U64, U64, P, P,
-                                                  F32, P, P]),
+                                                  I32, F32, P, P]),
+    "objeta_hip_cache_prefetch": (I32, [P, P, P, P, U64, P]),
+    "objeta_hip_cache_preload_shared": (I32, [P, P, U64, U64, P, P, P]),
 }
 
 

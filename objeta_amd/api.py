@@ -567,6 +567,37 @@ class ExpertCache:
     def release_transient(self, ptr: int) -> None:
         check(self.L.objeta_hip_cache_release_transient(self.h, C.c_void_p(ptr)))
 
+    def prefetch(self, items) -> int:
+        """Cross-layer prefetch: items = [(ExpertCacheKey, host array)]; starts the copies
+        of the absent ones on the copy stream and returns the number started. The host
+        arrays must stay alive until the copies end (pinned memory lets them overlap)."""
+        items = list(items)
+        n = len(items)
+        keys = (CacheKey * max(1, n))()
+        srcs = (C.c_void_p * max(1, n))()
+        sizes = (C.c_uint64 * max(1, n))()
+        for i, (k, a) in enumerate(items):
+            a = np.asarray(a)
+            if not a.flags.c_contiguous:
+                raise ValueError("prefetch needs contiguous host arrays (they are read after the call returns)")
+            keys[i] = k.c()
+            srcs[i] = a.ctypes.data
+            sizes[i] = a.nbytes
+        issued = C.c_uint64(0)
+        check(self.L.objeta_hip_cache_prefetch(self.h, keys, srcs, sizes, n, C.byref(issued)))
+        return issued.value
+
+    def preload_shared(self, shared_experts, first_layer: int = 0, stream=None):
+        """The shared-expert preload (deepseek_single_layer_moe.rs:1698-1730): insert_pinned of
+        every layer's six FP8 shared tensors, shared_experts = [(gate_w, gate_s, up_w, up_s,
+        down_w, down_s)] per layer. Returns (bytes, ms)."""
+        arr, keep = _host_experts(shared_experts)
+        nbytes, ms = C.c_uint64(0), C.c_float(0)
+        check(self.L.objeta_hip_cache_preload_shared(self.h, arr, len(shared_experts), first_layer, stream,
+                                                     C.byref(nbytes), C.byref(ms)))
+        del keep
+        return nbytes.value, ms.value
+
     def pin(self, key: ExpertCacheKey) -> None:
         k = key.c()
         check(self.L.objeta_hip_cache_pin(self.h, C.byref(k)))
@@ -603,9 +634,24 @@ def _telemetry_moe(t: MoeTelemetry) -> dict:
     return d
 
 
+class HostExpertSet:
+    """A layer's host expert tensors marshalled once for the executor entry points
+    (the reference passes &[ExpertWeights]; rebuilding the C array on every call costs
+    about a millisecond of Python at 128 experts). Keeps the arrays alive."""
+
+    def __init__(self, experts):
+        self.arr, self.keep = _host_experts(experts)
+        self.n = len(experts)
+
+    def __len__(self) -> int:
+        return self.n
+
+
 def _host_experts(experts):
     """(HostExpert array, kept arrays) for [(gate, up, down)] or
     [(gate_w, gate_s, up_w, up_s, down_w, down_s)] host tensors."""
+    if isinstance(experts, HostExpertSet):
+        return experts.arr, experts.keep
     keep = []
     arr = (HostExpert * max(1, len(experts)))()
     for i, e in enumerate(experts):
@@ -656,11 +702,13 @@ def _moe_execute_native_fp4(self, quant, stream, experts, selected_experts, x, h
 
 def _moe_execute_official_fp4(self, quant, stream, experts, selected_experts, hidden_state, hidden_size: int,
                               intermediate_size: int, out_dim: int, layer_id: int,
-                              cache: ExpertCache | None = None, shared_expert=None, swiglu_limit: float = 10.0):
+                              cache: ExpertCache | None = None, shared_expert=None, swiglu_limit: float = 10.0,
+                              shared_from_cache: bool = False):
     """execute_selected_moe_official_routed_fp4_cuda (moe.rs:1393-1663): experts =
-    [(gate_w, gate_s, up_w, up_s, down_w, down_s)] split-FP4 host bytes; shared_expert =
-    (gate_w, up_w, down_w, gate_s, up_s, down_s) device addresses of the FP8 shared
-    expert, or None. Returns (out, telemetry)."""
+    [(gate_w, gate_s, up_w, up_s, down_w, down_s)] split-FP4 host bytes (or a
+    HostExpertSet); shared_expert = (gate_w, up_w, down_w, gate_s, up_s, down_s) device
+    addresses of the FP8 shared expert, or None; shared_from_cache resolves the shared
+    expert from the cache's preloaded entries first. Returns (out, telemetry)."""
     arr, keep = _host_experts(experts)
     ids = np.array([s[0] for s in selected_experts], np.uint64)
     ws = np.array([s[1] for s in selected_experts], np.float32)
@@ -673,8 +721,8 @@ def _moe_execute_official_fp4(self, quant, stream, experts, selected_experts, hi
     check(self.L.objeta_hip_moe_execute_official_fp4(
         self.backend.ctx, stream, arr, len(experts), ids.ctypes.data_as(C.c_void_p), ws.ctypes.data_as(C.c_void_p),
         ids.size, xv.ctypes.data_as(C.c_void_p), xv.size, hidden_size, intermediate_size, out_dim, layer_id,
-        cache.h if cache is not None else None, None if sh is None else C.byref(sh), swiglu_limit,
-        out.ctypes.data_as(C.c_void_p), C.byref(tel)))
+        cache.h if cache is not None else None, None if sh is None else C.byref(sh), 1 if shared_from_cache else 0,
+        swiglu_limit, out.ctypes.data_as(C.c_void_p), C.byref(tel)))
     del keep
     return out[:out_dim], _telemetry_moe(tel)
 

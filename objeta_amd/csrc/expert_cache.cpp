@@ -24,6 +24,7 @@
 // fused kernels wait only for its own copies, so copies overlap compute. With no
 // misses the call is one fused launch pair for all selected experts.
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <list>
 #include <map>
@@ -68,6 +69,7 @@ struct Block {
     int refs = 0;          // executor references of a call in flight
     bool in_cache = false;  // owned by a cache entry
     std::vector<hipEvent_t> fence;
+    hipEvent_t ready = nullptr;  // recorded on the copy stream after the fill; NULL once known complete
 };
 
 }  // namespace
@@ -119,6 +121,10 @@ hipEvent_t take_event(Cache* c) {
 void fence_block(Cache* c, Block* b) {
     for (hipEvent_t e : b->fence) c->event_pool.push_back(e);
     b->fence.clear();
+    if (b->ready) {  // the copy-stream fence below orders after the fill
+        c->event_pool.push_back(b->ready);
+        b->ready = nullptr;
+    }
     if (!c->ctx) return;
     auto rec = [&](hipStream_t s) {
         hipEvent_t e = take_event(c);
@@ -132,10 +138,12 @@ void fence_block(Cache* c, Block* b) {
 void destroy_block(Cache* c, Block* b) {
     if (c->ctx && b->ptr) {
         for (hipEvent_t e : b->fence) (void)hipEventSynchronize(e);
+        if (b->ready) (void)hipEventSynchronize(b->ready);
         (void)hipFree(b->ptr);
         c->device_bytes -= b->bytes;
     }
     for (hipEvent_t e : b->fence) c->event_pool.push_back(e);
+    if (b->ready) c->event_pool.push_back(b->ready);
     delete b;
 }
 
@@ -192,20 +200,53 @@ int32_t acquire_block(Cache* c, size_t bytes, hipStream_t s, Block** out) {
     return 0;
 }
 
-// Copies host bytes into a block on the copy stream, ordered after `s`.
+// Copies host bytes into a block on the copy stream, ordered after `s` (s NULL: after
+// nothing but earlier copy-stream work, for prefetches), and records the block's
+// ready event after the copy.
 int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t s) {
     if (!c->ctx || n == 0) return 0;
     if (!h_src) OBJ_FAIL(kInvalidInput, "copy tensor into the cache", "NULL host pointer");
     hipStream_t cs = c->ctx->copy_stream;
-    hipEvent_t e = take_event(c);
-    if (!e) OBJ_FAIL(kDriver, "copy tensor into the cache", "event creation failed");
-    hipError_t r = hipEventRecord(e, s);
-    if (r == hipSuccess) r = hipStreamWaitEvent(cs, e, 0);
-    c->event_pool.push_back(e);
+    hipError_t r = hipSuccess;
+    if (s) {
+        hipEvent_t e = take_event(c);
+        if (!e) OBJ_FAIL(kDriver, "copy tensor into the cache", "event creation failed");
+        r = hipEventRecord(e, s);
+        if (r == hipSuccess) r = hipStreamWaitEvent(cs, e, 0);
+        c->event_pool.push_back(e);
+    }
     if (r == hipSuccess) r = hipMemcpyAsync(b->ptr, h_src, n, hipMemcpyHostToDevice, cs);
+    if (r == hipSuccess) {
+        if (b->ready) c->event_pool.push_back(b->ready);
+        b->ready = take_event(c);
+        if (!b->ready) OBJ_FAIL(kDriver, "copy tensor into the cache", "event creation failed");
+        r = hipEventRecord(b->ready, cs);
+    }
     if (r != hipSuccess) {
         (void)hipGetLastError();
         OBJ_FAIL(kDriver, "copy tensor into the cache", hipGetErrorString(r));
+    }
+    return 0;
+}
+
+// Orders work enqueued on `s` from now on after the block's fill (a prefetch or an
+// insert made for another stream may still be copying). s NULL: waits on the host.
+int32_t wait_ready(Cache* c, Block* b, hipStream_t s) {
+    if (!b->ready) return 0;
+    hipError_t r = hipEventQuery(b->ready);
+    if (r == hipSuccess) {
+        c->event_pool.push_back(b->ready);
+        b->ready = nullptr;
+        return 0;
+    }
+    if (r != hipErrorNotReady) {
+        (void)hipGetLastError();
+        OBJ_FAIL(kDriver, "wait for a cache copy", hipGetErrorString(r));
+    }
+    OBJ_HIP(s ? hipStreamWaitEvent(s, b->ready, 0) : hipEventSynchronize(b->ready), "wait for a cache copy");
+    if (!s) {
+        c->event_pool.push_back(b->ready);
+        b->ready = nullptr;
     }
     return 0;
 }
@@ -404,6 +445,7 @@ int32_t objeta_hip_cache_get(objeta_hip_expert_cache* c, const objeta_hip_cache_
     if (!key || !hit) OBJ_FAIL(kInvalidInput, "cache get", "NULL argument");
     Block* b = lookup(c, to_key(*key));
     *hit = b ? 1 : 0;
+    if (b && c->ctx) OBJ_TRY(wait_ready(c, b, nullptr));  // a prefetch may still be copying
     if (d_ptr) *d_ptr = b ? b->ptr : nullptr;
     if (nbytes) *nbytes = b ? c->map.find(to_key(*key))->second.size : 0;
     return 0;
@@ -440,6 +482,10 @@ int32_t objeta_hip_cache_get_or_insert(objeta_hip_expert_cache* c, const objeta_
     if (!key || !d_ptr || !hit || !cached) OBJ_FAIL(kInvalidInput, "cache get_or_insert", "NULL argument");
     Block* b = lookup(c, to_key(*key));
     if (b) {
+        if (c->ctx) {
+            hipStream_t s = resolve_stream(c->ctx, stream);
+            OBJ_TRY(wait_ready(c, b, s));
+        }
         *hit = 1;
         *cached = 1;
         *d_ptr = b->ptr;
@@ -545,6 +591,68 @@ int32_t objeta_hip_cache_release_transient(objeta_hip_expert_cache* c, const voi
     Block* b = it->second;
     c->transients.erase(it);
     retire_block(c, b);
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_prefetch(objeta_hip_expert_cache* c, const objeta_hip_cache_key* keys,
+                                  const void* const* h_srcs, const uint64_t* nbytes, uint64_t n, uint64_t* issued) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "cache prefetch"));
+    if (n && (!keys || !h_srcs || !nbytes)) OBJ_FAIL(kInvalidInput, "cache prefetch", "NULL argument");
+    if (c->ctx) OBJ_HIP(hipSetDevice(c->ctx->device), "hipSetDevice");
+    uint64_t done = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const Key k = to_key(keys[i]);
+        // resident keys and tensors the capacity could never hold are left alone
+        if (c->map.count(k) || nbytes[i] > c->st.capacity_bytes) continue;
+        Block* b = nullptr;
+        OBJ_TRY(stage_tensor(c, h_srcs[i], nbytes[i], nullptr, &b));
+        if (!insert_block(c, k, b, nbytes[i])) {
+            retire_block(c, b);
+            continue;
+        }
+        ++done;
+    }
+    if (issued) *issued = done;
+    return 0;
+    OBJ_GUARD_END
+}
+
+int32_t objeta_hip_cache_preload_shared(objeta_hip_expert_cache* c, const objeta_hip_host_expert* shared,
+                                        uint64_t n_layers, uint64_t first_layer, objeta_hip_stream stream,
+                                        uint64_t* bytes, float* ms) {
+    OBJ_GUARD_BEGIN
+    OBJ_TRY(check_cache(c, "preload shared experts"));
+    if (n_layers && !shared) OBJ_FAIL(kInvalidInput, "preload shared experts", "NULL shared expert array");
+    const auto t0 = std::chrono::steady_clock::now();
+    uint64_t total = 0;
+    for (uint64_t l = 0; l < n_layers; ++l) {
+        const objeta_hip_host_expert& e = shared[l];
+        const struct {
+            const void* h;
+            uint64_t n;
+            int32_t kind;
+        } parts[6] = {{e.gate, e.gate_len, OBJETA_HIP_TENSOR_SHARED_GATE_WEIGHT},
+                      {e.gate_scale, e.gate_scale_len, OBJETA_HIP_TENSOR_SHARED_GATE_SCALE},
+                      {e.up, e.up_len, OBJETA_HIP_TENSOR_SHARED_UP_WEIGHT},
+                      {e.up_scale, e.up_scale_len, OBJETA_HIP_TENSOR_SHARED_UP_SCALE},
+                      {e.down, e.down_len, OBJETA_HIP_TENSOR_SHARED_DOWN_WEIGHT},
+                      {e.down_scale, e.down_scale_len, OBJETA_HIP_TENSOR_SHARED_DOWN_SCALE}};
+        for (const auto& p : parts) {
+            objeta_hip_cache_key key{};
+            key.layer_id = first_layer + l;
+            key.expert_id = 0;
+            key.tensor_kind = p.kind;
+            key.quant_format = OBJETA_HIP_FP4_E2M1;
+            const void* d = nullptr;
+            OBJ_TRY(objeta_hip_cache_insert_pinned(c, &key, p.h, p.n, stream, &d));
+            total += p.n;
+        }
+    }
+    if (c->ctx && n_layers) OBJ_HIP(hipStreamSynchronize(c->ctx->copy_stream), "preload shared experts");
+    if (bytes) *bytes = total;
+    if (ms) *ms = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return 0;
     OBJ_GUARD_END
 }
@@ -691,6 +799,7 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
             } else if (cache) {
                 b = lookup(cache, key);
                 hit = b != nullptr;
+                if (hit && cache->ctx) OBJ_TRY(wait_ready(cache, b, s));
             }
             Cache* home = cache && !bypass ? cache : pool;
             if (!hit) {
@@ -958,7 +1067,8 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
     objeta_hip_context* ctx, objeta_hip_stream stream, const objeta_hip_host_expert* experts, uint64_t n_experts,
     const uint64_t* sel_ids, const float* sel_weights, uint64_t n_selected, const float* x, uint64_t x_len,
     uint64_t hidden, uint64_t intermediate, uint64_t out_dim, uint64_t layer_id, objeta_hip_expert_cache* cache,
-    const objeta_hip_expert_ptrs* shared_fp8, float swiglu_limit, float* out, objeta_hip_moe_telemetry* tel) {
+    const objeta_hip_expert_ptrs* shared_fp8, int32_t shared_from_cache, float swiglu_limit, float* out,
+    objeta_hip_moe_telemetry* tel) {
     OBJ_GUARD_BEGIN
     OBJ_TRY(check_ctx(ctx, "execute_selected_moe_official_routed_fp4"));
     const char* action = "validate execute_selected_moe_official_routed_fp4_cuda input";
@@ -1010,13 +1120,42 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
     std::memcpy(h0, x, hidden * 4);
     if (k) std::memcpy(h0 + tail, sel_weights, k * 4);
     for (uint64_t j = 0; j < k; ++j) h_ids[j] = static_cast<uint32_t>(j);  // slot j reads table entry j
-    if (shared_fp8) h_tab[k] = *shared_fp8;
     OBJ_HIP(hipEventRecord(ev[X0], s), "record event");
     OBJ_HIP(hipMemcpyAsync(d_x, h0, hidden * 4, hipMemcpyHostToDevice, s), "official_h2d");
     OBJ_HIP(hipEventRecord(ev[X1], s), "record event");
 
     StagedExperts st;
     int32_t rc = stage_selected(ctx, cache, experts, sel_ids, k, OBJETA_HIP_FP4_E2M1, layer_id, false, s, h_tab, st);
+    // The shared expert: with shared_from_cache, the cache's six Shared* entries of
+    // this layer first (get in key order, stopping at the first miss, as the sketch
+    // in crates/objeta-cuda/src/moe_tmp.txt:1-35 resolves it), else the argument.
+    bool have_sh = false, sh_cached = false;
+    uint64_t sh_cached_bytes = 0;
+    if (rc == 0 && shared_from_cache && cache) {
+        const int32_t kinds[6] = {OBJETA_HIP_TENSOR_SHARED_GATE_WEIGHT, OBJETA_HIP_TENSOR_SHARED_GATE_SCALE,
+                                  OBJETA_HIP_TENSOR_SHARED_UP_WEIGHT,   OBJETA_HIP_TENSOR_SHARED_UP_SCALE,
+                                  OBJETA_HIP_TENSOR_SHARED_DOWN_WEIGHT, OBJETA_HIP_TENSOR_SHARED_DOWN_SCALE};
+        const void* p[6] = {};
+        int q = 0;
+        for (; q < 6 && rc == 0; ++q) {
+            const Key key{layer_id, 0, kinds[q], OBJETA_HIP_FP4_E2M1};
+            Block* b = lookup(cache, key);
+            if (!b) break;
+            if (cache->ctx) rc = wait_ready(cache, b, s);
+            b->refs += 1;
+            st.held.push_back({cache, b});
+            p[q] = b->ptr;
+            sh_cached_bytes += cache->map.find(key)->second.size;
+        }
+        if (rc == 0 && q == 6) {
+            h_tab[k] = {p[0], p[2], p[4], p[1], p[3], p[5]};
+            have_sh = sh_cached = true;
+        }
+    }
+    if (!have_sh && shared_fp8) {
+        h_tab[k] = *shared_fp8;
+        have_sh = true;
+    }
     if (rc) {
         (void)hipStreamSynchronize(ctx->copy_stream);
         st.release();
@@ -1032,7 +1171,7 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
             break;
         }
         const OfficialMarks marks{ev[GU1], ev[SH1], ev[AQ1], ev[DN1]};
-        if ((rc = launch_moe_official_fp4(ctx, s, d_tab, k ? k : 1, shared_fp8 ? d_tab + k : nullptr, d_ids, d_w, 1, k,
+        if ((rc = launch_moe_official_fp4(ctx, s, d_tab, k ? k : 1, have_sh ? d_tab + k : nullptr, d_ids, d_w, 1, k,
                                           d_x, d_out, hidden, intermediate, out_dim, swiglu_limit, nullptr, nullptr,
                                           &marks)))
             break;
@@ -1060,10 +1199,12 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
         uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
         const uint64_t single_expert_bytes = 2 * (gu_w + gu_s) + dn_w + dn_s;
         const uint64_t working = uniq.size() * single_expert_bytes;
-        // the reference's shared byte formula (moe.rs:1618-1624), scales counted per 128
-        const uint64_t sh_total = shared_fp8 ? 2 * (intermediate * hidden) + out_dim * intermediate +
-                                                   2 * (intermediate * hidden / 128) + out_dim * intermediate / 128
-                                             : 0;
+        // the reference's shared byte formula (moe.rs:1618-1624), scales counted per 128;
+        // a shared expert taken from the cache counts its resident bytes as reused
+        const uint64_t sh_formula = 2 * (intermediate * hidden) + out_dim * intermediate +
+                                    2 * (intermediate * hidden / 128) + out_dim * intermediate / 128;
+        const uint64_t sh_total = sh_cached ? sh_cached_bytes : (have_sh ? sh_formula : 0);
+        const uint64_t sh_loaded = sh_cached ? 0 : sh_total;
         const uint64_t loaded = st.w_loaded + st.s_loaded, reused = st.w_reused + st.s_reused;
         objeta_hip_moe_telemetry t{};
         t.selected_expert_count = k;
@@ -1085,16 +1226,17 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
         t.gate_up_qgemv_ms = elapsed(ev[X1], ev[GU1]);
         t.activation_ms = elapsed(ev[SH1], ev[AQ1]);
         t.down_qgemv_ms = elapsed(ev[AQ1], ev[DN1]);
-        t.shared_expert_ms = shared_fp8 ? elapsed(ev[GU1], ev[SH1]) + elapsed(ev[DN1], ev[D2H0]) : 0.f;
+        t.shared_expert_ms = have_sh ? elapsed(ev[GU1], ev[SH1]) + elapsed(ev[DN1], ev[D2H0]) : 0.f;
         t.total_ms = elapsed(ev[T0], ev[T1]) - elapsed(ev[D2H0], ev[T1]);
         t.bytes_per_expert = single_expert_bytes;
         t.selected_working_set_bytes = working;
         t.routed_fp4_bytes_loaded = loaded;
         t.routed_fp4_bytes_reused = reused;
-        t.shared_fp8_bytes_loaded = sh_total;
+        t.shared_fp8_bytes_loaded = sh_loaded;
+        t.shared_fp8_bytes_reused = sh_total - sh_loaded;
         t.total_logical_bytes = working + sh_total;
-        t.total_loaded_bytes = loaded + sh_total;
-        t.total_reused_bytes = reused;
+        t.total_loaded_bytes = loaded + sh_loaded;
+        t.total_reused_bytes = reused + (sh_total - sh_loaded);
         *tel = t;
     }
     return 0;

@@ -112,7 +112,7 @@ def test_library_cache_matches_model_on_random_sequences(seed):
     sizes = {k: int(rng.integers(1, cap // 2 + 50)) for k in keys}
     for step in range(400):
         op = rng.choice(["get", "insert", "get_or_insert", "pin", "insert_pinned", "touch", "evict", "clear",
-                         "reset"], p=[.25, .2, .25, .05, .02, .1, .08, .02, .03])
+                         "reset", "prefetch"], p=[.2, .2, .25, .05, .02, .1, .08, .02, .03, .05])
         k = keys[int(rng.integers(len(keys)))]
         if op == "get":
             assert (lib.get(_key(k)) is not None) == model.get(k)
@@ -142,6 +142,17 @@ def test_library_cache_matches_model_on_random_sequences(seed):
         elif op == "clear":
             lib.clear()
             model.clear()
+        elif op == "prefetch":
+            # an insert of absent keys that fit, never a get (no hit or miss counted)
+            k2 = keys[int(rng.integers(len(keys)))]
+            arrs = [np.zeros(sizes[k], np.uint8), np.zeros(sizes[k2], np.uint8)]
+            n = lib.prefetch([(_key(k), arrs[0]), (_key(k2), arrs[1])])
+            want = 0
+            for kk in dict.fromkeys([k, k2]):
+                if kk not in model.sizes and sizes[kk] <= cap:
+                    model.insert(kk, sizes[kk])
+                    want += 1
+            assert n == want
         else:
             lib.reset_counters()
             model.reset_counters()
@@ -160,3 +171,24 @@ def test_library_cache_insert_stops_when_only_pinned_remain():
     lib.insert_pinned(a, np.zeros(80, np.uint8))
     _, cached = lib.insert(b, np.zeros(50, np.uint8))
     assert cached and lib.resident_bytes == 130 and lib.eviction_count == 0
+
+
+def test_library_preload_shared_pins_six_tensors_per_layer():
+    """The shared-expert preload (deepseek_single_layer_moe.rs:1698-1730): insert_pinned of
+    the six shared tensors per layer under (layer, 0, Shared*, FP4); eviction skips them."""
+    lens = (3000, 100, 3000, 100, 2500, 80)
+    shared = [tuple(np.zeros(n, np.uint8) for n in lens) for _ in range(3)]
+    lib = ExpertCache(50_000)
+    nbytes, ms = lib.preload_shared(shared, first_layer=5)
+    assert nbytes == 3 * sum(lens) and ms >= 0
+    st = lib.stats()
+    assert st["pinned_bytes"] == st["resident_bytes"] == nbytes
+    kinds = [ExpertTensorKind.SharedGateWeight, ExpertTensorKind.SharedGateScale, ExpertTensorKind.SharedUpWeight,
+             ExpertTensorKind.SharedUpScale, ExpertTensorKind.SharedDownWeight, ExpertTensorKind.SharedDownScale]
+    assert lib.order() == [(5 + l, 0, int(k), int(QuantFormat.DeepSeekFp4E2M1)) for l in range(3) for k in kinds]
+    assert lib.evict_lru() is None
+    # a regular insert that needs room evicts around the pinned entries
+    big = ExpertCacheKey(9, 1, ExpertTensorKind.GateWeight, QuantFormat.DeepSeekFp4E2M1)
+    _, cached = lib.insert(big, np.zeros(50_000 - nbytes + 1, np.uint8))
+    assert cached and lib.stats()["pinned_bytes"] == nbytes
+    lib.close()
