@@ -503,8 +503,12 @@ def run_deepseek(env: Env, args, seed):
 # ------------------------------------------------------------- cache misses
 def run_misses(env: Env, st: QwenStack, args, xs, P, report):
     """The stack through the host-in/host-out executor with the expert cache at 25% of
-    the expert bytes and every expert in pinned host memory; routing on the device."""
-    from objeta_amd import ExpertCache, PinnedHostBuffer
+    the expert bytes and every expert in pinned host memory; routing on the device.
+    Two runs from an empty cache: the executor alone, and with a speculative
+    cross-layer prefetch (after layer l's call, layer l+1's router evaluated on layer
+    l's input predicts its experts, whose absent tensors start copying while the host
+    routes layer l+1)."""
+    from objeta_amd import ExpertCache, ExpertCacheKey, ExpertTensorKind, HostExpertSet, PinnedHostBuffer, QuantFormat
     be = env.be
     L, H, E, K, I = st.layers, st.H, st.E, st.K, st.I
     eb = st.expert_bytes
@@ -523,6 +527,8 @@ def run_misses(env: Env, st: QwenStack, args, xs, P, report):
         return (host[base + g:base + g + st.gu_bytes], host[base + u:base + u + st.gu_bytes],
                 host[base + d:base + d + st.dn_bytes])
     experts = [[tensors(l, e) for e in range(E)] for l in range(L)]
+    sets = [HostExpertSet(experts[l]) for l in range(L)]
+    kinds = (ExpertTensorKind.Gate, ExpertTensorKind.Up, ExpertTensorKind.Down)
     # PCIe probe: one 256 MiB pinned -> device copy
     probe = be.alloc(256 << 20)
     ev0, ev1 = env.event(), env.event()
@@ -534,48 +540,76 @@ def run_misses(env: Env, st: QwenStack, args, xs, P, report):
     env.drop_events([ev0, ev1])
     probe.free()
     capacity = (L * E * eb) // 4
-    cache = ExpertCache(capacity, be)
     d_h = be.alloc(4 * H)
     d_ids, d_w = be.alloc(4 * K), be.alloc(4 * K)
-    tok_us, h2d_ms, loaded, logical, tel_runs, last = [], 0.0, 0, 0, [], None
+    p_ids, p_w = be.alloc(4 * K), be.alloc(4 * K)
     n_tok = args.miss_tokens
-    for t in range(n_tok + 2):  # two warm-up tokens fill the cache
-        h = xs.download(np.float32, H, offset=4 * (t % P) * H)
-        c0 = time.perf_counter()
-        for l in range(L):
-            d_h.upload(h)
-            env.check(env.lib.objeta_hip_router_topk_device(env.ctx, None, st.router_w[l].addr(),
-                                                            st.router_b[l].addr(), d_h.addr(), 1, E, H, K, 1,
-                                                            d_ids.addr(), d_w.addr()))
-            ids = d_ids.download(np.uint32, K)
-            ws = d_w.download(np.float32, K)
-            sel = [(int(i), float(w)) for i, w in zip(ids, ws)]
-            out, tel = env.moe.execute_selected_moe_cuda(None, None, experts[l], sel, h, H, I, H, l, cache)
-            last = (l, sel, h.copy(), out.copy())
-            h = (h + out).astype(np.float32)
+
+    def route(l, ids, ws):
+        env.check(env.lib.objeta_hip_router_topk_device(env.ctx, None, st.router_w[l].addr(), st.router_b[l].addr(),
+                                                        d_h.addr(), 1, E, H, K, 1, ids.addr(), ws.addr()))
+
+    def run(prefetch: bool):
+        cache = ExpertCache(capacity, be)
+        tok_us, h2d_ms, loaded, logical, tel_runs, last = [], 0.0, 0, 0, [], None
+        predicted, correct, issued = 0, 0, 0
+        pred_next = None
+        for t in range(n_tok + 2):  # two warm-up tokens fill the cache
+            h = xs.download(np.float32, H, offset=4 * (t % P) * H)
+            c0 = time.perf_counter()
+            for l in range(L):
+                d_h.upload(h)
+                route(l, d_ids, d_w)
+                if prefetch and l + 1 < L:
+                    route(l + 1, p_ids, p_w)  # layer l+1's router on layer l's input
+                ids = d_ids.download(np.uint32, K)
+                ws = d_w.download(np.float32, K)
+                if pred_next is not None and t >= 2:
+                    predicted += K
+                    correct += len(set(int(i) for i in ids) & pred_next)
+                sel = [(int(i), float(w)) for i, w in zip(ids, ws)]
+                out, tel = env.moe.execute_selected_moe_cuda(None, None, sets[l], sel, h, H, I, H, l, cache)
+                pred_next = None
+                if prefetch and l + 1 < L:
+                    pred = [int(i) for i in p_ids.download(np.uint32, K)]
+                    pred_next = set(pred)
+                    issued += cache.prefetch([(ExpertCacheKey(l + 1, e, kd, QuantFormat.Q4_0), a)
+                                              for e in pred for kd, a in zip(kinds, experts[l + 1][e])])
+                last = (l, sel, h.copy(), out.copy())
+                h = (h + out).astype(np.float32)
+                if t >= 2:
+                    h2d_ms += tel["h2d_ms"]
+                    loaded += tel["actual_expert_bytes_loaded"]
+                    logical += tel["logical_expert_bytes_requested"]
+                    tel_runs.append(tel)
             if t >= 2:
-                h2d_ms += tel["h2d_ms"]
-                loaded += tel["actual_expert_bytes_loaded"]
-                logical += tel["logical_expert_bytes_requested"]
-                tel_runs.append(tel)
-        if t >= 2:
-            tok_us.append((time.perf_counter() - c0) * 1e6)
-    cst = cache.stats()
-    cache.close()
-    s = stats(tok_us)
+                tok_us.append((time.perf_counter() - c0) * 1e6)
+        cst = cache.stats()
+        cache.close()
+        s = stats(tok_us)
+        res = {"us_per_token_end_to_end": rnd(s, 1), "us_per_token_layer": round(s["avg"] / L, 2),
+               "hit_rate_bytes": round(1.0 - loaded / logical, 4) if logical else None,
+               "expert_bytes_loaded_per_token": loaded // max(1, n_tok),
+               "pcie_gbps_on_misses": round(loaded / (h2d_ms * 1e-3) / 1e9, 1) if h2d_ms > 0 else None,
+               "cache": {k: cst[k] for k in ("hit_count", "miss_count", "eviction_count", "resident_bytes",
+                                              "cache_insert_accept_count")}}
+        if prefetch:
+            res["prediction_accuracy"] = round(correct / predicted, 4) if predicted else None
+            res["prefetch_tensors_issued_per_token"] = round(issued / (n_tok + 2), 1)
+        return res, tel_runs, last
+
+    base, tel_runs, last = run(False)
+    pre, _, _ = run(True)
     res = {"tokens": n_tok, "layers": L, "cache_capacity_bytes": capacity, "expert_bytes_total": L * E * eb,
-           "us_per_token_end_to_end": rnd(s, 1), "us_per_token_layer": round(s["avg"] / L, 2),
-           "hit_rate_bytes": round(1.0 - loaded / logical, 4) if logical else None,
-           "expert_bytes_loaded_per_token": loaded // max(1, n_tok),
-           "pcie_gbps_on_misses": round(loaded / (h2d_ms * 1e-3) / 1e9, 1) if h2d_ms > 0 else None,
-           "pcie_probe_gbps": round(probe_gbps, 1), "host_staging_s": round(stage_s, 1),
-           "cache": {k: cst[k] for k in ("hit_count", "miss_count", "eviction_count", "resident_bytes")},
-           "path": "router on the device, ids to the host, execute_selected (host x in, host out), one call per layer"}
+           **base, "pcie_probe_gbps": round(probe_gbps, 1), "host_staging_s": round(stage_s, 1),
+           "path": "router on the device, ids to the host, execute_selected (host x in, host out), one call per "
+                   "layer; host experts marshalled once per layer (HostExpertSet)",
+           "with_prefetch": pre}
     if report is not None:
         report["moe_tel"] = tel_runs
         report["moe_shape"] = (H, I, H, K)
         report["moe_last"] = last
-    del experts, host
+    del experts, host, sets
     pin.free()
     return res
 
