@@ -649,6 +649,80 @@ int32_t objeta_hip_moe_execute_official_fp4(objeta_hip_context* ctx, objeta_hip_
                                             const objeta_hip_expert_ptrs* shared_fp8, int32_t shared_from_cache,
                                             float swiglu_limit, float* out, objeta_hip_moe_telemetry* tel);
 
+/* ------------------------------------------------------ checkpoint ingest */
+/* Memory-mapped safetensors files: ModelWeights (crates/objeta-parser/src/lib.rs:
+ * 88-293). A path names one file or a directory whose *.safetensors shards are
+ * read in file-name order (a later shard's tensor replaces an earlier one of the
+ * same name). Tensor data stays in the mapping until objeta_hip_st_close; raw
+ * pointers are zero-copy views of it. Errors of files and headers are
+ * OBJETA_HIP_ERR_IO, as the reference's driver wraps ModelWeights errors. */
+typedef struct objeta_hip_st_model objeta_hip_st_model;
+
+/* Dtype (lib.rs:30-41). */
+enum {
+    OBJETA_HIP_DT_F32 = 0,
+    OBJETA_HIP_DT_F16 = 1,
+    OBJETA_HIP_DT_BF16 = 2,
+    OBJETA_HIP_DT_I64 = 3,
+    OBJETA_HIP_DT_I32 = 4,
+    OBJETA_HIP_DT_I8 = 5,
+    OBJETA_HIP_DT_U8 = 6,
+    OBJETA_HIP_DT_F8_E8M0 = 7,
+    OBJETA_HIP_DT_F8_E4M3 = 8,
+    OBJETA_HIP_DT_BOOL = 9
+};
+
+/* TensorInfo (lib.rs:20-28); shape holds the first 8 dimensions, file the index of
+ * the shard the tensor came from. */
+typedef struct {
+    int32_t dtype;
+    uint32_t ndim;
+    uint64_t shape[8];
+    uint64_t nbytes;
+    uint64_t nelem;
+    uint32_t file;
+    uint32_t reserved;
+} objeta_hip_st_info;
+
+/* ModelWeights::open (lib.rs:104-178) with parse_header (lib.rs:180-213). */
+int32_t objeta_hip_st_open(const char* path, objeta_hip_st_model** out);
+int32_t objeta_hip_st_close(objeta_hip_st_model* model);
+/* len (lib.rs:279-281); keys (lib.rs:221-224) by index, in sorted name order:
+ * *len = the name's length, buf (nullable) receives it NUL-terminated. */
+int32_t objeta_hip_st_len(const objeta_hip_st_model* model, uint64_t* n);
+int32_t objeta_hip_st_key(const objeta_hip_st_model* model, uint64_t i, char* buf, uint64_t cap, uint64_t* len);
+/* info / contains (lib.rs:216-230): *found = 0 when the name is absent. */
+int32_t objeta_hip_st_info_get(const objeta_hip_st_model* model, const char* name, int32_t* found,
+                               objeta_hip_st_info* out);
+/* get_raw (lib.rs:232-241): the tensor's bytes in the mapping. */
+int32_t objeta_hip_st_get_raw(const objeta_hip_st_model* model, const char* name, const void** ptr,
+                              uint64_t* nbytes);
+/* get_f32 (lib.rs:243-276): F32 copied, F16 and BF16 converted (half_to_f32 and
+ * bf16_to_f32, lib.rs:297-330); other dtypes fail. out NULL: only *nelem. */
+int32_t objeta_hip_st_get_f32(const objeta_hip_st_model* model, const char* name, float* out, uint64_t cap,
+                              uint64_t* nelem);
+/* A routed DeepSeek expert of layer `layer` (mtp != 0: the "mtp.<layer>" block
+ * family) found by classify_tensor's rules (crates/objeta-parser/src/deepseek.rs:
+ * 178-262; w1 = gate, w3 = up, w2 = down, ".scale" = E8M0 scales), as
+ * find_fp4_expert_tensors does (deepseek_single_layer_moe.rs:410-520): the split
+ * FP4 tensors (I8/U8 [rows][cols/2] + F8_E8M0 [rows][cols/32]) as zero-copy host
+ * tensors for the executors, with the expert's dimensions. */
+int32_t objeta_hip_st_deepseek_expert(const objeta_hip_st_model* model, uint64_t layer, uint64_t expert,
+                                      int32_t mtp, objeta_hip_host_expert* out, uint64_t* hidden,
+                                      uint64_t* intermediate, uint64_t* out_dim);
+/* load_shared_expert_fp8 (deepseek_single_layer_moe.rs:1034-1080): the FP8 shared
+ * expert "<prefix>.ffn.shared_experts.w{1,3,2}.{weight,scale}" (F8_E4M3 [rows][cols]
+ * with E8M0 scales on the 128 x 128 tile grid). */
+int32_t objeta_hip_st_deepseek_shared_expert(const objeta_hip_st_model* model, uint64_t layer, int32_t mtp,
+                                             objeta_hip_host_expert* out, uint64_t* hidden,
+                                             uint64_t* intermediate, uint64_t* out_dim);
+/* find_router_tensor (deepseek_single_layer_moe.rs:226-330): the single router
+ * "...gate.weight" tensor [num_experts][hidden] of the layer and block family
+ * (Hyper-Connection hc_ffn_* tensors excluded). name_buf (nullable) receives its
+ * name; read it with objeta_hip_st_get_f32. */
+int32_t objeta_hip_st_deepseek_router(const objeta_hip_st_model* model, uint64_t layer, int32_t mtp,
+                                      char* name_buf, uint64_t cap, objeta_hip_st_info* info);
+
 #ifdef __cplusplus
 }
 #endif

@@ -173,6 +173,16 @@ SIGNATURES = {
                                                   I32, F32, P, P]),
     "objeta_hip_cache_prefetch": (I32, [P, P, P, P, U64, P]),
     "objeta_hip_cache_preload_shared": (I32, [P, P, U64, U64, P, P, P]),
+    "objeta_hip_st_open": (I32, [C.c_char_p, P]),
+    "objeta_hip_st_close": (I32, [P]),
+    "objeta_hip_st_len": (I32, [P, P]),
+    "objeta_hip_st_key": (I32, [P, U64, P, U64, P]),
+    "objeta_hip_st_info_get": (I32, [P, C.c_char_p, P, P]),
+    "objeta_hip_st_get_raw": (I32, [P, C.c_char_p, P, P]),
+    "objeta_hip_st_get_f32": (I32, [P, C.c_char_p, P, U64, P]),
+    "objeta_hip_st_deepseek_expert": (I32, [P, U64, U64, I32, P, P, P, P]),
+    "objeta_hip_st_deepseek_shared_expert": (I32, [P, U64, I32, P, P, P, P]),
+    "objeta_hip_st_deepseek_router": (I32, [P, U64, I32, P, U64, P]),
 }
 
 

@@ -195,8 +195,12 @@ __device__ __forceinline__ int reg_value(const uint32_t (&n)[4], uint32_t m, int
     }
 }
 
+// Inlined, with a rolled loop: an out-of-line call (arrays passed by reference, a
+// call frame) gave every kernel using it a private stack although this path runs
+// only for non-finite block scales; the small arrays indexed in the loop stay in
+// registers.
 template <int F, int NT>
-__device__ __noinline__ void block_dot_reference_form(const uint32_t (&n)[4], uint32_t m, float scale,
+__device__ __forceinline__ void block_dot_reference_form(const uint32_t (&n)[4], uint32_t m, float scale,
                                                          const float* const (&xs)[NT], int xoff,
                                                          float (&acc)[NT]) {
 #pragma unroll 1
@@ -234,16 +238,8 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw],
                 n1[0] = d[4]; n1[1] = d[5]; n1[2] = d[6];
                 n0[3] = n1[3] = 0;
             }
-            // the out-of-line call gets a copy: were acc itself passed by reference,
-            // its address would escape and it would live in scratch memory on the
-            // fast path too (a memory round trip per pair)
-            float acc_slow[NT];
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc_slow[t] = acc[t];
-            block_dot_reference_form<F, NT>(n0, m0, s0, xs_slow, 0, acc_slow);
-            block_dot_reference_form<F, NT>(n1, m1, s1, xs_slow, 32, acc_slow);
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] = acc_slow[t];
+            block_dot_reference_form<F, NT>(n0, m0, s0, xs_slow, 0, acc);
+            block_dot_reference_form<F, NT>(n1, m1, s1, xs_slow, 32, acc);
             return;
         }
     }

@@ -42,11 +42,15 @@ __device__ __forceinline__ float silu_mul(float g, float u, float limit) {
 
 // The SwiGLU of the official compositions (crates/objeta-parser/src/deepseek.rs:
 // 1680-1686, 1708-1713): only the up projection is clamped, exp is glibc's expf
-// (Rust's f32::exp) and the division is IEEE.
+// (Rust's f32::exp) and the division is the IEEE float quotient, here the double
+// quotient rounded once to float (exact: a double carries more than 2 * 24 + 2
+// bits, so the double rounding of a float division is innocuous). __fdiv_rn in this
+// spot gave every kernel of the file a private stack.
 __device__ __forceinline__ float swiglu_official(float g, float u, float limit) {
     if (u < -limit) u = -limit;
     else if (u > limit) u = limit;
-    return rules::div_rn(g, 1.0f + rmath::expf_glibc(-g)) * u;
+    const float d = 1.0f + rmath::expf_glibc(-g);
+    return static_cast<float>(static_cast<double>(g) / static_cast<double>(d)) * u;
 }
 
 __device__ __forceinline__ float swiglu(float g, float u, float limit, uint32_t official) {
@@ -486,15 +490,21 @@ hipError_t launch_gate_up_rows(hipStream_t s, const objeta_hip_expert_ptrs* tabl
     // two rows per slot when that still leaves a few workgroups per CU
     const uint32_t gs = 64 / lpr;
     const uint64_t blocks_u2 = static_cast<uint64_t>(sh.n_tokens) * sh.kk() * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2));
-    // (FP8 rows carry 17 dwords each: two row slots of them would spill)
-    const bool u2 = blocks_u2 >= 2ull * cus && ch <= 2 && R::kDw <= 9;
-    switch (ch) {
-        case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel)
-                          : gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel);
-        case 2: return u2 ? gate_up_fast<R, 2, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel)
-                          : gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel);
-        case 3: return gate_up_fast<R, 1, 3>(s, table, ids, x, act, sh, lpr, limit, err, sel);
-        default: return gate_up_fast<R, 1, 4>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+    // FP8 rows carry 17 dwords each: two row slots, or more than two chunks per
+    // lane, would spill (the official layer rejects shapes with more)
+    if constexpr (R::kDw > 9) {
+        if (ch == 1) return gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+        return gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+    } else {
+        const bool u2 = blocks_u2 >= 2ull * cus && ch <= 2;
+        switch (ch) {
+            case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel)
+                              : gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+            case 2: return u2 ? gate_up_fast<R, 2, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel)
+                              : gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+            case 3: return gate_up_fast<R, 1, 3>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+            default: return gate_up_fast<R, 1, 4>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+        }
     }
 }
 
@@ -505,19 +515,26 @@ hipError_t launch_down_rows(hipStream_t s, const objeta_hip_expert_ptrs* table, 
     const uint32_t pairs = sh.inter >> 6;
     const uint32_t lpr = pick_lpr(pairs);
     const uint32_t ch = pairs / lpr;
-    if (jw == 2) {
-        switch (ch) {
-            case 1: return down_fast<R, 1, 1, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
-            case 2: return down_fast<R, 1, 2, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
-            case 3: return down_fast<R, 1, 3, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
-            default: return down_fast<R, 1, 4, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+    if constexpr (R::kDw > 9) {  // FP8 rows: one or two chunks per lane (see launch_gate_up_rows)
+        if (jw == 2) return ch == 1 ? down_fast<R, 1, 1, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel)
+                                    : down_fast<R, 1, 2, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+        return ch == 1 ? down_fast<R, 1, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel)
+                       : down_fast<R, 1, 2, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+    } else {
+        if (jw == 2) {
+            switch (ch) {
+                case 1: return down_fast<R, 1, 1, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+                case 2: return down_fast<R, 1, 2, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+                case 3: return down_fast<R, 1, 3, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+                default: return down_fast<R, 1, 4, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+            }
         }
-    }
-    switch (ch) {
-        case 1: return down_fast<R, 1, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
-        case 2: return down_fast<R, 1, 2, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
-        case 3: return down_fast<R, 1, 3, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
-        default: return down_fast<R, 1, 4, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+        switch (ch) {
+            case 1: return down_fast<R, 1, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+            case 2: return down_fast<R, 1, 2, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+            case 3: return down_fast<R, 1, 3, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+            default: return down_fast<R, 1, 4, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
+        }
     }
 }
 
@@ -696,7 +713,9 @@ int32_t launch_moe_official_fp4(objeta_hip_context* ctx, hipStream_t s, const ob
     ssh.shared = shared;
     ssh.official = true;
     if (shared) {
-        const bool fits = fast_shape(ssh.hidden) && fast_shape(ssh.inter) &&
+        auto chunks = [](uint32_t cols) { return (cols >> 6) / pick_lpr(cols >> 6); };
+        const bool fits = fast_shape(ssh.hidden) && fast_shape(ssh.inter) && chunks(ssh.hidden) <= 2 &&
+                          chunks(ssh.inter) <= 2 &&
                           static_cast<size_t>(ssh.hidden >> 6) * kPad * sizeof(float) + 16 <= max_lds(ctx) &&
                           down_lds_bytes(ssh, 1, 1) <= max_lds(ctx);
         if (!fits)

@@ -36,16 +36,19 @@ constexpr int kChunkBatch = 8;  // 256-element chunks loaded per batch (8 float4
 // restatement in the oracle agrees with glibc on all of [-110, 0] (exhaustively)
 // and double exp rounded once to float differs from it on 97,052 of those
 // arguments. Table entry i: the correctly rounded double 2^(i/32) minus i << 47.
+// (a file-scope table: a function-local one indexed per lane is placed in private
+// scratch memory in some kernels)
+static __device__ const uint64_t kExpTab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
 __device__ __forceinline__ float expf_glibc(float x) {
-    constexpr uint64_t kTab[32] = {
-        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {  // |x| >= 88, inf or nan
@@ -62,7 +65,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd = __dsub_rn(kd, kShift);
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    const double sc = __builtin_bit_cast(double, kTab[ki % 32] + (ki << 47));
+    const double sc = __builtin_bit_cast(double, kExpTab[ki % 32] + (ki << 47));
     const double z = __builtin_fma(kC0, r, kC1);
     const double r2 = __dmul_rn(r, r);
     double y = __builtin_fma(kC2, r, 1.0);
