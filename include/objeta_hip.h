@@ -339,12 +339,15 @@ int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, obje
 
 /* One MoE layer on the device: the router of objeta_hip_router_topk_device over
  * d_router_w [n_experts][hidden] (+ d_router_bias) writes d_ids_out/d_weights_out
- * [n_tokens][k], then objeta_hip_moe_selected_device runs the selected experts of
- * d_table (n_experts entries), for any number of tokens (the per-assignment
- * kernels measure faster than objeta_hip_moe_grouped_device at 16, 32 and 64
- * tokens on MI355X). No host synchronisation; graph-capturable. No
- * reference counterpart as one call: the reference routes on the host
- * (deepseek_single_layer_moe.rs:687-743) and then calls execute_selected_moe_cuda. */
+ * [n_tokens][k], then the selected experts of d_table (n_experts entries) run:
+ * below 12 tokens on the per-assignment kernels of objeta_hip_moe_selected_device,
+ * from 12 tokens on the grouped-token products of objeta_hip_moe_grouped_device
+ * whenever that path takes the shape (on MI355X at hidden 2048, 128 experts,
+ * top-8 the per-assignment kernels are faster at 8 tokens, the grouped ones at 16
+ * and beyond). The two agree within the fp32 tolerance, not bit for bit. No host
+ * synchronisation; graph-capturable. No reference counterpart as one call: the
+ * reference routes on the host (deepseek_single_layer_moe.rs:687-743) and then
+ * calls execute_selected_moe_cuda. */
 int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
                                     const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
                                     const float* d_router_w, const float* d_router_bias, uint64_t k,
@@ -354,7 +357,8 @@ int32_t objeta_hip_moe_layer_device(objeta_hip_context* ctx, int32_t format, obj
                                     uint64_t out_dim, float swiglu_limit);
 
 /* objeta_hip_moe_layer_device with the shared expert of
- * objeta_hip_moe_selected_shared_device (d_shared NULL: none). */
+ * objeta_hip_moe_selected_shared_device (d_shared NULL: none); on the grouped
+ * path the shared expert is one more group holding every token. */
 int32_t objeta_hip_moe_layer_shared_device(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
                                            const objeta_hip_expert_ptrs* d_table, uint64_t n_experts,
                                            const objeta_hip_expert_ptrs* d_shared, const float* d_router_w,

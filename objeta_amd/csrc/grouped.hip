@@ -6,12 +6,12 @@
 // down matrices are read once for all of its tokens, the products running on
 // MFMA (v_mfma_f32_16x16x32_f16). Per layer:
 //
-//   moe_group_kernel     assignments (token, slot) sorted by expert, stable; one
-//                        group per distinct selected expert
-//   moe_split_kernel     activation rows -> two fp16 parts (see below), per token
-//   moe_grouped_kernel   per (group, 16 rows): silu(gate x) * (up x) for the group
+//   moe_prepare_kernel   assignments (token, slot) sorted by expert, stable, cut
+//                        into sets of up to 8 per expert; and each token's
+//                        activation row -> two fp16 parts (see below)
+//   moe_grouped_kernel   per (set, 16 rows): silu(gate x) * (up x) for the set
 //   moe_split_kernel     the activations of every assignment
-//   moe_grouped_kernel   per (group, 16 rows): down act for every assignment
+//   moe_grouped_kernel   per (set, 16 rows): down act for every assignment
 //   moe_combine_kernel   out = residual + sum_j w_j down_j in slot order
 //
 // Exactness. Weights enter the MFMA as fp16 values that are exact for every
@@ -54,20 +54,48 @@ constexpr uint32_t kGMaxTable = 1024;   // experts per table
 constexpr uint32_t kGMaxAssign = 1024;  // tokens * k per call
 constexpr uint32_t kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 
+// One work item of the grouped products: up to 8 assignments (token, slot) that
+// selected the same expert, with that expert's table entry copied in, so a
+// workgroup reaches its weights and activations through one load.
+struct SetRec {
+    objeta_hip_expert_ptrs p;
+    uint16_t mem[8];  // act rows: assignments t*k + j (in order), or n_assign + t for the
+                      // shared expert; unused slots repeat the last; mem[0] bits
+                      // 12..15 hold the member count - 1
+};
+static_assert(sizeof(SetRec) == 64, "one 64-byte record per set");
+
 struct GroupWs {
-    uint32_t* hdr;         // [0] number of groups
-    uint32_t* grp_expert;  // [A]
-    uint32_t* grp_start;   // [A + 1]
-    uint32_t* alist;       // [A] assignment t*k + j, grouped by expert
+    uint32_t* hdr;  // [0] number of groups, [1] number of member sets
+    SetRec* sets;   // [A] (a set holds at least one assignment)
 };
 
+// The power of two 2^s that brings a row of maximum magnitude m below 2^14 (s = 0
+// for a zero or non-finite row).
+__device__ __forceinline__ int split_shift(float m) {
+    int s = 0;
+    if (m > 0.0f && __builtin_isfinite(m)) {
+        int ex;
+        (void)frexpf(m, &ex);  // m < 2^ex
+        s = 14 - ex;
+        s = s > 100 ? 100 : (s < -100 ? -100 : s);
+    }
+    return s;
+}
+
 // ------------------------------------------------------------------ grouping
-__global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restrict__ ids, uint32_t n_assign,
-                                                        uint32_t n_table, GroupWs w, uint32_t* __restrict__ err) {
+// The shared expert (when given) follows as one more group: member t is token t,
+// its act row n_assign + t.
+__device__ void group_assignments(const uint32_t* __restrict__ ids, uint32_t n_assign, uint32_t n_table,
+                                  const objeta_hip_expert_ptrs* __restrict__ table,
+                                  const objeta_hip_expert_ptrs* __restrict__ shared, uint32_t n_tokens, GroupWs w,
+                                  uint32_t* __restrict__ err) {
     __shared__ uint32_t cnt[kGMaxTable];
     __shared__ uint32_t pos[kGMaxTable];
     __shared__ uint32_t sid[kGMaxAssign];
-    __shared__ uint32_t wtot[2][4];
+    __shared__ uint32_t sal[kGMaxAssign];   // assignments grouped by expert
+    __shared__ uint32_t sinfo[kGMaxAssign];  // set: expert | first member << 11 | (count - 1) << 22
+    __shared__ uint32_t wtot[3][4];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (uint32_t e = tid; e < n_table; e += 256) cnt[e] = 0;
     for (uint32_t a = tid; a < n_assign; a += 256) sid[a] = ids[a];
@@ -79,52 +107,58 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
     }
     if (bad) atomicOr(err, 1u);
     __syncthreads();
-    // exclusive prefix over experts of the counts (positions) and of the non-empty
-    // flags (group numbers); thread t owns experts [t*per, (t+1)*per)
+    // exclusive prefix over experts of the counts (positions), of the non-empty
+    // flags (group numbers) and of the member sets; thread t owns experts
+    // [t*per, (t+1)*per)
     const uint32_t per = (n_table + 255) / 256;
     const uint32_t e0 = tid * per < n_table ? tid * per : n_table;
     const uint32_t e1 = e0 + per < n_table ? e0 + per : n_table;
-    uint32_t sc = 0, sg = 0;
+    uint32_t sc = 0, sg = 0, ss = 0;
     for (uint32_t e = e0; e < e1; ++e) {
         sc += cnt[e];
         sg += cnt[e] ? 1u : 0u;
+        ss += (cnt[e] + 7) / 8;
     }
-    uint32_t ic = sc, ig = sg;
+    uint32_t ic = sc, ig = sg, is = ss;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t oc = __shfl_up(ic, off, 64), og = __shfl_up(ig, off, 64);
+        const uint32_t oc = __shfl_up(ic, off, 64), og = __shfl_up(ig, off, 64), os = __shfl_up(is, off, 64);
         if (static_cast<int>(lane) >= off) {
             ic += oc;
             ig += og;
+            is += os;
         }
     }
     if (lane == 63) {
         wtot[0][wave] = ic;
         wtot[1][wave] = ig;
+        wtot[2][wave] = is;
     }
     __syncthreads();
-    uint32_t bc = 0, bg = 0, tc = 0, tg = 0;
+    uint32_t bc = 0, bs = 0, tg = 0, ts = 0;
     for (uint32_t v = 0; v < 4; ++v) {
         if (v < wave) {
             bc += wtot[0][v];
-            bg += wtot[1][v];
+            bs += wtot[2][v];
         }
-        tc += wtot[0][v];
         tg += wtot[1][v];
+        ts += wtot[2][v];
     }
-    uint32_t pc = bc + ic - sc, pg = bg + ig - sg;
+    uint32_t pc = bc + ic - sc, ps = bs + is - ss;
     for (uint32_t e = e0; e < e1; ++e) {
         if (cnt[e]) {
-            w.grp_expert[pg] = e;
-            w.grp_start[pg] = pc;
             pos[e] = pc;
+            for (uint32_t j = 0; j < cnt[e]; j += 8) {
+                const uint32_t m = cnt[e] - j < 8 ? cnt[e] - j : 8;
+                sinfo[ps++] = e | ((pc + j) << 11) | ((m - 1) << 22);
+            }
             pc += cnt[e];
-            ++pg;
         }
     }
+    const uint32_t n_sh = shared ? (n_tokens + 7) / 8 : 0;
     if (tid == 0) {
-        w.hdr[0] = tg;
-        w.grp_start[tg] = tc;
+        w.hdr[0] = tg + (shared ? 1 : 0);
+        w.hdr[1] = ts + n_sh;
     }
     __syncthreads();
     // stable order inside a group: rank among the earlier assignments of the expert
@@ -133,7 +167,26 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
         if (e >= n_table) continue;
         uint32_t r = 0;
         for (uint32_t b = 0; b < a; ++b) r += sid[b] == e ? 1u : 0u;
-        w.alist[pos[e] + r] = a;
+        sal[pos[e] + r] = a;
+    }
+    __syncthreads();
+    for (uint32_t si = tid; si < ts + n_sh; si += 256) {
+        SetRec r;
+        uint32_t m1;
+        if (si < ts) {
+            const uint32_t info = sinfo[si];
+            const uint32_t e = info & 0x7FFu, st = (info >> 11) & 0x7FFu;
+            m1 = info >> 22;
+            r.p = table[e];
+            for (uint32_t j = 0; j < 8; ++j) r.mem[j] = static_cast<uint16_t>(sal[st + (j < m1 ? j : m1)]);
+        } else {
+            const uint32_t t0 = 8 * (si - ts);
+            m1 = (n_tokens - t0 < 8 ? n_tokens - t0 : 8) - 1;
+            r.p = *shared;
+            for (uint32_t j = 0; j < 8; ++j) r.mem[j] = static_cast<uint16_t>(n_assign + t0 + (j < m1 ? j : m1));
+        }
+        r.mem[0] = static_cast<uint16_t>(r.mem[0] | (m1 << 12));
+        w.sets[si] = r;
     }
 }
 
@@ -142,11 +195,9 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
 // lo = fp16(x 2^s - hi), stored in the (w0,w4),(w1,w5),.. order of each group of
 // 8; mult[row] = 2^-s restores the products. A non-finite row keeps s = 0 (its
 // infinities and NaNs propagate).
-__global__ __launch_bounds__(256) void moe_split_kernel(const float* __restrict__ src, uint32_t cols,
-                                                        _Float16* __restrict__ hi, _Float16* __restrict__ lo,
-                                                        float* __restrict__ mult) {
+__device__ void split_row(const float* __restrict__ src, uint32_t cols, _Float16* __restrict__ hi,
+                          _Float16* __restrict__ lo, float* __restrict__ mult, uint32_t row) {
     __shared__ float red[4];
-    const uint32_t row = blockIdx.x;
     const float* x = src + static_cast<size_t>(row) * cols;
     float m = 0.0f;
     bool finite = true;
@@ -160,13 +211,7 @@ __global__ __launch_bounds__(256) void moe_split_kernel(const float* __restrict_
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int s = 0;
-    if (m > 0.0f && __builtin_isfinite(m)) {
-        int ex;
-        (void)frexpf(m, &ex);  // m < 2^ex
-        s = 14 - ex;
-        s = s > 100 ? 100 : (s < -100 ? -100 : s);
-    }
+    const int s = split_shift(m);
     if (threadIdx.x == 0) mult[row] = ldexpf(1.0f, -s);
     _Float16* h = hi + static_cast<size_t>(row) * cols;
     _Float16* l = lo + static_cast<size_t>(row) * cols;
@@ -187,16 +232,30 @@ __global__ __launch_bounds__(256) void moe_split_kernel(const float* __restrict_
     }
 }
 
-// ------------------------------------------------------ weights -> B operand
-// The lane's 8 weights (k group kg of block blk of its pair d) as fp16 exact
-// values in the (w0,w4),(w1,w5),(w2,w6),(w3,w7) order, and the block's scale
-// (times the format's constant). kg is lane-dependent: registers are picked with
-// selects, never indexed.
-__device__ __forceinline__ uint32_t pick4(uint32_t kg, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    const uint32_t lo = (kg & 1) ? b : a, hi = (kg & 1) ? d : c;
-    return (kg & 2) ? hi : lo;
+// Block 0 groups the assignments; block 1 + t splits row t of x.
+__global__ __launch_bounds__(256) void moe_prepare_kernel(const uint32_t* __restrict__ ids, uint32_t n_assign,
+                                                          uint32_t n_table,
+                                                          const objeta_hip_expert_ptrs* __restrict__ table,
+                                                          const objeta_hip_expert_ptrs* __restrict__ shared,
+                                                          uint32_t n_tokens, GroupWs w,
+                                                          uint32_t* __restrict__ err, const float* __restrict__ x,
+                                                          uint32_t cols, _Float16* __restrict__ xh,
+                                                          _Float16* __restrict__ xl, float* __restrict__ xmult) {
+    if (blockIdx.x == 0) group_assignments(ids, n_assign, n_table, table, shared, n_tokens, w, err);
+    else split_row(x, cols, xh, xl, xmult, blockIdx.x - 1);
 }
 
+// One workgroup per row.
+__global__ __launch_bounds__(256) void moe_split_kernel(const float* __restrict__ src, uint32_t cols,
+                                                        _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                        float* __restrict__ mult) {
+    split_row(src, cols, hi, lo, mult, blockIdx.x);
+}
+
+
+// ------------------------------------------------------ weights -> B operand
+// A lane's 8 weights of one block as exact fp16 values in the (w0,w4),(w1,w5),
+// (w2,w6),(w3,w7) order of the split activations.
 __device__ __forceinline__ half8 pack8(h2 a, h2 b, h2 c, h2 d) {
     half8 r;
     r[0] = a.x; r[1] = a.y; r[2] = b.x; r[3] = b.y;
@@ -226,73 +285,91 @@ __device__ __forceinline__ half8 nibbles_to_b(uint32_t n, uint32_t m8) {
     return pack8(a, b, c, d);
 }
 
+// IQ3_0: 2-bit lows lo16 (weights 8kg .. 8kg+7) and 1-bit highs h8 -> the 8 weights
+// q - 4 as exact fp16 in the (w0,w4),(w1,w5),.. order.
+__device__ __forceinline__ half8 iq3_to_b(uint32_t lo16, uint32_t h8) {
+    const h2 k4 = {(_Float16)1028.0f, (_Float16)1028.0f};
+    h2 p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // weights i and i + 4
+        const uint32_t t = (lo16 >> (2 * i)) & 0x303u;
+        const uint32_t hh = (h8 >> i) & 0x11u;
+        const uint32_t v = (t & 3u) | ((t & 0x300u) << 8) | ((hh & 1u) << 2) | ((hh & 0x10u) << 14);
+        p[i] = as_h2(v | 0x64006400u) - k4;
+    }
+    return pack8(p[0], p[1], p[2], p[3]);
+}
+
+// ----------------------------------------------------------- grouped GEMMs
+// A workgroup streams a 16-row slab of one group's expert (gate and up together,
+// or down) through LDS in chunks of kChunkOf columns, double-buffered: while its
+// four waves multiply chunk c (wave w: the w-th quarter of the chunk's blocks), the
+// loads of chunk c+1 (every thread's share, 64-byte runs within rows) and the next
+// activation operands are already in flight. Each lane takes its MFMA operand (8
+// weights of one output row) and the block scale from LDS; the four waves' partial
+// sums meet in LDS at the end. 8 group members per MFMA column set; the member
+// sets of all groups are separate work items (a larger group's sets stream the slab
+// in parallel workgroups).
+// columns per staged chunk: 16 blocks for gate and up together, 8 for down (the
+// widths that measured fastest; narrower chunks keep more workgroups resident)
+template <bool GATEUP>
+constexpr uint32_t kChunkOf = GATEUP ? 512 : 256;
+constexpr uint32_t kSlab = 16;      // rows per workgroup (one MFMA tile)
+
+// Staged row segments of a 64-row slab: weights (and, for the split FP4 layout,
+// the E8M0 scales) of columns [c0, c0 + kc), row stride padded by one dword so the
+// lanes of different rows read different banks.
 template <class R>
-struct LaneBlock;
+struct Tile;
 
 template <int F>
-struct LaneBlock<QRows<F>> {
-    static __device__ __forceinline__ half8 get(const uint32_t (&d)[Fmt<F>::kPairDw], int blk, uint32_t kg,
+struct Tile<QRows<F>> {
+    static constexpr int kBB = Fmt<F>::kBlockBytes;
+    static constexpr bool kScales = false;
+    static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 32 * kBB / 4; }  // dwords per row segment
+    static constexpr __host__ __device__ uint32_t sdw(uint32_t) { return 0; }
+    static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) { return kSlab * (wdw(kc) + 1); }
+    static __device__ __forceinline__ size_t wpitch(const QRows<F>& m) { return m.row_bytes; }
+    static __device__ __forceinline__ size_t spitch(const QRows<F>&) { return 0; }
+    static __device__ __forceinline__ const uint8_t* wrow(const QRows<F>& m, uint32_t c0) {
+        return m.q + static_cast<size_t>(c0 / 32) * kBB;
+    }
+    static __device__ __forceinline__ const uint8_t* srow(const QRows<F>&, uint32_t) { return nullptr; }
+    // block b of a row (LDS row base `w`), k group kg: 8 weights and the scale
+    static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t*, uint32_t b, uint32_t kg,
                                                 float& scale) {
+        const uint8_t* blk = w + b * kBB;
+        auto u16 = [&](uint32_t o) { return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(blk + o)); };
+        scale = f16_to_f32(u16(0));
         if constexpr (F == kQ4) {
-            // bytes 0-1 scale0, 2-17 nibbles0, 18-19 scale1, 20-35 nibbles1
-            if (blk == 0) {
-                scale = f16_to_f32(d[0] & 0xFFFFu);
-                const uint32_t n = pick4(kg, alignb(d[1], d[0], 2), alignb(d[2], d[1], 2), alignb(d[3], d[2], 2),
-                                         alignb(d[4], d[3], 2));
-                return nibbles_to_b<false>(n, 0);
-            }
-            scale = f16_to_f32(d[4] >> 16);
-            return nibbles_to_b<false>(pick4(kg, d[5], d[6], d[7], d[8]), 0);
+            return nibbles_to_b<false>(u16(2 + 4 * kg) | (u16(4 + 4 * kg) << 16), 0);
         } else if constexpr (F == kQ5) {
-            // bytes 0-1 scale0, 2-5 mask0, 6-21 nibbles0, 22-23 scale1, 24-27 mask1, 28-43 nibbles1
-            if (blk == 0) {
-                scale = f16_to_f32(d[0] & 0xFFFFu);
-                const uint32_t m = (alignb(d[1], d[0], 2) >> (8 * kg)) & 0xFFu;
-                const uint32_t n = pick4(kg, alignb(d[2], d[1], 2), alignb(d[3], d[2], 2), alignb(d[4], d[3], 2),
-                                         alignb(d[5], d[4], 2));
-                return nibbles_to_b<true>(n, m);
-            }
-            scale = f16_to_f32(d[5] >> 16);
-            return nibbles_to_b<true>(pick4(kg, d[7], d[8], d[9], d[10]), (d[6] >> (8 * kg)) & 0xFFu);
+            return nibbles_to_b<true>(u16(6 + 4 * kg) | (u16(8 + 4 * kg) << 16), blk[2 + kg]);
         } else {
-            // bytes 0-1 scale0, 2-9 lows0, 10-13 highs0, 14-15 scale1, 16-23 lows1, 24-27 highs1
-            uint32_t l0, l1, hb;
-            if (blk == 0) {
-                scale = f16_to_f32(d[0] & 0xFFFFu);
-                l0 = alignb(d[1], d[0], 2);
-                l1 = alignb(d[2], d[1], 2);
-                hb = alignb(d[3], d[2], 2);
-            } else {
-                scale = f16_to_f32(d[3] >> 16);
-                l0 = d[4];
-                l1 = d[5];
-                hb = d[6];
-            }
-            const uint32_t lo16 = ((kg & 2) ? l1 : l0) >> (16 * (kg & 1)) & 0xFFFFu;  // 2 bits per weight
-            const uint32_t h8 = (hb >> (8 * kg)) & 0xFFu;                             // 1 bit per weight
-            const h2 k4 = {(_Float16)1028.0f, (_Float16)1028.0f};
-            h2 p[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {  // weights i and i + 4
-                const uint32_t t = (lo16 >> (2 * i)) & 0x303u;
-                const uint32_t hh = (h8 >> i) & 0x11u;
-                const uint32_t v = (t & 3u) | ((t & 0x300u) << 8) | ((hh & 1u) << 2) | ((hh & 0x10u) << 14);
-                p[i] = as_h2(v | 0x64006400u) - k4;
-            }
-            return pack8(p[0], p[1], p[2], p[3]);
+            return iq3_to_b(u16(2 + 2 * kg), blk[10 + kg]);
         }
     }
 };
 
 template <>
-struct LaneBlock<Fp4Rows> {
-    static __device__ __forceinline__ half8 get(const uint32_t (&d)[9], int blk, uint32_t kg, float& scale) {
-        scale = e8m0_to_f32((d[8] >> (8 * blk)) & 0xFFu) * 16384.0f;
-        const uint32_t n = blk == 0 ? pick4(kg, d[0], d[1], d[2], d[3]) : pick4(kg, d[4], d[5], d[6], d[7]);
-        // E2M1 code c -> fp16 bits ((c & 7) << 9) | ((c & 8) << 12) = value * 2^-14
+struct Tile<Fp4Rows> {
+    static constexpr bool kScales = true;
+    static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 8; }   // kc / 2 bytes
+    static constexpr __host__ __device__ uint32_t sdw(uint32_t kc) { return kc / 128; }  // kc / 32 bytes (kc % 128 == 0)
+    static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) {
+        return kSlab * (wdw(kc) + 1) + kSlab * (sdw(kc) + 1);
+    }
+    static __device__ __forceinline__ size_t wpitch(const Fp4Rows& m) { return m.wrow; }
+    static __device__ __forceinline__ size_t spitch(const Fp4Rows& m) { return m.srow; }
+    static __device__ __forceinline__ const uint8_t* wrow(const Fp4Rows& m, uint32_t c0) { return m.w + c0 / 2; }
+    static __device__ __forceinline__ const uint8_t* srow(const Fp4Rows& m, uint32_t c0) { return m.s + c0 / 32; }
+    static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t* sc, uint32_t b, uint32_t kg,
+                                                float& scale) {
+        scale = e8m0_to_f32(sc[b]) * 16384.0f;
+        const uint32_t n = *reinterpret_cast<const uint32_t*>(w + 16 * b + 4 * kg);
         h2 p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; ++i) {  // E2M1 code c -> fp16 bits ((c & 7) << 9) | ((c & 8) << 12) = value * 2^-14
             const uint32_t t = (n >> (4 * i)) & 0x000F000Fu;
             p[i] = as_h2(((t & 0x00070007u) << 9) | ((t & 0x00080008u) << 12));
         }
@@ -300,132 +377,184 @@ struct LaneBlock<Fp4Rows> {
     }
 };
 
-// ----------------------------------------------------------- grouped GEMMs
-// Cached (not non-temporal) pair loads: the four lanes of a row read the same
-// bytes and consecutive pairs share cache lines, so the lines must stay in L1/L2
-// until the wave has used them.
-template <class R>
-struct PairLoad;
-template <int F>
-struct PairLoad<QRows<F>> {
-    static __device__ __forceinline__ void load(const QRows<F>& m, uint32_t r, uint32_t p, uint32_t (&d)[Fmt<F>::kPairDw]) {
-        const gptr<uint32_t> q = as_global(reinterpret_cast<const uint32_t*>(m.pair_ptr(r, p)));
+// This thread's share of a slab's row segments (seg dwords per row): thread t takes
+// row t / 16 and its dwords t % 16, t % 16 + 16, ... Rows past `rows` read the last
+// row.
+template <int N>
+__device__ __forceinline__ void slab_load(const uint8_t* base, size_t pitch, uint32_t r0, uint32_t rows, uint32_t seg,
+                                          uint32_t (&v)[N]) {
+    const uint32_t rr = threadIdx.x >> 4, c0 = threadIdx.x & 15;
+    const uint32_t r = r0 + rr < rows ? r0 + rr : rows - 1;
+    const gptr<uint32_t> src = as_global(reinterpret_cast<const uint32_t*>(base + static_cast<size_t>(r) * pitch));
 #pragma unroll
-        for (int i = 0; i < Fmt<F>::kPairDw; ++i) d[i] = q[i];
+    for (int q = 0; q < N; ++q) {
+        if (static_cast<uint32_t>(q) * 16u >= seg) break;  // uniform: a short chunk needs fewer units
+        const uint32_t c = c0 + static_cast<uint32_t>(q) * 16u;
+        v[q] = src[c < seg ? c : seg - 1];
     }
-};
-template <>
-struct PairLoad<Fp4Rows> {
-    static __device__ __forceinline__ void load(const Fp4Rows& m, uint32_t r, uint32_t p, uint32_t (&d)[9]) {
-        const gptr<uint32_t> q = as_global(reinterpret_cast<const uint32_t*>(m.w + static_cast<size_t>(r) * m.wrow + p * 32u));
+}
+template <int N>
+__device__ __forceinline__ void slab_store(uint32_t* lds, uint32_t seg, const uint32_t (&v)[N]) {
+    const uint32_t rr = threadIdx.x >> 4, c0 = threadIdx.x & 15;
+    uint32_t* dst = lds + rr * (seg + 1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d[i] = q[i];
-        d[8] = *as_global(reinterpret_cast<const uint16_t*>(m.s + static_cast<size_t>(r) * m.srow + p * 2u));
+    for (int q = 0; q < N; ++q) {
+        if (static_cast<uint32_t>(q) * 16u >= seg) break;
+        const uint32_t c = c0 + static_cast<uint32_t>(q) * 16u;
+        if (c < seg) dst[c] = v[q];
     }
+}
+
+// One chunk's staged bytes of every matrix of the workgroup, in registers.
+template <class R, int M, uint32_t CH>
+struct Staged {
+    static constexpr int kUnits = (Tile<R>::wdw(CH) + 15) / 16;
+    uint32_t w[M][kUnits];
+    uint32_t s[M][1];  // FP4 scales: CH / 128 <= 16 dwords per row
 };
 
-constexpr int kGPairs = 1;  // pairs per wave per step (more in flight measured slower: registers)
-
-// grid = (ceil(rows / 16), max groups), 4 waves: the workgroup owns output rows
-// [16 blockIdx.x, +16) of the group's expert and wave w the w-th quarter of the
-// pairs (k split); the four partial sums meet in LDS. 8 group members per MFMA
-// column set. GATEUP: rows = inter over x (cols = hidden), writes act; else
-// rows = out_dim over act (cols = inter), writes part.
+// grid = (ceil(rows / 16), gy), 256 threads; workgroup (x, y) takes member sets y,
+// y + gy, ... (the number of sets is known only on the device). GATEUP: rows = inter
+// over the split x rows (cols = hidden), writes act; else rows = out_dim over the
+// split act rows (cols = inter), writes part. Dynamic LDS: two chunk buffers of
+// every matrix.
 template <class R, bool GATEUP>
-__global__ __launch_bounds__(256) void moe_grouped_kernel(
-    const objeta_hip_expert_ptrs* __restrict__ table, GroupWs gw, const _Float16* __restrict__ vh,
-    const _Float16* __restrict__ vl, const float* __restrict__ vmult, float* __restrict__ out, uint32_t cols,
-    uint32_t rows, uint32_t k, float limit) {
-    __shared__ f32x4 red[GATEUP ? 2 : 1][3][64];
-    const uint32_t g = blockIdx.y;
-    if (g >= gw.hdr[0]) return;
+__global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Float16* __restrict__ vh,
+                                                          const _Float16* __restrict__ vl,
+                                                          const float* __restrict__ vmult, float* __restrict__ out,
+                                                          uint32_t cols, uint32_t rows, uint32_t k, uint32_t n_assign,
+                                                          float limit) {
+    extern __shared__ uint32_t tl[];
+    // the cross-wave partial sums reuse the chunk buffers once a set's products are done
+    auto red = reinterpret_cast<f32x4 (*)[3][64]>(tl);
+    constexpr int kMats = GATEUP ? 2 : 1;
+    constexpr uint32_t kChunk = kChunkOf<GATEUP>;
+    constexpr int kB = kChunk / 32 / 4;  // blocks per wave and chunk
+    const uint32_t n_sets = gw.hdr[1];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t row = blockIdx.x * 16 + (lane & 15), kg = lane >> 4;
-    const uint32_t rc = row < rows ? row : rows - 1;
-    const uint32_t e = gw.grp_expert[g];
-    const uint32_t s0 = gw.grp_start[g], m = gw.grp_start[g + 1] - s0;
-    const objeta_hip_expert_ptrs P = table[e];
-    const R w0 = GATEUP ? RowsOf<R>::make(P.gate, P.gate_scale, cols) : RowsOf<R>::make(P.down, P.down_scale, cols);
-    const R w1 = RowsOf<R>::make(P.up, P.up_scale, cols);
-    const uint32_t pairs = cols >> 6;
-    const uint32_t ppw = (pairs + 3) / 4;
-    const uint32_t p0 = wave * ppw < pairs ? wave * ppw : pairs;
-    const uint32_t p1 = p0 + ppw < pairs ? p0 + ppw : pairs;
-    for (uint32_t c0 = 0; c0 < m; c0 += 8) {
-        // A operand: member c0 + (lane&15)/2 of the group, part (lane&1)
-        const uint32_t jm = c0 + ((lane & 15) >> 1);
-        const uint32_t am = gw.alist[s0 + (jm < m ? jm : m - 1)];
-        const uint32_t vrow = GATEUP ? am / k : am;  // token row of x, or the assignment's act row
-        const gptr<half8> src = as_global(reinterpret_cast<const half8*>(
-            ((lane & 1) ? vl : vh) + static_cast<size_t>(vrow) * cols + 8 * kg));
-        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-        for (uint32_t pb = p0; pb < p1; pb += kGPairs) {
-            uint32_t d0[kGPairs][R::kDw], d1[kGPairs][R::kDw];
-            half8 xa[kGPairs][2];
+    const uint32_t r0 = blockIdx.x * kSlab;
+    const uint32_t row = r0 + (lane & 15), kg = lane >> 4;
+    const uint32_t nchunks = (cols + kChunk - 1) / kChunk;
+    const uint32_t buf_dw = kMats * Tile<R>::lds_dw(kChunk);
+    for (uint32_t si = blockIdx.y; si < n_sets; si += gridDim.y) {
+        const SetRec sr = gw.sets[si];
+        const objeta_hip_expert_ptrs& P = sr.p;
+        const uint32_t m = (sr.mem[0] >> 12) + 1u;
+        auto member = [&](uint32_t j) {  // assignment of member j (< 8)
+            uint32_t a = sr.mem[0] & 0xFFFu;
 #pragma unroll
-            for (int i = 0; i < kGPairs; ++i) {
-                const uint32_t p = pb + i < p1 ? pb + i : p1 - 1;
-                PairLoad<R>::load(w0, rc, p, d0[i]);
-                if constexpr (GATEUP) PairLoad<R>::load(w1, rc, p, d1[i]);
-                xa[i][0] = src[8 * p];  // half8 units: 64 halves per pair
-                xa[i][1] = src[8 * p + 4];
+            for (uint32_t q = 1; q < 8; ++q) a = j == q ? sr.mem[q] : a;
+            return a;
+        };
+        R mt[kMats];
+        mt[0] = GATEUP ? RowsOf<R>::make(P.gate, P.gate_scale, cols) : RowsOf<R>::make(P.down, P.down_scale, cols);
+        if constexpr (GATEUP) mt[kMats - 1] = RowsOf<R>::make(P.up, P.up_scale, cols);
+        const size_t wpitch = Tile<R>::wpitch(mt[0]), spitch = Tile<R>::spitch(mt[0]);
+        // A operand rows: member (lane&15)/2 of the set, part (lane&1)
+        const uint32_t am = member((lane & 15) >> 1);
+        // token row of x (routed or shared act row), or the act row itself
+        auto xrow = [&](uint32_t a) { return a < n_assign ? a / k : a - n_assign; };
+        const uint32_t vrow = GATEUP ? xrow(am) : am;
+        auto stage = [&](uint32_t kc0, Staged<R, kMats, kChunk>& st) {
+            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
+#pragma unroll
+            for (int t = 0; t < kMats; ++t) {
+                slab_load(Tile<R>::wrow(mt[t], kc0), wpitch, r0, rows, Tile<R>::wdw(kc), st.w[t]);
+                if constexpr (Tile<R>::kScales)
+                    slab_load(Tile<R>::srow(mt[t], kc0), spitch, r0, rows, Tile<R>::sdw(kc), st.s[t]);
             }
-            // every load of the batch is in flight before the first product; pairs
-            // past p1 (clamped copies) are computed and dropped, so the batch has no
-            // branch for the scheduler to sink loads into
-            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto operands = [&](uint32_t kc0, half8 (&xr)[kB]) {
+            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
+            const uint32_t nb = kc / 32, per = (nb + 3) / 4;
+            const uint32_t b0 = wave * per < nb ? wave * per : nb, b1 = b0 + per < nb ? b0 + per : nb;
 #pragma unroll
-            for (int i = 0; i < kGPairs; ++i) {
-                const bool use = pb + i < p1;
+            for (int i = 0; i < kB; ++i) {
+                const uint32_t b = b0 + static_cast<uint32_t>(i) < b1 ? b0 + static_cast<uint32_t>(i) : (b1 ? b1 - 1 : 0);
+                const size_t at = static_cast<size_t>(vrow) * cols + kc0 + 32 * b + 8 * kg;
+                xr[i] = *as_global(reinterpret_cast<const half8*>(((lane & 1) ? vl : vh) + at));
+            }
+        };
+        auto commit = [&](uint32_t kc0, uint32_t buf, const Staged<R, kMats, kChunk>& st) {
+            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
 #pragma unroll
-                for (int blk = 0; blk < 2; ++blk) {
+            for (int t = 0; t < kMats; ++t) {
+                uint32_t* base = tl + buf * buf_dw + t * Tile<R>::lds_dw(kChunk);
+                slab_store(base, Tile<R>::wdw(kc), st.w[t]);
+                if constexpr (Tile<R>::kScales)
+                    slab_store(base + kSlab * (Tile<R>::wdw(kc) + 1), Tile<R>::sdw(kc), st.s[t]);
+            }
+        };
+        f32x4 acc[kMats];
+#pragma unroll
+        for (int t = 0; t < kMats; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        Staged<R, kMats, kChunk> st;
+        half8 xa[kB];
+        stage(0, st);
+        operands(0, xa);
+        commit(0, 0, st);
+        __syncthreads();
+        for (uint32_t c = 0; c < nchunks; ++c) {
+            const uint32_t kc0 = c * kChunk;
+            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
+            if (c + 1 < nchunks) stage(kc0 + kChunk, st);  // in flight during the products below
+            const uint32_t nb = kc / 32, per = (nb + 3) / 4;
+            const uint32_t b0 = wave * per < nb ? wave * per : nb, b1 = b0 + per < nb ? b0 + per : nb;
+#pragma unroll
+            for (int t = 0; t < kMats; ++t) {
+                const uint32_t* base = tl + (c & 1) * buf_dw + t * Tile<R>::lds_dw(kChunk);
+                const uint8_t* wl = reinterpret_cast<const uint8_t*>(base + (lane & 15) * (Tile<R>::wdw(kc) + 1));
+                const uint8_t* sl = reinterpret_cast<const uint8_t*>(base + kSlab * (Tile<R>::wdw(kc) + 1) +
+                                                                     (lane & 15) * (Tile<R>::sdw(kc) + 1));
+#pragma unroll
+                for (int i = 0; i < kB; ++i) {
+                    if (b0 + static_cast<uint32_t>(i) >= b1) break;
+                    float sc;
+                    const half8 bw = Tile<R>::get(wl, sl, b0 + static_cast<uint32_t>(i), kg, sc);
                     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                    float sc0;
-                    const half8 b0 = LaneBlock<R>::get(d0[i], blk, kg, sc0);
-                    const f32x4 r0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[i][blk], b0, z, 0, 0, 0);
+                    const f32x4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[i], bw, z, 0, 0, 0);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc0[q] = use ? __builtin_fmaf(sc0, r0[q], acc0[q]) : acc0[q];
-                    if constexpr (GATEUP) {
-                        float sc1;
-                        const half8 b1 = LaneBlock<R>::get(d1[i], blk, kg, sc1);
-                        const f32x4 r1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[i][blk], b1, z, 0, 0, 0);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) acc1[q] = use ? __builtin_fmaf(sc1, r1[q], acc1[q]) : acc1[q];
-                    }
+                    for (int q = 0; q < 4; ++q) acc[t][q] = __builtin_fmaf(sc, r[q], acc[t][q]);
                 }
             }
+            if (c + 1 < nchunks) {
+                // the next activation operands (into the registers just used) travel
+                // while the staged weights are stored; buffer (c+1)&1 was last read in
+                // iteration c-1, which every wave has finished (the barrier below)
+                operands(kc0 + kChunk, xa);
+                commit(kc0 + kChunk, (c + 1) & 1, st);
+            }
+            __syncthreads();
         }
         // the four waves' partial sums (same lane layout) meet in LDS; wave 0 adds
         if (wave > 0) {
-            red[0][wave - 1][lane] = acc0;
-            if constexpr (GATEUP) red[GATEUP ? 1 : 0][wave - 1][lane] = acc1;
+#pragma unroll
+            for (int t = 0; t < kMats; ++t) red[t][wave - 1][lane] = acc[t];
         }
         __syncthreads();
         if (wave == 0) {
 #pragma unroll
-            for (int v = 0; v < 3; ++v) {
-                acc0 += red[0][v][lane];
-                if constexpr (GATEUP) acc1 += red[GATEUP ? 1 : 0][v][lane];
-            }
-            // lane: output row `row`, members c0 + 2kg + q (q = 0, 1) as (hi, lo) in 2q, 2q+1
+            for (int v = 0; v < 3; ++v)
+#pragma unroll
+                for (int t = 0; t < kMats; ++t) acc[t] += red[t][v][lane];
+            // lane: output row `row`, members 2kg + q (q = 0, 1) as (hi, lo) in 2q, 2q+1
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                const uint32_t j = c0 + 2 * kg + static_cast<uint32_t>(q);
-                if (j < m && row < rows) {
-                    const uint32_t a = gw.alist[s0 + j];
-                    const float mul = vmult[GATEUP ? a / k : a];
-                    const float v0 = (acc0[2 * q] + acc0[2 * q + 1]) * mul;
-                    if constexpr (GATEUP) {
-                        const float v1 = (acc1[2 * q] + acc1[2 * q + 1]) * mul;
-                        float gv = v0, uv = v1;
-                        if (limit > 0.0f) {
-                            uv = fminf(limit, fmaxf(-limit, uv));
-                            gv = fminf(limit, gv);
-                        }
-                        out[static_cast<size_t>(a) * rows + row] = (gv / (1.0f + expf(-gv))) * uv;
-                    } else {
-                        out[static_cast<size_t>(a) * rows + row] = v0;
+                const uint32_t j = 2 * kg + static_cast<uint32_t>(q);  // uniform over 16 lanes
+                const bool live = j < m && row < rows;
+                const uint32_t a = member(j);  // unused slots repeat the last member
+                const float mul = vmult[GATEUP ? xrow(a) : a];
+                const float v0 = (acc[0][2 * q] + acc[0][2 * q + 1]) * mul;
+                if constexpr (GATEUP) {
+                    const float v1 = (acc[kMats - 1][2 * q] + acc[kMats - 1][2 * q + 1]) * mul;
+                    float gv = v0, uv = v1;
+                    if (limit > 0.0f) {
+                        uv = fminf(limit, fmaxf(-limit, uv));
+                        gv = fminf(limit, gv);
                     }
+                    if (live) out[static_cast<size_t>(a) * rows + row] = (gv / (1.0f + expf(-gv))) * uv;
+                } else {
+                    if (live) out[static_cast<size_t>(a) * rows + row] = v0;
                 }
             }
         }
@@ -433,11 +562,13 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(
     }
 }
 
-// out[t][r] = residual[t][r] + sum_j w[t][j] * part[t*k + j][r], slots in order; an
-// out-of-table id makes the element NaN (the id was reported by the grouping).
+// out[t][r] = residual[t][r] + sum_j w[t][j] * part[t*k + j][r], slots in order, then
+// + shared_part[t][r] (the shared expert, weight 1, last); an out-of-table id makes
+// the element NaN (the id was reported by the grouping).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint32_t* __restrict__ ids, const float* __restrict__ wts,
-                                                          const float* __restrict__ part, const float* resid, float* out,
-                                                          uint32_t k, uint32_t out_dim, uint32_t n_table) {
+                                                          const float* __restrict__ part,
+                                                          const float* __restrict__ shared_part, const float* resid,
+                                                          float* out, uint32_t k, uint32_t out_dim, uint32_t n_table) {
     const uint32_t t = blockIdx.y;
     const uint32_t r = blockIdx.x * 256 + threadIdx.x;
     if (r >= out_dim) return;
@@ -447,28 +578,47 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint32_t* __rest
         const float v = ids[a] < n_table ? part[static_cast<size_t>(a) * out_dim + r] : __builtin_nanf("");
         acc = __builtin_fmaf(wts[a], v, acc);
     }
+    if (shared_part) acc += shared_part[static_cast<size_t>(t) * out_dim + r];
     out[static_cast<size_t>(t) * out_dim + r] = acc;
 }
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 template <class R>
-hipError_t launch_grouped(hipStream_t s, const objeta_hip_expert_ptrs* table, GroupWs gw, const _Float16* xh,
-                          const _Float16* xl, const float* xmult, float* act, _Float16* ah, _Float16* al,
-                          float* amult, float* part, uint32_t n_assign, uint32_t max_groups, uint32_t k,
-                          uint32_t hidden, uint32_t inter, uint32_t out_dim, float limit) {
-    hipLaunchKernelGGL((moe_grouped_kernel<R, true>), dim3((inter + 15) / 16, max_groups), dim3(256), 0, s, table, gw,
-                       xh, xl, xmult, act, hidden, inter, k, limit);
-    hipLaunchKernelGGL(moe_split_kernel, dim3(n_assign), dim3(256), 0, s, act, inter, ah, al, amult);
-    hipLaunchKernelGGL((moe_grouped_kernel<R, false>), dim3((out_dim + 15) / 16, max_groups), dim3(256), 0, s, table,
-                       gw, ah, al, amult, part, inter, out_dim, k, 0.0f);
+hipError_t launch_grouped(hipStream_t s, GroupWs gw, const _Float16* xh, const _Float16* xl, const float* xmult,
+                          float* act, _Float16* ah, _Float16* al, float* amult, float* part, uint32_t n_assign,
+                          uint32_t n_rows, uint32_t max_sets, uint32_t k,
+                          uint32_t hidden, uint32_t inter, uint32_t out_dim, float limit, uint32_t cus) {
+    // about sixteen workgroups per CU over all slabs, at most one per member set
+    auto gy = [&](uint32_t rows) {
+        const uint32_t slabs = (rows + kSlab - 1) / kSlab;
+        const uint32_t want = (16 * cus + slabs - 1) / slabs;
+        return want < 1 ? 1u : (want > max_sets ? max_sets : want);
+    };
+    const size_t lds_gu = 2 * 2 * 4 * static_cast<size_t>(Tile<R>::lds_dw(kChunkOf<true>));
+    const size_t lds_dn = 2 * 4 * static_cast<size_t>(Tile<R>::lds_dw(kChunkOf<false>));
+    hipLaunchKernelGGL((moe_grouped_kernel<R, true>), dim3((inter + kSlab - 1) / kSlab, gy(inter)), dim3(256), lds_gu,
+                       s, gw, xh, xl, xmult, act, hidden, inter, k, n_assign, limit);
+    hipLaunchKernelGGL(moe_split_kernel, dim3(n_rows), dim3(256), 0, s, act, inter, ah, al, amult);
+    hipLaunchKernelGGL((moe_grouped_kernel<R, false>), dim3((out_dim + kSlab - 1) / kSlab, gy(out_dim)), dim3(256),
+                       lds_dn, s, gw, ah, al, amult, part, inter, out_dim, k, n_assign, 0.0f);
     return hipGetLastError();
 }
 
 }  // namespace
 
+bool grouped_supported(int32_t format, uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden,
+                       uint64_t inter, uint64_t out_dim) {
+    if (format < OBJETA_HIP_Q4_0 || format > OBJETA_HIP_FP4_E2M1) return false;
+    if (k == 0 || k > 32 || n_table == 0 || n_table > kGMaxTable || n_tokens * k > kGMaxAssign) return false;
+    if (hidden == 0 || inter == 0 || hidden % 64 || inter % 64 || hidden > (1u << 20) || inter > (1u << 20) ||
+        out_dim > (1u << 20))
+        return false;
+    return format != OBJETA_HIP_FP4_E2M1 || (hidden % 128 == 0 && inter % 128 == 0);
+}
+
 int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
-                           uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
+                           uint64_t n_table, const objeta_hip_expert_ptrs* shared, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                            const float* x, const float* resid, float* out, uint64_t hidden, uint64_t inter,
                            uint64_t out_dim, float limit) {
     const char* action = "launch grouped-token MoE";
@@ -483,31 +633,32 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
     if (hidden == 0 || inter == 0 || hidden % 64 || inter % 64 || hidden > (1u << 20) || inter > (1u << 20) ||
         out_dim > (1u << 20))
         OBJ_FAIL(kUnsupported, action, "hidden and intermediate must be non-zero multiples of 64 (<= 2^20)");
+    if (format == OBJETA_HIP_FP4_E2M1 && (hidden % 128 || inter % 128))
+        OBJ_FAIL(kUnsupported, action, "the grouped path takes split-FP4 experts with hidden and intermediate % 128 == 0");
     if (!table || !ids || !wts || !x || !out) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     if (reinterpret_cast<uintptr_t>(x) % 16) OBJ_FAIL(kInvalidInput, action, "x must be 16-byte aligned");
     const uint32_t A = static_cast<uint32_t>(n_tokens * k), T = static_cast<uint32_t>(n_tokens);
+    const uint32_t NR = A + (shared ? T : 0);                  // act rows: routed, then shared
+    const uint32_t NS = A + (shared ? (T + 7) / 8 : 0);        // member sets at most
     const uint32_t H = static_cast<uint32_t>(hidden), I = static_cast<uint32_t>(inter), O = static_cast<uint32_t>(out_dim);
-    // workspace: group lists, split x, act, split act, per-assignment down rows
+    // workspace: set records, split x, act, split act, per-assignment down rows
     size_t off = 0;
     const size_t o_hdr = off; off += align256(16);
-    const size_t o_ge = off; off += align256(4ull * A);
-    const size_t o_gs = off; off += align256(4ull * (A + 1));
-    const size_t o_al = off; off += align256(4ull * A);
+    const size_t o_set = off; off += align256(sizeof(SetRec) * NS);
     const size_t o_xm = off; off += align256(4ull * T);
-    const size_t o_am = off; off += align256(4ull * A);
+    const size_t o_am = off; off += align256(4ull * NR);
     const size_t o_xh = off; off += align256(2ull * T * H);
     const size_t o_xl = off; off += align256(2ull * T * H);
-    const size_t o_act = off; off += align256(4ull * A * I);
-    const size_t o_ah = off; off += align256(2ull * A * I);
-    const size_t o_all = off; off += align256(2ull * A * I);
-    const size_t o_part = off; off += align256(4ull * A * O);
+    const size_t o_act = off; off += align256(4ull * NR * I);
+    const size_t o_ah = off; off += align256(2ull * NR * I);
+    const size_t o_all = off; off += align256(2ull * NR * I);
+    const size_t o_part = off; off += align256(4ull * NR * O);
     void* wsp = nullptr;
     OBJ_TRY(ensure_workspace(ctx, s, kWsGrouped, off, &wsp));
     char* b = static_cast<char*>(wsp);
-    GroupWs gw{reinterpret_cast<uint32_t*>(b + o_hdr), reinterpret_cast<uint32_t*>(b + o_ge),
-               reinterpret_cast<uint32_t*>(b + o_gs), reinterpret_cast<uint32_t*>(b + o_al)};
-    float* xmult = reinterpret_cast<float*>(b + o_xm);
+    GroupWs gw{reinterpret_cast<uint32_t*>(b + o_hdr), reinterpret_cast<SetRec*>(b + o_set)};
     float* amult = reinterpret_cast<float*>(b + o_am);
+    float* xmult = reinterpret_cast<float*>(b + o_xm);
     auto* xh = reinterpret_cast<_Float16*>(b + o_xh);
     auto* xl = reinterpret_cast<_Float16*>(b + o_xl);
     float* act = reinterpret_cast<float*>(b + o_act);
@@ -515,32 +666,33 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
     auto* al = reinterpret_cast<_Float16*>(b + o_all);
     float* part = reinterpret_cast<float*>(b + o_part);
     uint32_t* err = ctx->err_word;
-    const uint32_t max_groups = A < n_table ? A : static_cast<uint32_t>(n_table);
-    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, s, ids, A, static_cast<uint32_t>(n_table), gw, err);
-    hipLaunchKernelGGL(moe_split_kernel, dim3(T), dim3(256), 0, s, x, H, xh, xl, xmult);
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    hipLaunchKernelGGL(moe_prepare_kernel, dim3(1 + T), dim3(256), 0, s, ids, A, static_cast<uint32_t>(n_table), table,
+                       shared, T, gw, err, x, H, xh, xl, xmult);
     hipError_t e;
     const uint32_t kk = static_cast<uint32_t>(k);
     switch (format) {
         case OBJETA_HIP_Q4_0:
-            e = launch_grouped<QRows<kQ4>>(s, table, gw, xh, xl, xmult, act, ah, al, amult, part, A, max_groups, kk, H,
-                                           I, O, limit);
+            e = launch_grouped<QRows<kQ4>>(s, gw, xh, xl, xmult, act, ah, al, amult, part, A, NR, NS, kk, H,
+                                           I, O, limit, cus);
             break;
         case OBJETA_HIP_Q5_0:
-            e = launch_grouped<QRows<kQ5>>(s, table, gw, xh, xl, xmult, act, ah, al, amult, part, A, max_groups, kk, H,
-                                           I, O, limit);
+            e = launch_grouped<QRows<kQ5>>(s, gw, xh, xl, xmult, act, ah, al, amult, part, A, NR, NS, kk, H,
+                                           I, O, limit, cus);
             break;
         case OBJETA_HIP_IQ3_0:
-            e = launch_grouped<QRows<kIQ3>>(s, table, gw, xh, xl, xmult, act, ah, al, amult, part, A, max_groups, kk,
-                                            H, I, O, limit);
+            e = launch_grouped<QRows<kIQ3>>(s, gw, xh, xl, xmult, act, ah, al, amult, part, A, NR, NS, kk,
+                                            H, I, O, limit, cus);
             break;
         default:
-            e = launch_grouped<Fp4Rows>(s, table, gw, xh, xl, xmult, act, ah, al, amult, part, A, max_groups, kk, H, I,
-                                        O, limit);
+            e = launch_grouped<Fp4Rows>(s, gw, xh, xl, xmult, act, ah, al, amult, part, A, NR, NS, kk, H, I,
+                                        O, limit, cus);
             break;
     }
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(moe_combine_kernel, dim3((O + 255) / 256, T), dim3(256), 0, s, ids, wts, part, resid, out, kk,
-                           O, static_cast<uint32_t>(n_table));
+        hipLaunchKernelGGL(moe_combine_kernel, dim3((O + 255) / 256, T), dim3(256), 0, s, ids, wts, part,
+                           shared ? part + static_cast<size_t>(A) * O : nullptr, resid, out, kk, O,
+                           static_cast<uint32_t>(n_table));
         e = hipGetLastError();
     }
     if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
@@ -560,7 +712,7 @@ extern "C" int32_t objeta_hip_moe_grouped_device(objeta_hip_context* ctx, int32_
     OBJ_GUARD_BEGIN
     OBJ_TRY(check_ctx(ctx, "moe_grouped_device"));
     OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
-    return launch_moe_grouped(ctx, format, resolve_stream(ctx, stream), d_table, n_table, d_ids, d_weights, n_tokens,
-                              k, d_x, d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit);
+    return launch_moe_grouped(ctx, format, resolve_stream(ctx, stream), d_table, n_table, nullptr, d_ids, d_weights,
+                              n_tokens, k, d_x, d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit);
     OBJ_GUARD_END
 }

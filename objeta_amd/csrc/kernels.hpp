@@ -81,8 +81,15 @@ int32_t bind_static_scratch(objeta_hip_context* ctx);
 int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
                         float** out);
 
+// Batches from this many tokens run the grouped-token products in the layer entry
+// points (measured on MI355X at hidden 2048, 128 experts, top-8: per-assignment
+// faster at 8 tokens, grouped at 16 and beyond).
+constexpr uint64_t kGroupedMinTokens = 12;
+// Whether launch_moe_grouped takes this shape.
+bool grouped_supported(int32_t format, uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden,
+                       uint64_t inter, uint64_t out_dim);
 int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
-                           uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
+                           uint64_t n_table, const objeta_hip_expert_ptrs* shared, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                            const float* x, const float* resid, float* out, uint64_t hidden, uint64_t inter,
                            uint64_t out_dim, float limit);
 

@@ -897,6 +897,15 @@ int32_t objeta_hip_moe_layer_shared_device(objeta_hip_context* ctx, int32_t form
     hipStream_t s = resolve_stream(ctx, stream);
     if (n_tokens == 0) return 0;
     if (!d_ids_out || !d_weights_out) OBJ_FAIL(kInvalidInput, "moe_layer_device", "NULL routing output");
+    // a batch whose tokens share experts: each selected expert's matrices once for
+    // all of its tokens
+    if (out_dim > 0 && n_tokens >= kGroupedMinTokens && d_table &&
+        grouped_supported(format, n_experts, n_tokens, k, hidden, intermediate, out_dim)) {
+        OBJ_TRY(launch_router(ctx, s, d_router_w, d_router_bias, d_x, n_tokens, n_experts, hidden, k, renormalize,
+                              d_ids_out, d_weights_out, nullptr, nullptr));
+        return launch_moe_grouped(ctx, format, s, d_table, n_experts, d_shared, d_ids_out, d_weights_out, n_tokens, k,
+                                  d_x, d_residual, d_out, hidden, intermediate, out_dim, swiglu_limit);
+    }
     // the router also resolves the selection to table entries for the expert kernels
     void* sws = nullptr;
     OBJ_TRY(ensure_workspace(ctx, s, kWsSelTab, static_cast<size_t>(n_tokens * (k ? k : 1)) * sizeof(objeta_hip_expert_ptrs),

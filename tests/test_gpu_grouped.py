@@ -122,3 +122,45 @@ def test_grouped_rejects_unsupported_shapes(backend):
         moe.grouped_device(Q4, table, d, d, 1, 1, d, None, d, 96, 64, 64)  # hidden 96 is not a multiple of 64
     assert e.value.kind == "Unsupported"
     del keep
+
+
+@pytest.mark.parametrize("fmt,E,K,T,H,I,limit", [
+    (Q4, 32, 4, 12, 512, 256, 0.0),     # the smallest batch the layer entry point groups
+    (FP4, 16, 4, 20, 1024, 512, 0.0),
+    (Q5, 24, 3, 40, 256, 128, 0.0),     # five shared-expert sets
+    (Q4, 16, 2, 13, 256, 128, 0.05),    # SwiGLU clamp (against the per-assignment path)
+])
+def test_layer_batch_runs_grouped_with_shared_expert(backend, fmt, E, K, T, H, I, limit):
+    """objeta_hip_moe_layer_shared_device at a batch: router, then the grouped
+    products with the shared expert as one more group (every token, weight 1, added
+    after the routed sum as moe.rs:1552-1600 does). Each token matches the oracle's
+    routing and selected_moe with the shared expert, and the per-assignment path on
+    the same selection."""
+    experts = make_experts(fmt, E + 1, H, I, H, seed=40 + fmt, gen="gauss")
+    table, keep = device_table(backend, fmt, experts[:E])
+    shared, keep_s = device_table(backend, fmt, experts[E:])
+    w_r = orc.gauss(E * H, 50 + fmt, 0.02)
+    xs = orc.gauss(T * H, 60 + fmt, 1.0).reshape(T, H)
+    d_x = backend.to_device(xs.ravel())
+    d_out, d_ref = backend.alloc(4 * T * H), backend.alloc(4 * T * H)
+    d_ids, d_w = backend.alloc(4 * T * K), backend.alloc(4 * T * K)
+    moe = MoeExecutor(backend)
+    moe.layer_device(fmt, table, backend.to_device(w_r), None, K, T, d_x, d_x, d_out, d_ids, d_w, H, I, H,
+                     swiglu_limit=limit, shared=shared)
+    moe.selected_device(fmt, table, d_ids, d_w, T, K, d_x, d_x, d_ref, H, I, H, swiglu_limit=limit, shared=shared)
+    backend.synchronize()
+    assert moe.device_error() == 0
+    ids = d_ids.download(np.uint32, T * K).reshape(T, K)
+    out = d_out.download(np.float32, T * H).reshape(T, H)
+    per = d_ref.download(np.float32, T * H).reshape(T, H)
+    oe = oracle_experts(fmt, experts)
+    for t in range(T):
+        rid, rw, _, _ = orc.router(w_r, xs[t], E, H, K, renormalize=True)
+        assert np.array_equal(ids[t], rid), t
+        if limit == 0.0:  # the clamp's own oracle check is test_gpu_moe.test_moe_swiglu_limit
+            sel = [(int(i), float(v)) for i, v in zip(rid, rw)]
+            ref = orc.selected_moe(fmt, oe[:E], sel, xs[t], H, I, H, shared=oe[E])
+            assert_moe_close(out[t] - xs[t], ref)
+    scale = float(np.max(np.abs(per)))
+    assert float(np.max(np.abs(out - per))) <= 1e-4 * scale
+    del keep, keep_s
