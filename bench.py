@@ -15,8 +15,9 @@ Also measured in the same run (each in its own object of the JSON line):
 - kernels: each layer kernel alone (router, gate/up, down), replayed from a graph
   of launches that rotate over more weight bytes than the 256 MB MALL holds; one
   roofline entry each, and `roofline` names the one with the most time;
-- batch: 16 tokens per step through the same 48 layers, per-assignment kernels
-  and the grouped-token product;
+- batch: 16 and 32 tokens per step through the same 48 layers: the layer entry
+  point (grouped-token MFMA products from 12 tokens) against the router plus the
+  per-assignment kernels;
 - gemv: Q4_0 [1024 x 4096] batch 1, and Q4_0 / Q5_0 / IQ3_0 at [4096 x 4096] and
   [14336 x 4096], batch 1 and 8, each over a >= 4 GB rotated working set;
 - deepseek: one H 7168 / 256 routed + 1 shared / top-8 / I 2048 FP4 layer at
@@ -343,49 +344,61 @@ def run_kernels(env: Env, st: QwenStack, layer_io, reps: int):
     return entries
 
 
-# ------------------------------------------------------------------- batch 16
+# ------------------------------------------------------------------- batches
 def run_batch(env: Env, st: QwenStack, args, seed):
-    L, H, E, K, I, B = st.layers, st.H, st.E, st.K, st.I, args.batch
+    """Batches of args.batch and 2 * args.batch tokens through every layer: the layer
+    entry point (router, then the grouped-token products from 12 tokens on) against
+    the router followed by the per-assignment kernels on the same selections."""
+    L, H, E, K, I = st.layers, st.H, st.E, st.K, st.I
     be = env.be
-    xb = be.alloc(4 * B * H)
-    env.fill_gauss(xb.ptr, B * H, seed + 99, 1.0)
-    hb = be.alloc(4 * B * H)
-    idsb = be.alloc(4 * L * B * K)
-    wtsb = be.alloc(4 * L * B * K)
+    out = {"path": "objeta_hip_moe_layer_device (router + grouped-token MFMA products from 12 tokens) vs "
+                   "router + objeta_hip_moe_selected_device (per-assignment kernels); one graph per pass of "
+                   f"{L} layers"}
+    for B in (args.batch, 2 * args.batch):
+        xb = be.alloc(4 * B * H)
+        env.fill_gauss(xb.ptr, B * H, seed + 99 + B, 1.0)
+        hb = be.alloc(4 * B * H)
+        idsb = be.alloc(4 * L * B * K)
+        wtsb = be.alloc(4 * L * B * K)
 
-    def enqueue(grouped: bool):
-        for l in range(L):
-            src = xb.addr() if l == 0 else hb.addr()
-            li, lw = idsb.addr(4 * l * B * K), wtsb.addr(4 * l * B * K)
-            if grouped:
-                env.check(env.lib.objeta_hip_router_topk_device(env.ctx, env.stream, st.router_w[l].addr(),
-                                                                st.router_b[l].addr(), src, B, E, H, K, 1, li, lw))
-                env.moe.grouped_device(st.fmt, st.tables[l], li, lw, B, K, src, src, hb.addr(), H, I, H,
-                                       stream=env.stream)
-            else:
-                env.moe.layer_device(st.fmt, st.tables[l], st.router_w[l], st.router_b[l], K, B, src, src, hb.addr(),
-                                     li, lw, H, I, H, stream=env.stream)
+        def enqueue(layer_entry: bool, B=B, xb=xb, hb=hb, idsb=idsb, wtsb=wtsb):
+            for l in range(L):
+                src = xb.addr() if l == 0 else hb.addr()
+                li, lw = idsb.addr(4 * l * B * K), wtsb.addr(4 * l * B * K)
+                if layer_entry:
+                    env.moe.layer_device(st.fmt, st.tables[l], st.router_w[l], st.router_b[l], K, B, src, src,
+                                         hb.addr(), li, lw, H, I, H, stream=env.stream)
+                else:
+                    env.check(env.lib.objeta_hip_router_topk_device(env.ctx, env.stream, st.router_w[l].addr(),
+                                                                    st.router_b[l].addr(), src, B, E, H, K, 1, li,
+                                                                    lw))
+                    env.moe.selected_device(st.fmt, st.tables[l], li, lw, B, K, src, src, hb.addr(), H, I, H,
+                                            stream=env.stream)
 
-    res = {}
-    for grouped in (True, False):
-        enqueue(grouped)
-        be.synchronize(env.stream)
-        g = env.capture(lambda grouped=grouped: enqueue(grouped))
-        for _ in range(3):
-            env.launch(g)
-        be.synchronize(env.stream)
-        _, per = env.per_step(lambda i: env.launch(g), max(5, args.steps // 20))
-        res[grouped] = stats(per)
-        env.destroy([g])
-    ids_all = idsb.download(np.uint32, L * B * K).reshape(L, B * K)
-    uniq = [len(set(int(v) for v in ids_all[l])) for l in range(L)]
-    ub = sum(uniq) * st.expert_bytes
-    return {"tokens": B, "path": "layer entry point: router + per-assignment gate/up and down kernels",
-            "us_per_step": rnd(res[False], 1), "us_per_token_layer": round(res[False]["avg"] / (L * B), 3),
-            "grouped_path_us_per_step": rnd(res[True], 1),
+        res = {}
+        for layer_entry in (True, False):
+            enqueue(layer_entry)
+            be.synchronize(env.stream)
+            g = env.capture(lambda le=layer_entry: enqueue(le))
+            for _ in range(3):
+                env.launch(g)
+            be.synchronize(env.stream)
+            _, per = env.per_step(lambda i: env.launch(g), max(5, args.steps // 20))
+            res[layer_entry] = stats(per)
+            env.destroy([g])
+        ids_all = idsb.download(np.uint32, L * B * K).reshape(L, B * K)
+        uniq = [len(set(int(v) for v in ids_all[l])) for l in range(L)]
+        ub = sum(uniq) * st.expert_bytes
+        out[f"batch{B}"] = {
+            "tokens": B, "us_per_step": rnd(res[True], 1), "us_per_token_layer": round(res[True]["avg"] / (L * B), 3),
+            "per_assignment_us_per_step": rnd(res[False], 1),
+            "speedup_vs_per_assignment": round(res[False]["avg"] / res[True]["avg"], 3),
             "unique_experts_per_layer": round(sum(uniq) / L, 1), "unique_expert_bytes_per_step": ub,
-            "expert_hbm_gbps": round(ub / (res[False]["avg"] * 1e-6) / 1e9, 1),
-            "grouped_expert_hbm_gbps": round(ub / (res[True]["avg"] * 1e-6) / 1e9, 1)}
+            "expert_hbm_gbps": round(ub / (res[True]["avg"] * 1e-6) / 1e9, 1),
+            "per_assignment_expert_hbm_gbps": round(ub / (res[False]["avg"] * 1e-6) / 1e9, 1)}
+        for b in (xb, hb, idsb, wtsb):
+            b.free()
+    return out
 
 
 # ------------------------------------------------------------------ GEMV sweep
@@ -467,8 +480,10 @@ def run_deepseek(env: Env, args, seed):
     w_r = be.alloc(4 * E * H)
     env.fill_gauss(w_r.ptr, E * H, seed + 5, 0.02)
     res = {"hidden": H, "intermediate": I, "experts": E, "shared_experts": 1, "top_k": K, "format": "DeepSeekFp4E2M1",
-           "expert_bytes": eb, "path": "objeta_hip_moe_layer_shared_device (router, gate/up + SiLU, down + "
-                                       "combine, shared expert last with weight 1) replayed from a hipGraph"}
+           "expert_bytes": eb, "path": "objeta_hip_moe_layer_shared_device replayed from a hipGraph: batch 1 on the "
+                                       "per-assignment kernels (router, gate/up + SiLU, down + combine, shared "
+                                       "expert last with weight 1), batch 32 on the grouped-token products with the "
+                                       "shared expert as one more group"}
     for T in (1, 32):
         P = 8
         xs = be.alloc(4 * P * T * H)
