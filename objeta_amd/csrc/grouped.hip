@@ -171,22 +171,32 @@ __device__ void group_assignments(const uint32_t* __restrict__ ids, uint32_t n_a
     }
     __syncthreads();
     for (uint32_t si = tid; si < ts + n_sh; si += 256) {
-        SetRec r;
-        uint32_t m1;
+        // the record: the expert's table entry, then 8 uint16 act rows (4 dwords),
+        // written field by field (a record assembled in a local lands in scratch)
+        const objeta_hip_expert_ptrs* src;
+        uint32_t first, m1;
         if (si < ts) {
             const uint32_t info = sinfo[si];
-            const uint32_t e = info & 0x7FFu, st = (info >> 11) & 0x7FFu;
+            src = table + (info & 0x7FFu);
+            first = (info >> 11) & 0x7FFu;
             m1 = info >> 22;
-            r.p = table[e];
-            for (uint32_t j = 0; j < 8; ++j) r.mem[j] = static_cast<uint16_t>(sal[st + (j < m1 ? j : m1)]);
         } else {
             const uint32_t t0 = 8 * (si - ts);
+            src = shared;
+            first = t0;
             m1 = (n_tokens - t0 < 8 ? n_tokens - t0 : 8) - 1;
-            r.p = *shared;
-            for (uint32_t j = 0; j < 8; ++j) r.mem[j] = static_cast<uint16_t>(n_assign + t0 + (j < m1 ? j : m1));
         }
-        r.mem[0] = static_cast<uint16_t>(r.mem[0] | (m1 << 12));
-        w.sets[si] = r;
+        auto row = [&](uint32_t j) {
+            const uint32_t jj = j < m1 ? j : m1;
+            return si < ts ? sal[first + jj] : n_assign + first + jj;
+        };
+        uint4 mem;
+        mem.x = (row(0) | (m1 << 12)) | (row(1) << 16);
+        mem.y = row(2) | (row(3) << 16);
+        mem.z = row(4) | (row(5) << 16);
+        mem.w = row(6) | (row(7) << 16);
+        w.sets[si].p = *src;
+        *reinterpret_cast<uint4*>(w.sets[si].mem) = mem;
     }
 }
 
@@ -562,6 +572,147 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
     }
 }
 
+// ------------------------------------------------------ batched GEMV on MFMA
+// y[b][r] = sum_c W[r][c] x[b][c] for up to 8 vectors at once: the grouped
+// products' down form with the matrix as the one expert and the vectors as the
+// members, so every weight is decoded once for all of them. A workgroup covers 16
+// rows over the column range [y * kGemvRange, (y + 1) * kGemvRange): it splits that
+// slice of every vector into two fp16 parts in LDS itself (with the slice's own
+// power of two, which the partial sums take back), and writes its partial sums to
+// part[range][b][r]; gemv_reduce_kernel adds the ranges in order.
+constexpr uint32_t kGemvChunk = 256;
+constexpr uint32_t kGemvRange = 512;             // columns per workgroup (two chunks)
+constexpr uint32_t kGemvXStride = kGemvRange + 8;  // halves per staged vector part (padded)
+
+template <class R>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(const void* __restrict__ w, const void* __restrict__ ws,
+                                                        const float* __restrict__ x, float* __restrict__ part,
+                                                        uint32_t rows, uint32_t cols, uint32_t n_vec) {
+    extern __shared__ uint32_t tl[];
+    __shared__ __align__(16) _Float16 xs[2][8][kGemvXStride];  // [hi / lo][vector][column of the range]
+    __shared__ float xmul[8];
+    constexpr uint32_t kChunk = kGemvChunk;
+    constexpr int kB = kChunk / 32 / 4;  // blocks per wave and chunk
+    auto red = reinterpret_cast<f32x4(*)[64]>(tl);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t r0 = blockIdx.x * kSlab;
+    const uint32_t lr = lane & 15, kg = lane >> 4, row = r0 + lr;
+    const uint32_t k0 = blockIdx.y * kGemvRange, k1 = k0 + kGemvRange < cols ? k0 + kGemvRange : cols;
+    const uint32_t nchunks = (k1 - k0 + kChunk - 1) / kChunk;
+    const uint32_t buf_dw = Tile<R>::lds_dw(kChunk);
+    const R mt = RowsOf<R>::make(w, ws, cols);
+    const size_t wpitch = Tile<R>::wpitch(mt), spitch = Tile<R>::spitch(mt);
+    auto span = [&](uint32_t kc0) { return k1 - kc0 < kChunk ? k1 - kc0 : kChunk; };
+    auto stage = [&](uint32_t kc0, Staged<R, 1, kChunk>& st) {
+        const uint32_t kc = span(kc0);
+        slab_load(Tile<R>::wrow(mt, kc0), wpitch, r0, rows, Tile<R>::wdw(kc), st.w[0]);
+        if constexpr (Tile<R>::kScales) slab_load(Tile<R>::srow(mt, kc0), spitch, r0, rows, Tile<R>::sdw(kc), st.s[0]);
+    };
+    auto commit = [&](uint32_t kc0, uint32_t buf, const Staged<R, 1, kChunk>& st) {
+        const uint32_t kc = span(kc0);
+        uint32_t* base = tl + buf * buf_dw;
+        slab_store(base, Tile<R>::wdw(kc), st.w[0]);
+        if constexpr (Tile<R>::kScales) slab_store(base + kSlab * (Tile<R>::wdw(kc) + 1), Tile<R>::sdw(kc), st.s[0]);
+    };
+    Staged<R, 1, kChunk> st;
+    stage(k0, st);  // the first weights travel while x is split
+    {
+        // 32 threads per vector, 16 consecutive columns (two groups of 8) each
+        const uint32_t b = threadIdx.x >> 5, c = (threadIdx.x & 31) * 16;
+        const bool live = b < n_vec && k0 + c < k1;
+        float v[16];
+        float m = 0.0f;
+        bool finite = true;
+        if (live) {
+            const gptr<f32x4> src = as_global(reinterpret_cast<const f32x4*>(x + static_cast<size_t>(b) * cols + k0 + c));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 f = src[q];
+                v[4 * q] = f[0]; v[4 * q + 1] = f[1]; v[4 * q + 2] = f[2]; v[4 * q + 3] = f[3];
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                finite = finite && __builtin_isfinite(v[i]);
+                m = fmaxf(m, fabsf(v[i]));
+            }
+        }
+        if (!finite) m = __builtin_inff();
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));  // the vector's 32 threads
+        const int sh = split_shift(m);
+        if (live) {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                half8 vh, vl;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    const float xv = ldexpf(v[8 * g + kPerm[d]], sh);
+                    const _Float16 th = static_cast<_Float16>(xv);
+                    vh[d] = th;
+                    vl[d] = static_cast<_Float16>(xv - static_cast<float>(th));
+                }
+                *reinterpret_cast<half8*>(&xs[0][b][c + 8 * g]) = vh;
+                *reinterpret_cast<half8*>(&xs[1][b][c + 8 * g]) = vl;
+            }
+        }
+        if (b < 8 && (threadIdx.x & 31) == 0) xmul[b] = ldexpf(1.0f, -sh);
+    }
+    // A operand rows: vector lr / 2 (the last one repeated past n_vec), part lr & 1
+    const _Float16* xa_row = &xs[lane & 1][(lr >> 1) < n_vec ? (lr >> 1) : n_vec - 1][0];
+    commit(k0, 0, st);
+    __syncthreads();
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        const uint32_t kc0 = k0 + c * kChunk;
+        const uint32_t kc = span(kc0);
+        if (c + 1 < nchunks) stage(kc0 + kChunk, st);  // in flight during the products below
+        const uint32_t nb = kc / 32, per = (nb + 3) / 4;
+        const uint32_t b0 = wave * per < nb ? wave * per : nb, b1 = b0 + per < nb ? b0 + per : nb;
+        const uint32_t* base = tl + (c & 1) * buf_dw;
+        const uint8_t* wl = reinterpret_cast<const uint8_t*>(base + lr * (Tile<R>::wdw(kc) + 1));
+        const uint8_t* sl =
+            reinterpret_cast<const uint8_t*>(base + kSlab * (Tile<R>::wdw(kc) + 1) + lr * (Tile<R>::sdw(kc) + 1));
+#pragma unroll
+        for (int i = 0; i < kB; ++i) {
+            if (b0 + static_cast<uint32_t>(i) >= b1) break;
+            const uint32_t bb = b0 + static_cast<uint32_t>(i);
+            const half8 xa = *reinterpret_cast<const half8*>(xa_row + (kc0 - k0) + 32 * bb + 8 * kg);
+            float sc;
+            const half8 bw = Tile<R>::get(wl, sl, bb, kg, sc);
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bw, z, 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(sc, r[q], acc[q]);
+        }
+        if (c + 1 < nchunks) commit(kc0 + kChunk, (c + 1) & 1, st);
+        __syncthreads();
+    }
+    if (wave > 0) red[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int v = 0; v < 3; ++v) acc += red[v][lane];
+        // lane: row `row`, vectors 2kg + q (q = 0, 1) as (hi, lo) in 2q, 2q+1
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t j = 2 * kg + static_cast<uint32_t>(q);
+            if (j < n_vec && row < rows)
+                part[(static_cast<size_t>(blockIdx.y) * n_vec + j) * rows + row] = (acc[2 * q] + acc[2 * q + 1]) * xmul[j];
+        }
+    }
+}
+
+// y[b][r] = sum over ranges s (in order) of part[s][b][r].
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                          uint32_t rows, uint32_t n_vec, uint32_t n_ranges) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const size_t n = static_cast<size_t>(n_vec) * rows;
+    if (i >= n) return;
+    float s = part[i];
+    for (uint32_t r = 1; r < n_ranges; ++r) s += part[static_cast<size_t>(r) * n + i];
+    y[i] = s;
+}
+
 // out[t][r] = residual[t][r] + sum_j w[t][j] * part[t*k + j][r], slots in order, then
 // + shared_part[t][r] (the shared expert, weight 1, last); an out-of-table id makes
 // the element NaN (the id was reported by the grouping).
@@ -606,6 +757,62 @@ hipError_t launch_grouped(hipStream_t s, GroupWs gw, const _Float16* xh, const _
 }
 
 }  // namespace
+
+bool gemv_mfma_supported(int32_t format, uint64_t rows, uint64_t cols, uint64_t batch, const void* w,
+                         const float* x) {
+    if (batch < kGemvMfmaMinBatch || rows == 0 || rows > (1u << 24) || cols == 0 || cols > (1u << 20)) return false;
+    if (reinterpret_cast<uintptr_t>(w) % 4 || reinterpret_cast<uintptr_t>(x) % 16) return false;
+    if (format == OBJETA_HIP_FP4_E2M1) return cols % 128 == 0;  // the split layout
+    return format >= OBJETA_HIP_Q4_0 && format <= OBJETA_HIP_IQ3_0 && cols % 64 == 0;
+}
+
+namespace {
+template <class R>
+hipError_t launch_gemv_mfma_t(hipStream_t s, const void* w, const void* ws, const float* x, float* y, float* part,
+                              uint32_t rows, uint32_t cols, uint32_t nv, uint32_t ks) {
+    const uint32_t slabs = (rows + kSlab - 1) / kSlab;
+    const size_t lds = 2 * 4 * static_cast<size_t>(Tile<R>::lds_dw(kGemvChunk));
+    // one range: the partial sums are the result
+    hipLaunchKernelGGL((gemv_mfma_kernel<R>), dim3(slabs, ks), dim3(256), lds, s, w, ws, x, ks > 1 ? part : y, rows,
+                       cols, nv);
+    if (ks > 1) {
+        const size_t n = static_cast<size_t>(nv) * rows;
+        hipLaunchKernelGGL(gemv_reduce_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, part, y,
+                           rows, nv, ks);
+    }
+    return hipGetLastError();
+}
+}  // namespace
+
+int32_t launch_gemv_mfma(objeta_hip_context* ctx, hipStream_t s, int32_t format, const void* w, const void* ws,
+                         const float* x, float* y, uint64_t rows, uint64_t cols, uint64_t batch) {
+    const char* action = "launch batched GEMV (MFMA)";
+    if (!gemv_mfma_supported(format, rows, cols, batch, w, x))
+        OBJ_FAIL(kUnsupported, action, "shape, batch or alignment outside the MFMA GEMV");
+    const uint32_t R = static_cast<uint32_t>(rows), K = static_cast<uint32_t>(cols);
+    const uint32_t ks = (K + kGemvRange - 1) / kGemvRange;  // column ranges
+    const uint32_t nvmax = static_cast<uint32_t>(batch < 8 ? batch : 8);
+    float* part = nullptr;
+    if (ks > 1) {
+        void* wsp = nullptr;
+        OBJ_TRY(ensure_workspace(ctx, s, kWsGemv, 4ull * ks * nvmax * R, &wsp));
+        part = static_cast<float*>(wsp);
+    }
+    for (uint64_t done = 0; done < batch; done += 8) {
+        const uint32_t nv = static_cast<uint32_t>(batch - done < 8 ? batch - done : 8);
+        const float* xb = x + done * cols;
+        float* yb = y + done * rows;
+        hipError_t e;
+        switch (format) {
+            case OBJETA_HIP_Q4_0: e = launch_gemv_mfma_t<QRows<kQ4>>(s, w, nullptr, xb, yb, part, R, K, nv, ks); break;
+            case OBJETA_HIP_Q5_0: e = launch_gemv_mfma_t<QRows<kQ5>>(s, w, nullptr, xb, yb, part, R, K, nv, ks); break;
+            case OBJETA_HIP_IQ3_0: e = launch_gemv_mfma_t<QRows<kIQ3>>(s, w, nullptr, xb, yb, part, R, K, nv, ks); break;
+            default: e = launch_gemv_mfma_t<Fp4Rows>(s, w, ws, xb, yb, part, R, K, nv, ks); break;
+        }
+        if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+    }
+    return 0;
+}
 
 bool grouped_supported(int32_t format, uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden,
                        uint64_t inter, uint64_t out_dim) {

@@ -78,7 +78,8 @@ enum WsSlot : int {
     kWsGrouped = 3,
     kWsSelTab = 4,
     kWsOfficial = 5,  // dequantized FP8 activations of the official path
-    kWsSlots = 6
+    kWsGemv = 6,      // split activations and partial sums of the batched MFMA GEMV
+    kWsSlots = 7
 };
 
 // The scratch of one stream. Calls on different streams of a context may be in

@@ -81,6 +81,16 @@ int32_t bind_static_scratch(objeta_hip_context* ctx);
 int32_t moe_act_scratch(objeta_hip_context* ctx, hipStream_t s, uint64_t n_tokens, uint64_t k, uint64_t inter,
                         float** out);
 
+// Batched GEMV on the matrix cores (every weight decoded once for up to 8 vectors):
+// Q4_0 / Q5_0 / IQ3_0 (cols % 64 == 0) or the split FP4 layout (cols % 128 == 0),
+// weights 4-byte and x 16-byte aligned, from kGemvMfmaMinBatch vectors. Results
+// within the fp32 tolerance of the per-vector kernels (activations split into two
+// fp16 parts, 22 significant bits).
+constexpr uint64_t kGemvMfmaMinBatch = 5;
+bool gemv_mfma_supported(int32_t format, uint64_t rows, uint64_t cols, uint64_t batch, const void* w,
+                         const float* x);
+int32_t launch_gemv_mfma(objeta_hip_context* ctx, hipStream_t s, int32_t format, const void* w, const void* ws,
+                         const float* x, float* y, uint64_t rows, uint64_t cols, uint64_t batch);
 // Batches from this many tokens run the grouped-token products in the layer entry
 // points (measured on MI355X at hidden 2048, 128 experts, top-8: per-assignment
 // faster at 8 tokens, grouped at 16 and beyond).

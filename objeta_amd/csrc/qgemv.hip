@@ -183,6 +183,9 @@ int32_t launch_qgemv(objeta_hip_context* ctx, int32_t format, hipStream_t s, con
     if (!d_q || !d_x || !d_y) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     if (rows > 0x7FFFFFFFull || cols > 0x7FFFFFFFull)
         OBJ_FAIL(kInvalidInput, action, "rows/cols exceed 2^31");
+    // several vectors: each weight decoded once for all of them, on the matrix cores
+    if (format != OBJETA_HIP_FP4_E2M1 && gemv_mfma_supported(format, rows, cols, batch, d_q, d_x))
+        return launch_gemv_mfma(ctx, s, format, d_q, nullptr, d_x, d_y, rows, cols, batch);
     const uint32_t r = static_cast<uint32_t>(rows), c = static_cast<uint32_t>(cols);
     const uint8_t* q = static_cast<const uint8_t*>(d_q);
     const bool aligned = (reinterpret_cast<uintptr_t>(q) % 4 == 0) && (reinterpret_cast<uintptr_t>(d_x) % 16 == 0);
@@ -240,6 +243,9 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
     if (rows == 0 || batch == 0) return 0;
     if (!d_w || !d_s || !d_x || !d_y) OBJ_FAIL(kInvalidInput, action, "NULL device pointer");
     if (rows > 0x7FFFFFFFull || cols > 0x7FFFFFFFull) OBJ_FAIL(kInvalidInput, action, "rows/cols exceed 2^31");
+    if (reinterpret_cast<uintptr_t>(d_s) % 4 == 0 &&
+        gemv_mfma_supported(OBJETA_HIP_FP4_E2M1, rows, cols, batch, d_w, d_x))
+        return launch_gemv_mfma(ctx, s, OBJETA_HIP_FP4_E2M1, d_w, d_s, d_x, d_y, rows, cols, batch);
     const uint32_t r = static_cast<uint32_t>(rows), c = static_cast<uint32_t>(cols);
     const uint8_t* w = static_cast<const uint8_t*>(d_w);
     const uint8_t* sc = static_cast<const uint8_t*>(d_s);

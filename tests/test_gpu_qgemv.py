@@ -199,3 +199,60 @@ def test_gemv_full_size_linearity(backend, quant, fmt):
     qall = dq.download(np.uint8, rows * rb).reshape(rows, rb)
     ref = orc.gemv(int(fmt), qall[sample].ravel(), x1, len(sample), cols)
     assert float(np.max(np.abs(y[0][sample] - ref))) <= 1e-4 * float(np.max(np.abs(ref)))
+
+
+# ---------------------------------------------------- batched GEMV on the matrix cores
+@pytest.mark.parametrize("fmt", FORMATS[:3])
+@pytest.mark.parametrize("rows,cols,batch", [(200, 704, 6), (37, 1536, 9), (1000, 64, 5)])
+def test_gemv_batched_mfma_column_ranges(backend, quant, fmt, rows, cols, batch):
+    """From five vectors the batched GEMV runs on MFMA, each workgroup over a range of
+    512 columns (the last one partial here) whose partial sums are added in range
+    order; every vector is checked against the oracle with the tight bound."""
+    m = orc.gauss(rows * cols, 40 + rows, 0.02)
+    q = orc.quantize_matrix(int(fmt), m, rows, cols)
+    xs = orc.gauss(batch * cols, 41 + cols, 1.0)
+    dy = backend.alloc(batch * rows * 4)
+    quant.launch_kernel(fmt, None, backend.to_device(q), backend.to_device(xs), dy, QGemvShape.new(fmt, rows, cols),
+                        batch=batch)
+    y = dy.download(np.float32, batch * rows).reshape(batch, rows)
+    for t in range(batch):
+        xt = xs[t * cols:(t + 1) * cols]
+        _assert_close(y[t], orc.gemv(int(fmt), q, xt, rows, cols), q, xt, fmt, rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(100, 640, 5), (48, 1024, 8)])
+def test_fp4_split_gemv_batched_mfma(backend, quant, rows, cols, batch):
+    rng = np.random.default_rng(rows * cols)
+    w = rng.integers(0, 256, size=rows * cols // 2, dtype=np.uint8)
+    s = rng.integers(112, 132, size=rows * cols // 32, dtype=np.uint8)
+    xs = orc.gauss(batch * cols, 6, 1.0)
+    dy = backend.alloc(batch * rows * 4)
+    quant.launch_kernel_split_fp4(None, backend.to_device(w), backend.to_device(s), backend.to_device(xs), dy, rows,
+                                  cols, batch=batch)
+    y = dy.download(np.float32, batch * rows).reshape(batch, rows)
+    for t in range(batch):
+        ref = orc.fp4_split_gemv(w, s, xs[t * cols:(t + 1) * cols], rows, cols)
+        assert float(np.max(np.abs(y[t] - ref))) <= 1e-4 * float(np.max(np.abs(ref)))
+
+
+def test_gemv_batched_mfma_non_finite_scales(backend, quant):
+    """Rows with an inf or NaN block scale give non-finite outputs on the MFMA path as
+    in the reference (not necessarily the same special value: the block sum is
+    scaled once); the other rows stay within the bar."""
+    fmt, rows, cols, batch = QuantFormat.Q4_0, 64, 1024, 8
+    q = orc.quantize_matrix(0, orc.gauss(rows * cols, 7, 0.02), rows, cols).reshape(rows, cols // 32, 18).copy()
+    q[5, 3, :2] = np.array([0x7C00], np.uint16).view(np.uint8)   # +inf scale
+    q[17, 30, :2] = np.array([0x7E00], np.uint16).view(np.uint8)  # NaN scale
+    q = q.ravel()
+    xs = orc.gauss(batch * cols, 8, 1.0)
+    dy = backend.alloc(batch * rows * 4)
+    quant.launch_kernel(fmt, None, backend.to_device(q), backend.to_device(xs), dy, QGemvShape.new(fmt, rows, cols),
+                        batch=batch)
+    y = dy.download(np.float32, batch * rows).reshape(batch, rows)
+    for t in range(batch):
+        ref = orc.gemv(0, q, xs[t * cols:(t + 1) * cols], rows, cols)
+        bad = ~np.isfinite(ref)
+        assert bad[5] and bad[17]
+        assert np.array_equal(~np.isfinite(y[t]), bad)
+        scale = float(np.max(np.abs(ref[~bad])))
+        assert float(np.max(np.abs(y[t][~bad] - ref[~bad]))) <= 1e-4 * scale
