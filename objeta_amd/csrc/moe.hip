@@ -181,8 +181,15 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(
     uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ sel, uint32_t kk,
     const objeta_hip_expert_ptrs* __restrict__ shared) {
     extern __shared__ float lds[];
-    const uint32_t t = blockIdx.x / blocks_per_token;
-    const uint32_t rb = blockIdx.x - t * blocks_per_token;
+    // The dispatcher hands consecutive workgroups to the eight XCDs in turn, so the
+    // workgroups b with one b % 8 share an XCD (and its L2). They take contiguous
+    // (token, row block) ranges: a 128-byte line shared by neighbouring row blocks
+    // (rows of inter/32 blocks need not end on a line) is then fetched once, not
+    // once per XCD.
+    const uint32_t nb = gridDim.x, xq = nb >> 3, xr = nb & 7, xc = blockIdx.x & 7;
+    const uint32_t g = xc * xq + (xc < xr ? xc : xr) + (blockIdx.x >> 3);
+    const uint32_t t = g / blocks_per_token;
+    const uint32_t rb = g - t * blocks_per_token;
     const uint32_t pairs = inter >> 6;
     // wave-uniform, so the expert id and table entry come through scalar loads,
     // which do not wait behind the vector loads of the activations
