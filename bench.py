@@ -22,6 +22,8 @@ Also measured in the same run (each in its own object of the JSON line):
   [14336 x 4096], batch 1 and 8, each over a >= 4 GB rotated working set;
 - deepseek: one H 7168 / 256 routed + 1 shared / top-8 / I 2048 FP4 layer at
   batch 1 and 32;
+- official: the same routed experts through the FP8-activation ("official
+  arithmetic") layer with an FP8 shared expert, batch 1 and 32;
 - misses: the headline stack through the host-in/host-out executor with the expert
   cache at 25% of the expert bytes, experts in pinned host memory: end-to-end
   us/token including the PCIe copies of the misses, and the copies' GB/s;
@@ -55,7 +57,7 @@ from objeta_amd.workloads import zipf_bias  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 ROTATE_BYTES = 4 << 30  # working set of the rotated GEMV measurements (>> 256 MB MALL)
-SECTIONS = ("headline", "kernels", "batch", "gemv", "deepseek", "misses", "cpu")
+SECTIONS = ("headline", "kernels", "batch", "gemv", "deepseek", "official", "misses", "cpu")
 # not in the default run: kernels of known traffic for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE
 EXTRA_SECTIONS = ("calibrate",)
 TRAFFIC_PROFILE = "profiles/moe_layer_q4_qwen3a3b_hbm_traffic.md"
@@ -515,6 +517,75 @@ def run_deepseek(env: Env, args, seed):
     return res
 
 
+# ------------------------------------------- DeepSeek official arithmetic (FP8)
+def run_official(env: Env, args, seed):
+    """The FP8-activation ("official arithmetic") layer at the DeepSeek shape: router,
+    then objeta_hip_moe_official_fp4_device (act_quant of x, FP4 routed gate/up with the
+    official SwiGLU, the FP8 shared expert, act_quant of the intermediates, FP4 routed
+    down, shared down), replayed from a hipGraph at batch 1 and 32."""
+    from objeta_amd import ExpertTable
+    from objeta_amd.workloads import fp8_random_expert
+    be = env.be
+    H, I, E, K = 7168, 2048, 256, 8
+    w_b, s_b = I * H // 2, I * H // 32
+    dw_b, ds_b = H * I // 2, H * I // 32
+    eb = 2 * (w_b + s_b) + dw_b + ds_b
+    arena = be.alloc(E * eb)
+    entries = []
+    for e in range(E):
+        base = arena.ptr + e * eb
+        gw, gs = base, base + w_b
+        uw, us = gs + s_b, gs + s_b + w_b
+        dw, ds = us + s_b, us + s_b + dw_b
+        for j, (wp, sp, r, c) in enumerate(((gw, gs, I, H), (uw, us, I, H), (dw, ds, H, I))):
+            env.check(env.lib.objeta_hip_fill_fp4_split_device(env.ctx, None, C.c_void_p(wp), C.c_void_p(sp), r, c,
+                                                               seed + 3 * e + j))
+        entries.append((gw, uw, dw, gs, us, ds))
+    table = ExpertTable(be, entries)
+    sh = [be.to_device(a) for a in fp8_random_expert(H, I, H, seed + 7)]
+    shared = ExpertTable(be, [(sh[0].addr(), sh[2].addr(), sh[4].addr(), sh[1].addr(), sh[3].addr(), sh[5].addr())])
+    shared_bytes = sum(int(a.nbytes) for a in sh)
+    w_r = be.alloc(4 * E * H)
+    env.fill_gauss(w_r.ptr, E * H, seed + 5, 0.02)
+    res = {"hidden": H, "intermediate": I, "experts": E, "top_k": K, "routed_format": "DeepSeekFp4E2M1",
+           "shared_format": "F8_E4M3, E8M0 128x128 tiles", "routed_expert_bytes": eb, "shared_expert_bytes": shared_bytes,
+           "path": "router, then objeta_hip_moe_official_fp4_device (FP8 activations), replayed from a hipGraph"}
+    for T in (1, 32):
+        P = 8
+        xs = be.alloc(4 * P * T * H)
+        env.fill_gauss(xs.ptr, P * T * H, seed + 10 + T, 1.0)
+        out = be.alloc(4 * T * H)
+        ids = be.alloc(4 * T * K)
+        wts = be.alloc(4 * T * K)
+
+        def enq(p, T=T, xs=xs, out=out, ids=ids, wts=wts):
+            x = xs.addr(4 * p * T * H)
+            env.check(env.lib.objeta_hip_router_topk_device(env.ctx, env.stream, w_r.addr(), None, x, T, E, H, K, 1,
+                                                            ids.addr(), wts.addr()))
+            env.moe.official_fp4_device(table, ids, wts, T, K, x, out, H, I, H, 10.0, stream=env.stream,
+                                        shared_fp8=shared)
+        enq(0)
+        be.synchronize(env.stream)
+        graphs = [env.capture(lambda p=p: enq(p)) for p in range(P)]
+        for i in range(5):
+            env.launch(graphs[i % P])
+        be.synchronize(env.stream)
+        _, per = env.per_step(lambda i: env.launch(graphs[i % P]), max(20, args.steps // 4))
+        s = stats(per)
+        sel = ids.download(np.uint32, T * K)
+        distinct = len(set(int(v) for v in sel))
+        ebytes = distinct * eb + shared_bytes
+        res[f"batch{T}"] = {"us_per_layer": rnd(s), "us_per_token": round(s["avg"] / T, 3),
+                            "expert_bytes_read": ebytes, "distinct_routed_experts": distinct,
+                            "expert_hbm_gbps": round(ebytes / (s["avg"] * 1e-6) / 1e9, 1),
+                            "expert_hbm_frac_of_peak": round(ebytes / (s["avg"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+        env.destroy(graphs)
+        for b in (xs, out, ids, wts):
+            b.free()
+    arena.free()
+    return res
+
+
 # ------------------------------------------------------------- cache misses
 def run_misses(env: Env, st: QwenStack, args, xs, P, report):
     """The stack through the host-in/host-out executor with the expert cache at 25% of
@@ -847,6 +918,10 @@ def main() -> int:
     if "deepseek" in sections:
         stage("deepseek")
         deepseek = run_deepseek(env, args, args.seed + 5000)
+    official = None
+    if "official" in sections:
+        stage("official")
+        official = run_official(env, args, args.seed + 6000)
     report = {} if args.report_dir else None
     misses = None
     if "misses" in sections:
@@ -901,6 +976,7 @@ def main() -> int:
         "batch": batch,
         "gemv": gemv,
         "deepseek": deepseek,
+        "official": official,
         "misses": misses,
         "cpu_baseline": cpu,
         "device": {"name": dev["name"], "arch": dev["arch"], "compute_units": dev["compute_units"]},

@@ -41,6 +41,8 @@
 #include "gemv_stream.hpp"
 #include "host_common.hpp"
 #include "kernels.hpp"
+#include "quant_rules.hpp"
+#include "swiglu.hpp"
 
 namespace objeta {
 namespace {
@@ -85,11 +87,13 @@ __device__ __forceinline__ int split_shift(float m) {
 
 // ------------------------------------------------------------------ grouping
 // The shared expert (when given) follows as one more group: member t is token t,
-// its act row n_assign + t.
+// its act row n_assign + t. Its member sets go after the routed ones in w, or, when
+// wsh.hdr is set (a shared expert of another format, multiplied by a launch of its
+// own), into wsh.
 __device__ void group_assignments(const uint32_t* __restrict__ ids, uint32_t n_assign, uint32_t n_table,
                                   const objeta_hip_expert_ptrs* __restrict__ table,
                                   const objeta_hip_expert_ptrs* __restrict__ shared, uint32_t n_tokens, GroupWs w,
-                                  uint32_t* __restrict__ err) {
+                                  GroupWs wsh, uint32_t* __restrict__ err) {
     __shared__ uint32_t cnt[kGMaxTable];
     __shared__ uint32_t pos[kGMaxTable];
     __shared__ uint32_t sid[kGMaxAssign];
@@ -156,9 +160,14 @@ __device__ void group_assignments(const uint32_t* __restrict__ ids, uint32_t n_a
         }
     }
     const uint32_t n_sh = shared ? (n_tokens + 7) / 8 : 0;
+    const bool apart = wsh.hdr != nullptr;
     if (tid == 0) {
-        w.hdr[0] = tg + (shared ? 1 : 0);
-        w.hdr[1] = ts + n_sh;
+        w.hdr[0] = tg + (shared && !apart ? 1 : 0);
+        w.hdr[1] = ts + (apart ? 0 : n_sh);
+        if (apart) {
+            wsh.hdr[0] = shared ? 1 : 0;
+            wsh.hdr[1] = n_sh;
+        }
     }
     __syncthreads();
     // stable order inside a group: rank among the earlier assignments of the expert
@@ -195,8 +204,9 @@ __device__ void group_assignments(const uint32_t* __restrict__ ids, uint32_t n_a
         mem.y = row(2) | (row(3) << 16);
         mem.z = row(4) | (row(5) << 16);
         mem.w = row(6) | (row(7) << 16);
-        w.sets[si].p = *src;
-        *reinterpret_cast<uint4*>(w.sets[si].mem) = mem;
+        SetRec* dst = si >= ts && apart ? &wsh.sets[si - ts] : &w.sets[si];
+        dst->p = *src;
+        *reinterpret_cast<uint4*>(dst->mem) = mem;
     }
 }
 
@@ -247,11 +257,11 @@ __global__ __launch_bounds__(256) void moe_prepare_kernel(const uint32_t* __rest
                                                           uint32_t n_table,
                                                           const objeta_hip_expert_ptrs* __restrict__ table,
                                                           const objeta_hip_expert_ptrs* __restrict__ shared,
-                                                          uint32_t n_tokens, GroupWs w,
+                                                          uint32_t n_tokens, GroupWs w, GroupWs wsh,
                                                           uint32_t* __restrict__ err, const float* __restrict__ x,
                                                           uint32_t cols, _Float16* __restrict__ xh,
                                                           _Float16* __restrict__ xl, float* __restrict__ xmult) {
-    if (blockIdx.x == 0) group_assignments(ids, n_assign, n_table, table, shared, n_tokens, w, err);
+    if (blockIdx.x == 0) group_assignments(ids, n_assign, n_table, table, shared, n_tokens, w, wsh, err);
     else split_row(x, cols, xh, xl, xmult, blockIdx.x - 1);
 }
 
@@ -312,7 +322,7 @@ __device__ __forceinline__ half8 iq3_to_b(uint32_t lo16, uint32_t h8) {
 
 // ----------------------------------------------------------- grouped GEMMs
 // A workgroup streams a 16-row slab of one group's expert (gate and up together,
-// or down) through LDS in chunks of kChunkOf columns, double-buffered: while its
+// or down) through LDS in chunks of Tile<R>::kChunkGU / kChunkDn columns, double-buffered: while its
 // four waves multiply chunk c (wave w: the w-th quarter of the chunk's blocks), the
 // loads of chunk c+1 (every thread's share, 64-byte runs within rows) and the next
 // activation operands are already in flight. Each lane takes its MFMA operand (8
@@ -320,15 +330,16 @@ __device__ __forceinline__ half8 iq3_to_b(uint32_t lo16, uint32_t h8) {
 // sums meet in LDS at the end. 8 group members per MFMA column set; the member
 // sets of all groups are separate work items (a larger group's sets stream the slab
 // in parallel workgroups).
-// columns per staged chunk: 16 blocks for gate and up together, 8 for down (the
-// widths that measured fastest; narrower chunks keep more workgroups resident)
-template <bool GATEUP>
-constexpr uint32_t kChunkOf = GATEUP ? 512 : 256;
 constexpr uint32_t kSlab = 16;      // rows per workgroup (one MFMA tile)
 
-// Staged row segments of a 64-row slab: weights (and, for the split FP4 layout,
+// Staged row segments of a 16-row slab: weights (and, for the split FP4 layout,
 // the E8M0 scales) of columns [c0, c0 + kc), row stride padded by one dword so the
-// lanes of different rows read different banks.
+// lanes of different rows read different banks. kChunkGU / kChunkDn: columns per
+// staged chunk for gate and up together / for down (16 and 8 blocks of 32 for the
+// 4-bit layouts, the widths that measured fastest: narrower chunks keep more
+// workgroups resident; 8 blocks of FP8 bytes fill the same LDS). kTileScale: one
+// E8M0 byte per 128 x 128 tile (FP8), taken per chunk into a register by
+// tile_scales instead of being staged per row.
 template <class R>
 struct Tile;
 
@@ -336,6 +347,8 @@ template <int F>
 struct Tile<QRows<F>> {
     static constexpr int kBB = Fmt<F>::kBlockBytes;
     static constexpr bool kScales = false;
+    static constexpr bool kTileScale = false;
+    static constexpr uint32_t kChunkGU = 512, kChunkDn = 256;
     static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 32 * kBB / 4; }  // dwords per row segment
     static constexpr __host__ __device__ uint32_t sdw(uint32_t) { return 0; }
     static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) { return kSlab * (wdw(kc) + 1); }
@@ -345,8 +358,9 @@ struct Tile<QRows<F>> {
         return m.q + static_cast<size_t>(c0 / 32) * kBB;
     }
     static __device__ __forceinline__ const uint8_t* srow(const QRows<F>&, uint32_t) { return nullptr; }
+    static __device__ __forceinline__ uint32_t tile_scales(const QRows<F>&, uint32_t, uint32_t, uint32_t) { return 0; }
     // block b of a row (LDS row base `w`), k group kg: 8 weights and the scale
-    static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t*, uint32_t b, uint32_t kg,
+    static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t*, uint32_t, uint32_t b, uint32_t kg,
                                                 float& scale) {
         const uint8_t* blk = w + b * kBB;
         auto u16 = [&](uint32_t o) { return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(blk + o)); };
@@ -364,6 +378,8 @@ struct Tile<QRows<F>> {
 template <>
 struct Tile<Fp4Rows> {
     static constexpr bool kScales = true;
+    static constexpr bool kTileScale = false;
+    static constexpr uint32_t kChunkGU = 512, kChunkDn = 256;
     static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 8; }   // kc / 2 bytes
     static constexpr __host__ __device__ uint32_t sdw(uint32_t kc) { return kc / 128; }  // kc / 32 bytes (kc % 128 == 0)
     static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) {
@@ -373,7 +389,8 @@ struct Tile<Fp4Rows> {
     static __device__ __forceinline__ size_t spitch(const Fp4Rows& m) { return m.srow; }
     static __device__ __forceinline__ const uint8_t* wrow(const Fp4Rows& m, uint32_t c0) { return m.w + c0 / 2; }
     static __device__ __forceinline__ const uint8_t* srow(const Fp4Rows& m, uint32_t c0) { return m.s + c0 / 32; }
-    static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t* sc, uint32_t b, uint32_t kg,
+    static __device__ __forceinline__ uint32_t tile_scales(const Fp4Rows&, uint32_t, uint32_t, uint32_t) { return 0; }
+    static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t* sc, uint32_t, uint32_t b, uint32_t kg,
                                                 float& scale) {
         scale = e8m0_to_f32(sc[b]) * 16384.0f;
         const uint32_t n = *reinterpret_cast<const uint32_t*>(w + 16 * b + 4 * kg);
@@ -384,6 +401,49 @@ struct Tile<Fp4Rows> {
             p[i] = as_h2(((t & 0x00070007u) << 9) | ((t & 0x00080008u) << 12));
         }
         return pack8(p[0], p[1], p[2], p[3]);
+    }
+};
+
+// FP8 E4M3 rows ([rows][cols] bytes) with an E8M0 byte per 128 x 128 tile. A code
+// decodes by the reference's rule (rules::f8e4m3_to_f32: exponent field 0 as
+// mant * 2^-5, 15 as +-448), and every such value (|v| in [2^-5, 448] or 0) is an
+// exact fp16. A 16-row slab lies inside one 128-row tile, so the chunk's scales are
+// one byte per 128 columns for all of its rows.
+template <>
+struct Tile<Fp8Rows> {
+    static constexpr bool kScales = false;
+    static constexpr bool kTileScale = true;
+    static constexpr uint32_t kChunkGU = 256, kChunkDn = 256;
+    static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 4; }  // kc bytes
+    static constexpr __host__ __device__ uint32_t sdw(uint32_t) { return 0; }
+    static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) { return kSlab * (wdw(kc) + 1); }
+    static __device__ __forceinline__ size_t wpitch(const Fp8Rows& m) { return m.wrow; }
+    static __device__ __forceinline__ size_t spitch(const Fp8Rows&) { return 0; }
+    static __device__ __forceinline__ const uint8_t* wrow(const Fp8Rows& m, uint32_t c0) { return m.w + c0; }
+    static __device__ __forceinline__ const uint8_t* srow(const Fp8Rows&, uint32_t) { return nullptr; }
+    // the scale bytes of the tiles under columns [c0, c0 + kc) (kc <= 512) of row r0's
+    // tile row, byte i for columns [c0 + 128 i, c0 + 128 i + 128); c0 % 128 == 0
+    static __device__ __forceinline__ uint32_t tile_scales(const Fp8Rows& m, uint32_t r0, uint32_t c0, uint32_t kc) {
+        const gptr<uint8_t> s = as_global(m.s + static_cast<size_t>(r0 >> 7) * m.scols + (c0 >> 7));
+        const uint32_t n = (kc + 127) >> 7;
+        uint32_t v = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i)
+            if (i < n) v |= static_cast<uint32_t>(s[i]) << (8 * i);
+        return v;
+    }
+    static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t*, uint32_t ts, uint32_t b, uint32_t kg,
+                                                float& scale) {
+        scale = e8m0_to_f32((ts >> (8 * (b >> 2))) & 0xFFu);
+        const uint32_t d0 = *reinterpret_cast<const uint32_t*>(w + 32 * b + 8 * kg);
+        const uint32_t d1 = *reinterpret_cast<const uint32_t*>(w + 32 * b + 8 * kg + 4);
+        half8 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // (w_i, w_{i+4}): the order of the split activations
+            h[2 * i] = static_cast<_Float16>(rules::f8e4m3_to_f32((d0 >> (8 * i)) & 0xFFu));
+            h[2 * i + 1] = static_cast<_Float16>(rules::f8e4m3_to_f32((d1 >> (8 * i)) & 0xFFu));
+        }
+        return h;
     }
 };
 
@@ -421,24 +481,25 @@ struct Staged {
     static constexpr int kUnits = (Tile<R>::wdw(CH) + 15) / 16;
     uint32_t w[M][kUnits];
     uint32_t s[M][1];  // FP4 scales: CH / 128 <= 16 dwords per row
+    uint32_t ts[M];    // FP8 tile scales of the chunk
 };
 
 // grid = (ceil(rows / 16), gy), 256 threads; workgroup (x, y) takes member sets y,
 // y + gy, ... (the number of sets is known only on the device). GATEUP: rows = inter
-// over the split x rows (cols = hidden), writes act; else rows = out_dim over the
-// split act rows (cols = inter), writes part. Dynamic LDS: two chunk buffers of
-// every matrix.
+// over the split x rows (cols = hidden), writes act (the official SwiGLU when
+// `official` is set); else rows = out_dim over the split act rows (cols = inter),
+// writes part. Dynamic LDS: two chunk buffers of every matrix.
 template <class R, bool GATEUP>
 __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Float16* __restrict__ vh,
                                                           const _Float16* __restrict__ vl,
                                                           const float* __restrict__ vmult, float* __restrict__ out,
                                                           uint32_t cols, uint32_t rows, uint32_t k, uint32_t n_assign,
-                                                          float limit) {
+                                                          float limit, uint32_t official) {
     extern __shared__ uint32_t tl[];
     // the cross-wave partial sums reuse the chunk buffers once a set's products are done
     auto red = reinterpret_cast<f32x4 (*)[3][64]>(tl);
     constexpr int kMats = GATEUP ? 2 : 1;
-    constexpr uint32_t kChunk = kChunkOf<GATEUP>;
+    constexpr uint32_t kChunk = GATEUP ? Tile<R>::kChunkGU : Tile<R>::kChunkDn;
     constexpr int kB = kChunk / 32 / 4;  // blocks per wave and chunk
     const uint32_t n_sets = gw.hdr[1];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -472,8 +533,10 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
                 slab_load(Tile<R>::wrow(mt[t], kc0), wpitch, r0, rows, Tile<R>::wdw(kc), st.w[t]);
                 if constexpr (Tile<R>::kScales)
                     slab_load(Tile<R>::srow(mt[t], kc0), spitch, r0, rows, Tile<R>::sdw(kc), st.s[t]);
+                if constexpr (Tile<R>::kTileScale) st.ts[t] = Tile<R>::tile_scales(mt[t], r0, kc0, kc);
             }
         };
+        uint32_t ts_cur[kMats];  // the tile scales of the chunk being multiplied
         auto operands = [&](uint32_t kc0, half8 (&xr)[kB]) {
             const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
             const uint32_t nb = kc / 32, per = (nb + 3) / 4;
@@ -493,6 +556,7 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
                 slab_store(base, Tile<R>::wdw(kc), st.w[t]);
                 if constexpr (Tile<R>::kScales)
                     slab_store(base + kSlab * (Tile<R>::wdw(kc) + 1), Tile<R>::sdw(kc), st.s[t]);
+                ts_cur[t] = st.ts[t];  // read only after the products of the previous chunk
             }
         };
         f32x4 acc[kMats];
@@ -520,7 +584,7 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
                 for (int i = 0; i < kB; ++i) {
                     if (b0 + static_cast<uint32_t>(i) >= b1) break;
                     float sc;
-                    const half8 bw = Tile<R>::get(wl, sl, b0 + static_cast<uint32_t>(i), kg, sc);
+                    const half8 bw = Tile<R>::get(wl, sl, ts_cur[t], b0 + static_cast<uint32_t>(i), kg, sc);
                     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
                     const f32x4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[i], bw, z, 0, 0, 0);
 #pragma unroll
@@ -557,12 +621,7 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
                 const float v0 = (acc[0][2 * q] + acc[0][2 * q + 1]) * mul;
                 if constexpr (GATEUP) {
                     const float v1 = (acc[kMats - 1][2 * q] + acc[kMats - 1][2 * q + 1]) * mul;
-                    float gv = v0, uv = v1;
-                    if (limit > 0.0f) {
-                        uv = fminf(limit, fmaxf(-limit, uv));
-                        gv = fminf(limit, gv);
-                    }
-                    if (live) out[static_cast<size_t>(a) * rows + row] = (gv / (1.0f + expf(-gv))) * uv;
+                    if (live) out[static_cast<size_t>(a) * rows + row] = swiglu(v0, v1, limit, official);
                 } else {
                     if (live) out[static_cast<size_t>(a) * rows + row] = v0;
                 }
@@ -607,12 +666,15 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const void* __restrict__
         const uint32_t kc = span(kc0);
         slab_load(Tile<R>::wrow(mt, kc0), wpitch, r0, rows, Tile<R>::wdw(kc), st.w[0]);
         if constexpr (Tile<R>::kScales) slab_load(Tile<R>::srow(mt, kc0), spitch, r0, rows, Tile<R>::sdw(kc), st.s[0]);
+        if constexpr (Tile<R>::kTileScale) st.ts[0] = Tile<R>::tile_scales(mt, r0, kc0, kc);
     };
+    uint32_t ts_cur = 0;  // the tile scales of the chunk being multiplied
     auto commit = [&](uint32_t kc0, uint32_t buf, const Staged<R, 1, kChunk>& st) {
         const uint32_t kc = span(kc0);
         uint32_t* base = tl + buf * buf_dw;
         slab_store(base, Tile<R>::wdw(kc), st.w[0]);
         if constexpr (Tile<R>::kScales) slab_store(base + kSlab * (Tile<R>::wdw(kc) + 1), Tile<R>::sdw(kc), st.s[0]);
+        ts_cur = st.ts[0];
     };
     Staged<R, 1, kChunk> st;
     stage(k0, st);  // the first weights travel while x is split
@@ -678,7 +740,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const void* __restrict__
             const uint32_t bb = b0 + static_cast<uint32_t>(i);
             const half8 xa = *reinterpret_cast<const half8*>(xa_row + (kc0 - k0) + 32 * bb + 8 * kg);
             float sc;
-            const half8 bw = Tile<R>::get(wl, sl, bb, kg, sc);
+            const half8 bw = Tile<R>::get(wl, sl, ts_cur, bb, kg, sc);
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
             const f32x4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bw, z, 0, 0, 0);
 #pragma unroll
@@ -735,24 +797,35 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint32_t* __rest
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// about sixteen workgroups per CU over all slabs, at most one per member set
+uint32_t grouped_gy(uint32_t rows, uint32_t max_sets, uint32_t cus) {
+    const uint32_t slabs = (rows + kSlab - 1) / kSlab;
+    const uint32_t want = (16 * cus + slabs - 1) / slabs;
+    return want < 1 ? 1u : (want > max_sets ? max_sets : want);
+}
+
+// One grouped product launch: GATEUP over the split x rows (hidden columns) into
+// act, else over the split act rows (inter columns) into part.
+template <class R, bool GATEUP>
+void launch_grouped_products(hipStream_t s, GroupWs gw, const _Float16* vh, const _Float16* vl, const float* vmult,
+                             float* dst, uint32_t cols, uint32_t rows, uint32_t k, uint32_t n_assign, float limit,
+                             bool official, uint32_t max_sets, uint32_t cus) {
+    const size_t lds = (GATEUP ? 2 : 1) * 2 * 4 *
+                       static_cast<size_t>(Tile<R>::lds_dw(GATEUP ? Tile<R>::kChunkGU : Tile<R>::kChunkDn));
+    hipLaunchKernelGGL((moe_grouped_kernel<R, GATEUP>), dim3((rows + kSlab - 1) / kSlab, grouped_gy(rows, max_sets, cus)),
+                       dim3(256), lds, s, gw, vh, vl, vmult, dst, cols, rows, k, n_assign, limit, official ? 1u : 0u);
+}
+
 template <class R>
 hipError_t launch_grouped(hipStream_t s, GroupWs gw, const _Float16* xh, const _Float16* xl, const float* xmult,
                           float* act, _Float16* ah, _Float16* al, float* amult, float* part, uint32_t n_assign,
                           uint32_t n_rows, uint32_t max_sets, uint32_t k,
                           uint32_t hidden, uint32_t inter, uint32_t out_dim, float limit, uint32_t cus) {
-    // about sixteen workgroups per CU over all slabs, at most one per member set
-    auto gy = [&](uint32_t rows) {
-        const uint32_t slabs = (rows + kSlab - 1) / kSlab;
-        const uint32_t want = (16 * cus + slabs - 1) / slabs;
-        return want < 1 ? 1u : (want > max_sets ? max_sets : want);
-    };
-    const size_t lds_gu = 2 * 2 * 4 * static_cast<size_t>(Tile<R>::lds_dw(kChunkOf<true>));
-    const size_t lds_dn = 2 * 4 * static_cast<size_t>(Tile<R>::lds_dw(kChunkOf<false>));
-    hipLaunchKernelGGL((moe_grouped_kernel<R, true>), dim3((inter + kSlab - 1) / kSlab, gy(inter)), dim3(256), lds_gu,
-                       s, gw, xh, xl, xmult, act, hidden, inter, k, n_assign, limit);
+    launch_grouped_products<R, true>(s, gw, xh, xl, xmult, act, hidden, inter, k, n_assign, limit, false, max_sets,
+                                     cus);
     hipLaunchKernelGGL(moe_split_kernel, dim3(n_rows), dim3(256), 0, s, act, inter, ah, al, amult);
-    hipLaunchKernelGGL((moe_grouped_kernel<R, false>), dim3((out_dim + kSlab - 1) / kSlab, gy(out_dim)), dim3(256),
-                       lds_dn, s, gw, ah, al, amult, part, inter, out_dim, k, n_assign, 0.0f);
+    launch_grouped_products<R, false>(s, gw, ah, al, amult, part, inter, out_dim, k, n_assign, 0.0f, false, max_sets,
+                                      cus);
     return hipGetLastError();
 }
 
@@ -875,7 +948,7 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
     uint32_t* err = ctx->err_word;
     const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
     hipLaunchKernelGGL(moe_prepare_kernel, dim3(1 + T), dim3(256), 0, s, ids, A, static_cast<uint32_t>(n_table), table,
-                       shared, T, gw, err, x, H, xh, xl, xmult);
+                       shared, T, gw, GroupWs{nullptr, nullptr}, err, x, H, xh, xl, xmult);
     hipError_t e;
     const uint32_t kk = static_cast<uint32_t>(k);
     switch (format) {
@@ -903,6 +976,90 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
         e = hipGetLastError();
     }
     if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+    return 0;
+}
+
+bool official_grouped_supported(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden, uint64_t inter,
+                                uint64_t out_dim) {
+    return n_tokens >= kOfficialGroupedMinTokens &&
+           grouped_supported(OBJETA_HIP_FP4_E2M1, n_table, n_tokens, k, hidden, inter, out_dim);
+}
+
+// The official layer of launch_moe_official_fp4 on the grouped-token products: x is
+// quantized and dequantized as there (its values, a 4-bit significand times a power
+// of two, split into fp16 parts exactly), the routed FP4 experts and the FP8 shared
+// expert (a launch of its own per phase, its member sets apart) read each matrix
+// once per member set, the intermediates are quantized in place, and the combine
+// adds w * down in slot order from zero, then the shared expert's down.
+int32_t launch_moe_official_grouped(objeta_hip_context* ctx, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                                    uint64_t n_table, const objeta_hip_expert_ptrs* shared, const uint32_t* ids,
+                                    const float* wts, uint64_t n_tokens, uint64_t k, const float* x, float* out,
+                                    uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit,
+                                    uint8_t* inter_values, uint8_t* inter_scales, const OfficialMarks* marks) {
+    const char* action = "launch official FP4 MoE (grouped)";
+    if (!official_grouped_supported(n_table, n_tokens, k, hidden, inter, out_dim))
+        OBJ_FAIL(kUnsupported, action, "shape outside the grouped official path");
+    const uint32_t T = static_cast<uint32_t>(n_tokens), A = static_cast<uint32_t>(n_tokens * k);
+    const uint32_t NR = A + (shared ? T : 0);       // act rows: routed, then shared
+    const uint32_t NSS = shared ? (T + 7) / 8 : 0;  // shared member sets
+    const uint32_t H = static_cast<uint32_t>(hidden), I = static_cast<uint32_t>(inter), O = static_cast<uint32_t>(out_dim);
+    size_t off = 0;
+    const size_t o_hdr = off; off += align256(16);
+    const size_t o_set = off; off += align256(sizeof(SetRec) * A);
+    const size_t o_hdr2 = off; off += align256(16);
+    const size_t o_set2 = off; off += align256(sizeof(SetRec) * (NSS ? NSS : 1));
+    const size_t o_xd = off; off += align256(4ull * T * H);
+    const size_t o_xm = off; off += align256(4ull * T);
+    const size_t o_am = off; off += align256(4ull * NR);
+    const size_t o_xh = off; off += align256(2ull * T * H);
+    const size_t o_xl = off; off += align256(2ull * T * H);
+    const size_t o_act = off; off += align256(4ull * NR * I);
+    const size_t o_ah = off; off += align256(2ull * NR * I);
+    const size_t o_al = off; off += align256(2ull * NR * I);
+    const size_t o_part = off; off += align256(4ull * NR * O);
+    void* wsp = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsGrouped, off, &wsp));
+    char* b = static_cast<char*>(wsp);
+    const GroupWs gw{reinterpret_cast<uint32_t*>(b + o_hdr), reinterpret_cast<SetRec*>(b + o_set)};
+    const GroupWs gws{reinterpret_cast<uint32_t*>(b + o_hdr2), reinterpret_cast<SetRec*>(b + o_set2)};
+    float* xd = reinterpret_cast<float*>(b + o_xd);
+    float* xmult = reinterpret_cast<float*>(b + o_xm);
+    float* amult = reinterpret_cast<float*>(b + o_am);
+    auto* xh = reinterpret_cast<_Float16*>(b + o_xh);
+    auto* xl = reinterpret_cast<_Float16*>(b + o_xl);
+    float* act = reinterpret_cast<float*>(b + o_act);
+    auto* ah = reinterpret_cast<_Float16*>(b + o_ah);
+    auto* al = reinterpret_cast<_Float16*>(b + o_al);
+    float* part = reinterpret_cast<float*>(b + o_part);
+    uint32_t* err = ctx->err_word;
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    const uint32_t kk = static_cast<uint32_t>(k);
+    auto mark = [&](hipEvent_t e) -> int32_t {
+        if (e) OBJ_HIP(hipEventRecord(e, s), "record event");
+        return 0;
+    };
+    OBJ_TRY(launch_act_quant(s, x, T, H, nullptr, nullptr, xd));
+    hipLaunchKernelGGL(moe_prepare_kernel, dim3(1 + T), dim3(256), 0, s, ids, A, static_cast<uint32_t>(n_table), table,
+                       shared, T, gw, shared ? gws : GroupWs{nullptr, nullptr}, err, xd, H, xh, xl, xmult);
+    launch_grouped_products<Fp4Rows, true>(s, gw, xh, xl, xmult, act, H, I, kk, A, limit, true, A, cus);
+    OBJ_HIP(hipGetLastError(), action);
+    OBJ_TRY(mark(marks ? marks->gate_up_end : nullptr));
+    if (shared) {
+        launch_grouped_products<Fp8Rows, true>(s, gws, xh, xl, xmult, act, H, I, kk, A, limit, true, NSS, cus);
+        OBJ_HIP(hipGetLastError(), action);
+    }
+    OBJ_TRY(mark(marks ? marks->shared_gate_up_end : nullptr));
+    OBJ_TRY(launch_act_quant(s, act, NR, I, inter_values, inter_scales, act));
+    OBJ_TRY(mark(marks ? marks->act_quant_end : nullptr));
+    hipLaunchKernelGGL(moe_split_kernel, dim3(NR), dim3(256), 0, s, act, I, ah, al, amult);
+    launch_grouped_products<Fp4Rows, false>(s, gw, ah, al, amult, part, I, O, kk, A, 0.0f, false, A, cus);
+    OBJ_HIP(hipGetLastError(), action);
+    OBJ_TRY(mark(marks ? marks->down_end : nullptr));
+    if (shared) launch_grouped_products<Fp8Rows, false>(s, gws, ah, al, amult, part, I, O, kk, A, 0.0f, false, NSS, cus);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((O + 255) / 256, T), dim3(256), 0, s, ids, wts, part,
+                       shared ? part + static_cast<size_t>(A) * O : nullptr, nullptr, out, kk, O,
+                       static_cast<uint32_t>(n_table));
+    OBJ_HIP(hipGetLastError(), action);
     return 0;
 }
 

@@ -67,6 +67,17 @@ int32_t launch_moe_official_fp4(objeta_hip_context* ctx, hipStream_t s, const ob
                                 uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit,
                                 uint8_t* inter_values, uint8_t* inter_scales, const OfficialMarks* marks);
 
+// The same layer on the grouped-token products (grouped.hip), for batches of at
+// least kOfficialGroupedMinTokens tokens in the grouped path's limits.
+constexpr uint64_t kOfficialGroupedMinTokens = 12;
+bool official_grouped_supported(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden, uint64_t inter,
+                                uint64_t out_dim);
+int32_t launch_moe_official_grouped(objeta_hip_context* ctx, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                                    uint64_t n_table, const objeta_hip_expert_ptrs* shared, const uint32_t* ids,
+                                    const float* wts, uint64_t n_tokens, uint64_t k, const float* x, float* out,
+                                    uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit,
+                                    uint8_t* inter_values, uint8_t* inter_scales, const OfficialMarks* marks);
+
 int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                         uint64_t n_table, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                         const float* act, const float* resid, float* out, uint64_t inter, uint64_t out_dim,

@@ -25,37 +25,11 @@
 #include "kernels.hpp"
 #include "quant_rules.hpp"
 #include "router_math.hpp"
+#include "swiglu.hpp"
 
 namespace objeta {
 namespace dev {
 
-
-// silu_mul (kernels/moe.cu:2-22); the CPU reference is moe.rs:1308-1315.
-__device__ __forceinline__ float silu_mul(float g, float u, float limit) {
-    if (limit > 0.0f) {
-        u = fminf(limit, fmaxf(-limit, u));
-        g = fminf(limit, g);
-    }
-    const float silu = g / (1.0f + expf(-g));
-    return silu * u;
-}
-
-// The SwiGLU of the official compositions (crates/objeta-parser/src/deepseek.rs:
-// 1680-1686, 1708-1713): only the up projection is clamped, exp is glibc's expf
-// (Rust's f32::exp) and the division is the IEEE float quotient, here the double
-// quotient rounded once to float (exact: a double carries more than 2 * 24 + 2
-// bits, so the double rounding of a float division is innocuous). __fdiv_rn in this
-// spot gave every kernel of the file a private stack.
-__device__ __forceinline__ float swiglu_official(float g, float u, float limit) {
-    if (u < -limit) u = -limit;
-    else if (u > limit) u = limit;
-    const float d = 1.0f + rmath::expf_glibc(-g);
-    return static_cast<float>(static_cast<double>(g) / static_cast<double>(d)) * u;
-}
-
-__device__ __forceinline__ float swiglu(float g, float u, float limit, uint32_t official) {
-    return official ? swiglu_official(g, u, limit) : silu_mul(g, u, limit);
-}
 
 // Expert id of assignment a; ids == nullptr means the identity. Returns false
 // (and raises the device error word) when the id is outside the table.
@@ -691,7 +665,8 @@ int32_t launch_moe_selected(objeta_hip_context* ctx, int32_t format, hipStream_t
 
 // ------------------------------------------------------- official FP4 layer
 // execute_selected_moe_official_routed_fp4_cuda (moe.rs:1393-1663) for a batch of
-// tokens, in six launches: act_quant(x) dequantized; the routed gate/up (FP4 split
+// tokens (from kOfficialGroupedMinTokens tokens on, launch_moe_official_grouped), in
+// six launches: act_quant(x) dequantized; the routed gate/up (FP4 split
 // weights, official SwiGLU) of every (token, slot); the shared expert's gate/up
 // (FP8 weights) into the rows after them; act_quant of all intermediates,
 // dequantized in place; the routed down with the weighted combine from zero
@@ -730,6 +705,11 @@ int32_t launch_moe_official_fp4(objeta_hip_context* ctx, hipStream_t s, const ob
                      strf("FP8 shared expert needs hidden %llu and intermediate %llu with a streaming lane split",
                           (unsigned long long)hidden, (unsigned long long)inter));
     }
+    // a batch: every routed expert's matrices (and the shared expert's) read once per
+    // member set instead of once per (token, slot)
+    if (official_grouped_supported(n_table, n_tokens, k, hidden, inter, out_dim))
+        return launch_moe_official_grouped(ctx, s, table, n_table, shared, ids, wts, n_tokens, k, x, out, hidden,
+                                           inter, out_dim, limit, inter_values, inter_scales, marks);
     const size_t xb = (static_cast<size_t>(n_tokens * hidden) * sizeof(float) + 255) & ~size_t(255);
     const size_t ab = static_cast<size_t>(n_tokens * kk * inter) * sizeof(float);
     void* ws = nullptr;

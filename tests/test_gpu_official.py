@@ -327,7 +327,7 @@ def check_official(out, q, s, experts, shared, selections, xs, hidden, inter, ou
     return flips
 
 
-@pytest.mark.parametrize("T,k,with_shared", [(1, 8, True), (2, 6, True), (1, 4, False)])
+@pytest.mark.parametrize("T,k,with_shared", [(1, 8, True), (2, 6, True), (1, 4, False), (12, 8, True)])
 def test_official_layer_deepseek_shape(backend, T, k, with_shared):
     hidden, inter, out_dim, n = 7168, 2048, 7168, 10
     experts = [fp4_random_expert(hidden, inter, out_dim, 900 + 7 * e) for e in range(n)]
@@ -338,6 +338,56 @@ def test_official_layer_deepseek_shape(backend, T, k, with_shared):
     xs = orc.gauss(T * hidden, 77 + T, 1.0).reshape(T, hidden)
     out, q, s = run_official(backend, experts, shared, selections, xs, hidden, inter, out_dim)
     check_official(out, q, s, experts, shared, selections, xs, hidden, inter, out_dim)
+
+
+@pytest.mark.parametrize("T,k,with_shared", [(12, 4, True), (33, 3, True), (16, 4, False)])
+def test_official_layer_batch_grouped(backend, T, k, with_shared):
+    """From 12 tokens on, the layer runs on the grouped-token products: the routed FP4
+    experts grouped by expert (about 20 assignments per expert at T=33, so groups span
+    several member sets of 8), the FP8 shared expert as one group of all tokens with
+    launches of its own. Same bar as the per-token path."""
+    hidden, inter, out_dim, n = 512, 384, 640, 5
+    experts = [fp4_random_expert(hidden, inter, out_dim, 300 + 3 * e) for e in range(n)]
+    shared = fp8_random_expert(hidden, inter, out_dim, 77) if with_shared else None
+    rng = np.random.default_rng(T * 7 + k)
+    selections = [[(int(e), float(w)) for e, w in zip(rng.choice(n, k, replace=False),
+                                                      rng.dirichlet(np.ones(k)).astype(F32))] for _ in range(T)]
+    xs = orc.gauss(T * hidden, 91 + T, 2.0).reshape(T, hidden)
+    out, q, s = run_official(backend, experts, shared, selections, xs, hidden, inter, out_dim)
+    check_official(out, q, s, experts, shared, selections, xs, hidden, inter, out_dim)
+
+
+def test_official_layer_batch_repeats_limits_and_bad_id(backend):
+    """The grouped official path with a token that selects one expert twice, the
+    clamp at 0.5 and at 0, and an out-of-table id (error bit 1, that token's output
+    NaN, the other tokens unaffected)."""
+    hidden, inter, out_dim, n = 256, 256, 384, 4
+    experts = [fp4_random_expert(hidden, inter, out_dim, 40 + e) for e in range(n)]
+    shared = fp8_random_expert(hidden, inter, out_dim, 41)
+    T = 14
+    rng = np.random.default_rng(5)
+    selections = [[(int(rng.integers(n)), float(rng.uniform(-1, 1))) for _ in range(3)] for _ in range(T)]
+    selections[3] = [(2, 0.5), (2, 0.25), (1, 0.25)]
+    xs = orc.gauss(T * hidden, 12, 3.0).reshape(T, hidden)
+    for limit in (0.5, 0.0):
+        out, q, s = run_official(backend, experts, shared, selections, xs, hidden, inter, out_dim, limit)
+        check_official(out, q, s, experts, shared, selections, xs, hidden, inter, out_dim, limit)
+    moe = MoeExecutor(backend)
+    keep = [[backend.to_device(a) for a in ex] for ex in experts]
+    table = ExpertTable(backend, [ptr_order(kp) for kp in keep])
+    sh_keep = [backend.to_device(a) for a in shared]
+    sh_table = ExpertTable(backend, [ptr_order(sh_keep)])
+    ids = np.array([[e for e, _ in sel] for sel in selections], np.uint32)
+    ids[6, 1] = n + 3
+    ws = np.array([[w for _, w in sel] for sel in selections], F32)
+    d_out = backend.alloc(4 * T * out_dim)
+    moe.official_fp4_device(table, backend.to_device(ids.ravel()), backend.to_device(ws.ravel()), T, 3,
+                            backend.to_device(xs.ravel()), d_out, hidden, inter, out_dim, 10.0, None, sh_table)
+    backend.synchronize()
+    assert moe.device_error() & 1
+    out = d_out.download(F32, T * out_dim).reshape(T, out_dim)
+    assert np.all(np.isnan(out[6]))
+    assert np.all(np.isfinite(np.delete(out, 6, axis=0)))
 
 
 def test_official_layer_small_shapes_and_limits(backend):
