@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
 // registers (lane l: elements [l*hidden/64, (l+1)*hidden/64)) and x is staged in
 // LDS, so a logit is one pass of lane-local prefix sums (exact_logit_lanes)
 // instead of a wave scan per 256 elements.
-constexpr uint32_t kRefineScratch = kRWaves * 2048;  // floats of row chunks for select_refine
+constexpr uint32_t kRefineScratch = kRWaves * 4096;  // floats of row chunks for select_refine
 
 template <int NB>
 __global__ __launch_bounds__(kRThreads) void router_lanes_kernel(
@@ -246,6 +246,93 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
                   sel_tab ? sel_tab + static_cast<size_t>(t) * k : nullptr);
 }
 
+// Batches (n_tokens >= 2) of router_split_kernel's shapes in two launches. First the
+// logits: the same arithmetic per (expert, token) as router_split_kernel, so a token
+// gets the same words as in a call of its own, but each row is read once for a group
+// of tb tokens (one workgroup per row and token holds a full-size LDS allocation for
+// the selection, which capped a batch at two workgroups per CU). grid = (E,
+// ceil(T / tb)); workgroup (e, g) keeps row e in registers and publishes its logit
+// and bound for tokens g*tb .. g*tb + tb - 1, the next token's activations in flight
+// during each sum.
+template <int NB>
+__global__ __launch_bounds__(kRThreads) void router_logits_batch_kernel(
+    const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x, uint32_t n_tokens,
+    uint32_t hidden, uint32_t tb, uint64_t* __restrict__ ws, const uint32_t* __restrict__ counters) {
+    __shared__ double red[8];
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const uint32_t e = blockIdx.x;
+    const uint32_t t0 = blockIdx.y * tb;
+    const uint32_t t1 = t0 + tb < n_tokens ? t0 + tb : n_tokens;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t n4 = hidden >> 10;  // float4 per lane
+    const uint32_t q0 = wave * n4 * 64u + lane * n4;
+    float4 wr[NB], xv[NB], xn[NB];
+    auto load_x = [&](uint32_t t, float4 (&dst)[NB]) {
+        const gptr<f32x4> x4 = as_global(reinterpret_cast<const f32x4*>(x + static_cast<size_t>(t) * hidden));
+#pragma unroll
+        for (int g = 0; g < NB; ++g) {
+            const f32x4 u = x4[q0 + (static_cast<uint32_t>(g) < n4 ? static_cast<uint32_t>(g) : n4 - 1)];
+            dst[g] = make_float4(u.x, u.y, u.z, u.w);
+        }
+    };
+    {
+        const gptr<f32x4> r4 = as_global(reinterpret_cast<const f32x4*>(w_r + static_cast<size_t>(e) * hidden));
+#pragma unroll
+        for (int g = 0; g < NB; ++g) {
+            const f32x4 v = r4[q0 + (static_cast<uint32_t>(g) < n4 ? static_cast<uint32_t>(g) : n4 - 1)];
+            wr[g] = make_float4(v.x, v.y, v.z, v.w);
+        }
+    }
+    load_x(t0, xv);
+    for (uint32_t t = t0; t < t1; ++t) {
+        if (t + 1 < t1) load_x(t + 1, xn);
+        // red: every wave has passed both barriers of the previous sum before this
+        // one writes it again
+        double total, abs_bound;
+        exact_logit_split<NB>(wr, xv, n4, lane, wave, red, total, abs_bound);
+        if (threadIdx.x == 0) {
+            const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+            uint64_t* ws_logit = ws + static_cast<size_t>(t) * 2 * kMaxExperts;
+            float lhat, bnd;
+            finish_logit(total, abs_bound, bias, e, hidden, lhat, bnd);
+            __hip_atomic_store(&ws_logit[e], tag(lhat, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ws_logit[kMaxExperts + e], tag(bnd, epoch), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int g = 0; g < NB; ++g) xv[g] = xn[g];
+    }
+}
+
+// Then one workgroup per token selects from the published words (all of this
+// epoch: the logits launch has finished), as workgroup 0 of router_split_kernel
+// does, and advances counters[t]; table / sel_tab as there (the table read from
+// global memory).
+__global__ __launch_bounds__(kRThreads) void router_select_batch_kernel(
+    const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
+    uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
+    float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
+    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ table,
+    objeta_hip_expert_ptrs* __restrict__ sel_tab) {
+    extern __shared__ float xs[];  // x in the padded pair layout, then the refinement scratch
+    const uint32_t t = blockIdx.x;
+    const float* xt = x + static_cast<size_t>(t) * hidden;
+    uint64_t* ws_logit = ws + static_cast<size_t>(t) * 2 * kMaxExperts;
+    uint64_t* ws_bound = ws_logit + kMaxExperts;
+    const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    for (uint32_t i = threadIdx.x; i < (hidden >> 2); i += kRThreads) {
+        const uint32_t c = i << 2;
+        *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = reinterpret_cast<const float4*>(xt)[i];
+    }
+    __syncthreads();
+    const uint32_t x_floats = (hidden / 64) * kPadX;
+    const float* xl = xs;
+    router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,
+                  renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit,
+                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch, table,
+                  sel_tab ? sel_tab + static_cast<size_t>(t) * k : nullptr);
+}
+
 __global__ __launch_bounds__(256) void softmax_exp_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                           uint64_t n) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
@@ -283,10 +370,32 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
     uint32_t* err = ctx->err_word;
     const bool lanes = vec && hidden % 256 == 0 && hidden <= 256u * 32u;
     const bool split = vec && hidden % 1024 == 0 && hidden <= 1024u * 8u;
+    // a batch of the split kernel's shapes: logits for groups of tokens, then one
+    // selection workgroup per token
+    const bool batched = split && n_tokens >= 2;
     // table resolution (split kernel, up to kSelTabMaxExperts experts) or none
     objeta_hip_expert_ptrs* st = (sel_tab && table && split && n_experts <= kSelTabMaxExperts) ? *sel_tab : nullptr;
     if (sel_tab) *sel_tab = st;
-    if (split) {
+    if (batched) {
+        // enough (row, token group) workgroups for about four per CU, up to 8 tokens each
+        const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+        uint64_t tb = (n_experts * n_tokens + 4ull * cus - 1) / (4ull * cus);
+        tb = tb < 1 ? 1 : (tb > 8 ? 8 : tb);
+        const dim3 lgrid(static_cast<uint32_t>(n_experts), static_cast<uint32_t>((n_tokens + tb - 1) / tb));
+        if (hidden <= 1024u * 2u)
+            hipLaunchKernelGGL(router_logits_batch_kernel<2>, lgrid, dim3(kRThreads), 0, s, w_r, bias, x,
+                               static_cast<uint32_t>(n_tokens), static_cast<uint32_t>(hidden),
+                               static_cast<uint32_t>(tb), ws, counters);
+        else
+            hipLaunchKernelGGL(router_logits_batch_kernel<8>, lgrid, dim3(kRThreads), 0, s, w_r, bias, x,
+                               static_cast<uint32_t>(n_tokens), static_cast<uint32_t>(hidden),
+                               static_cast<uint32_t>(tb), ws, counters);
+        const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
+        hipLaunchKernelGGL(router_select_batch_kernel, dim3(static_cast<uint32_t>(n_tokens)), dim3(kRThreads), lds, s,
+                           w_r, bias, x, static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
+                           static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err,
+                           st ? table : nullptr, st);
+    } else if (split) {
         const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float) +
                            (st ? static_cast<size_t>(n_experts) * sizeof(objeta_hip_expert_ptrs) : 0);
         const dim3 sgrid(static_cast<uint32_t>(n_experts), static_cast<uint32_t>(n_tokens));

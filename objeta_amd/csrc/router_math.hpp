@@ -597,19 +597,42 @@ __device__ void refine_rows(SelectLds<MAXE>& s, const float* __restrict__ w_r, c
         if (C > h16) C = h16;
         const uint32_t S = C + 4u;
         const uint32_t nchunks = (hidden + C - 1u) / C;
-        // waves 1..3: rounded products of chunk c into buffer c & 1
+        // waves 1..3: rounded products of chunk c into buffer c & 1 (16-byte row reads
+        // where the rows are 16-byte aligned; C is a multiple of 16)
+        const bool v4 = (hidden & 3u) == 0 && (reinterpret_cast<uintptr_t>(w_r) & 15u) == 0;
+        typedef __attribute__((address_space(3))) float lds_float;
         auto fill = [&](uint32_t c) {
-            float* buf = scratch + (c & 1u) * ng * S;
+            lds_float* buf = (lds_float*)(scratch + (c & 1u) * ng * S);
             const uint32_t c0 = c * C;
             const uint32_t m = hidden - c0 < C ? hidden - c0 : C;
+            if (v4) {
+                const uint32_t C4 = C >> 2, m4 = m >> 2;
+#pragma unroll 2
+                for (uint32_t item = threadIdx.x - 64u; item < ng * C4; item += kRThreads - 64u) {
+                    const uint32_t r = item / C4, i4 = item - r * C4;
+                    if (i4 < m4) {
+                        const uint32_t e = static_cast<uint32_t>(s.nlist[g0 + r]);
+                        const uint32_t h = c0 + 4u * i4;
+                        typedef float f32x4 __attribute__((ext_vector_type(4)));
+                        const f32x4 w = *dev::as_global(reinterpret_cast<const f32x4*>(w_r + static_cast<size_t>(e) * hidden + h));
+                        f32x4 p;
+                        p[0] = w[0] * xat(h);
+                        p[1] = w[1] * xat(h + 1u);
+                        p[2] = w[2] * xat(h + 2u);
+                        p[3] = w[3] * xat(h + 3u);
+                        *(__attribute__((address_space(3))) f32x4*)(buf + r * S + 4u * i4) = p;
+                    }
+                }
+            } else {
 #pragma unroll 4
-            for (uint32_t item = threadIdx.x - 64u; item < ng * C; item += kRThreads - 64u) {
-                const uint32_t r = item / C, i = item - r * C;
-                if (i < m) {
-                    const uint32_t e = static_cast<uint32_t>(s.nlist[g0 + r]);
-                    const float w = w_r[static_cast<size_t>(e) * hidden + c0 + i];
-                    const float p = w * xat(c0 + i);
-                    buf[r * S + i] = p;
+                for (uint32_t item = threadIdx.x - 64u; item < ng * C; item += kRThreads - 64u) {
+                    const uint32_t r = item / C, i = item - r * C;
+                    if (i < m) {
+                        const uint32_t e = static_cast<uint32_t>(s.nlist[g0 + r]);
+                        const float w = w_r[static_cast<size_t>(e) * hidden + c0 + i];
+                        const float p = w * xat(c0 + i);
+                        buf[r * S + i] = p;
+                    }
                 }
             }
         };
@@ -620,17 +643,43 @@ __device__ void refine_rows(SelectLds<MAXE>& s, const float* __restrict__ w_r, c
             if (wave != 0) {
                 if (c + 1u < nchunks) fill(c + 1u);
             } else if (lane < ng) {
+                // the scratch is LDS in every caller: reading it as such gives LDS loads
+                // (a generic pointer would give flat loads, counted with the memory loads)
+                typedef float f32x4 __attribute__((ext_vector_type(4)));
+                typedef __attribute__((address_space(3))) const f32x4 lds_f4;
                 const float* row = scratch + (c & 1u) * ng * S + lane * S;
+                lds_f4* row4 = (lds_f4*)(row);
                 const uint32_t m = hidden - c * C < C ? hidden - c * C : C;
-                const uint32_t m4 = m & ~3u;
-                for (uint32_t i = 0; i < m4; i += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(row + i);
-                    acc = acc + v.x;
-                    acc = acc + v.y;
-                    acc = acc + v.z;
-                    acc = acc + v.w;
+                const uint32_t nb = m >> 4;  // blocks of 16 products
+                // two register buffers: block j + 1 is read while block j is added (an
+                // LDS read takes far longer than the four adds it feeds)
+                f32x4 va[4], vb[4];
+                auto add4 = [&](const f32x4 (&v)[4]) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        acc = acc + v[q][0];
+                        acc = acc + v[q][1];
+                        acc = acc + v[q][2];
+                        acc = acc + v[q][3];
+                    }
+                };
+                auto load4 = [&](f32x4 (&v)[4], uint32_t j) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) v[q] = row4[4 * j + q];
+                };
+                // straight-line pairs (the last read of a pair re-reads a block in
+                // range), so the wait before each add covers that block's reads only
+                if (nb) load4(va, 0);
+                uint32_t j = 0;
+                for (; j + 2 <= nb; j += 2) {
+                    load4(vb, j + 1);
+                    add4(va);
+                    load4(va, j + 2 < nb ? j + 2 : j + 1);
+                    add4(vb);
                 }
-                for (uint32_t i = m4; i < m; ++i) acc = acc + row[i];
+                if (j < nb) add4(va);
+                const uint32_t m32 = nb << 4;
+                for (uint32_t i = m32; i < m; ++i) acc = acc + row[i];
             }
             __syncthreads();
         }
