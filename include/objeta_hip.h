@@ -340,11 +340,12 @@ int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, obje
 /* One MoE layer on the device: the router of objeta_hip_router_topk_device over
  * d_router_w [n_experts][hidden] (+ d_router_bias) writes d_ids_out/d_weights_out
  * [n_tokens][k], then the selected experts of d_table (n_experts entries) run:
- * below 12 tokens on the per-assignment kernels of objeta_hip_moe_selected_device,
- * from 12 tokens on the grouped-token products of objeta_hip_moe_grouped_device
+ * below 17 tokens on the per-assignment kernels of objeta_hip_moe_selected_device,
+ * from 17 tokens on the grouped-token products of objeta_hip_moe_grouped_device
  * whenever that path takes the shape (on MI355X at hidden 2048, 128 experts,
- * top-8 the per-assignment kernels are faster at 8 tokens, the grouped ones at 16
- * and beyond). The two agree within the fp32 tolerance, not bit for bit. No host
+ * top-8 with uniformly spread selections the per-assignment kernels are faster up
+ * to 16 tokens, the grouped ones from 18 on). The two agree within the fp32
+ * tolerance, not bit for bit. No host
  * synchronisation; graph-capturable. No reference counterpart as one call: the
  * reference routes on the host (deepseek_single_layer_moe.rs:687-743) and then
  * calls execute_selected_moe_cuda. */

@@ -105,7 +105,7 @@ int32_t launch_gemv_mfma(objeta_hip_context* ctx, hipStream_t s, int32_t format,
 // Batches from this many tokens run the grouped-token products in the layer entry
 // points (measured on MI355X at hidden 2048, 128 experts, top-8: per-assignment
 // faster at 8 tokens, grouped at 16 and beyond).
-constexpr uint64_t kGroupedMinTokens = 12;
+constexpr uint64_t kGroupedMinTokens = 17;
 // Whether launch_moe_grouped takes this shape.
 bool grouped_supported(int32_t format, uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden,
                        uint64_t inter, uint64_t out_dim);
