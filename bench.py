@@ -24,6 +24,7 @@ Also measured in the same run (each in its own object of the JSON line):
   batch 1 and 32;
 - official: the same routed experts through the FP8-activation ("official
   arithmetic") layer with an FP8 shared expert, batch 1 and 32;
+- router: the router alone at the DeepSeek and Qwen3-A3B shapes for 1 to 32 tokens;
 - misses: the headline stack through the host-in/host-out executor with the expert
   cache at 25% of the expert bytes, experts in pinned host memory: end-to-end
   us/token including the PCIe copies of the misses, and the copies' GB/s;
@@ -57,7 +58,7 @@ from objeta_amd.workloads import zipf_bias  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 ROTATE_BYTES = 4 << 30  # working set of the rotated GEMV measurements (>> 256 MB MALL)
-SECTIONS = ("headline", "kernels", "batch", "gemv", "deepseek", "official", "misses", "cpu")
+SECTIONS = ("headline", "kernels", "batch", "gemv", "deepseek", "official", "router", "misses", "cpu")
 # not in the default run: kernels of known traffic for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE
 EXTRA_SECTIONS = ("calibrate",)
 TRAFFIC_PROFILE = "profiles/moe_layer_q4_qwen3a3b_hbm_traffic.md"
@@ -517,6 +518,53 @@ def run_deepseek(env: Env, args, seed):
     return res
 
 
+# ------------------------------------------------------------- router alone
+def run_router(env: Env, args, seed):
+    """objeta_hip_router_topk_device alone at the DeepSeek (256 experts, hidden 7168)
+    and Qwen3-A3B (128 experts, hidden 2048) shapes, top-8, for 1 to 32 tokens: one
+    token runs router_split_kernel (logits and the selecting workgroup in one launch),
+    a batch the two-launch form (router_logits_batch_kernel, router_select_batch_kernel).
+    A hipGraph holds 32 consecutive calls over a pool of 32 tokens (T tokens per call,
+    the groups in turn) and the figure is the graph's time over 32, so it includes the
+    gap between dependent launches as a layer does. A call whose exact-sum bounds
+    cannot separate a decision recomputes the undecided logits in the reference's
+    sequential order; with a batch the slowest token sets the call's time."""
+    be = env.be
+    res = {"path": "32 calls of objeta_hip_router_topk_device per hipGraph (renormalised top-8)"}
+    for name, E, H in (("deepseek", 256, 7168), ("qwen3a3b", 128, 2048)):
+        K, P, N = 8, 32, 32
+        w = be.alloc(4 * E * H)
+        env.fill_gauss(w.ptr, E * H, seed + E, 0.02)
+        xs = be.alloc(4 * P * H)
+        env.fill_gauss(xs.ptr, P * H, seed + 7 + E, 1.0)
+        ids = be.alloc(4 * P * K)
+        wts = be.alloc(4 * P * K)
+        r = {"experts": E, "hidden": H, "top_k": K, "weight_bytes": 4 * E * H}
+        for T in (1, 2, 4, 8, 16, 32):
+            groups = P // T
+
+            def enq(T=T, groups=groups):
+                for i in range(N):
+                    g = i % groups
+                    env.check(env.lib.objeta_hip_router_topk_device(env.ctx, env.stream, w.addr(), None,
+                                                                    xs.addr(4 * g * T * H), T, E, H, K, 1,
+                                                                    ids.addr(4 * g * T * K), wts.addr(4 * g * T * K)))
+            enq()
+            be.synchronize(env.stream)
+            g = env.capture(enq)
+            for _ in range(3):
+                env.launch(g)
+            be.synchronize(env.stream)
+            _, per = env.per_step(lambda i: env.launch(g), max(10, args.steps // 4))
+            sc = stats([v / N for v in per])
+            r[f"tokens{T}"] = {"us_per_call": rnd(sc), "us_per_token": round(sc["avg"] / T, 3)}
+            env.destroy([g])
+        res[name] = r
+        for b in (w, xs, ids, wts):
+            b.free()
+    return res
+
+
 # ------------------------------------------- DeepSeek official arithmetic (FP8)
 def run_official(env: Env, args, seed):
     """The FP8-activation ("official arithmetic") layer at the DeepSeek shape: router,
@@ -922,6 +970,10 @@ def main() -> int:
     if "official" in sections:
         stage("official")
         official = run_official(env, args, args.seed + 6000)
+    router = None
+    if "router" in sections:
+        stage("router")
+        router = run_router(env, args, args.seed + 7000)
     report = {} if args.report_dir else None
     misses = None
     if "misses" in sections:
@@ -977,6 +1029,7 @@ def main() -> int:
         "gemv": gemv,
         "deepseek": deepseek,
         "official": official,
+        "router": router,
         "misses": misses,
         "cpu_baseline": cpu,
         "device": {"name": dev["name"], "arch": dev["arch"], "compute_units": dev["compute_units"]},
