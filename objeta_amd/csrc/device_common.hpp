@@ -324,25 +324,34 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&d)[Fmt<F>::kPairDw],
 // fp16 bits (c & 7) << 9 encode E2M1(c) * 2^-14 exactly (the f16 subnormal
 // covers E2M1's e=0 codes), and bit 3 of the code is the sign. One nibble dword
 // n (byte k: weight 2k low, 2k+1 high) against x[0..7]; accumulates
-// E2M1(q)*2^-14*x, the caller multiplies by the block scale * 2^14.
+// The 8 E2M1 codes of a dword (element 2j in the low nibble of byte j, 2j + 1 in
+// the high one) as exact fp16 pairs (w_{2j}, w_{2j+1}): gfx950's
+// v_cvt_scalef32_pk_f16_fp4 with scale 1, one instruction per byte (checked against
+// the E2M1 table on every byte and byte select, -0 for code 8 included).
+__device__ __forceinline__ void fp4_to_h2x4(uint32_t n, h2 (&p)[4]) {
+    p[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(n, 1.0f, 0);
+    p[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(n, 1.0f, 1);
+    p[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(n, 1.0f, 2);
+    p[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(n, 1.0f, 3);
+}
+
+// sum_i E2M1(q_i) * x_i over 8 weights (xa = x0..x3, xb = x4..x7); the caller
+// multiplies by the block scale.
 template <int NT>
 __device__ __forceinline__ void fp4_dot8(uint32_t n, const float4 (&xa)[NT], const float4 (&xb)[NT],
                                          float (&acc)[NT]) {
-    uint32_t n8 = n >> 8;
-    h2 a = as_h2(((n << 9) & 0x0E000E00u) | ((n << 12) & 0x80008000u));    // w0, w4
-    h2 b = as_h2(((n << 5) & 0x0E000E00u) | ((n << 8) & 0x80008000u));    // w1, w5
-    h2 c = as_h2(((n8 << 9) & 0x0E000E00u) | ((n8 << 12) & 0x80008000u));  // w2, w6
-    h2 d = as_h2(((n8 << 5) & 0x0E000E00u) | ((n8 << 8) & 0x80008000u));  // w3, w7
+    h2 p[4];
+    fp4_to_h2x4(n, p);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        acc[t] = __builtin_fmaf((float)a.x, xa[t].x, acc[t]);
-        acc[t] = __builtin_fmaf((float)a.y, xb[t].x, acc[t]);
-        acc[t] = __builtin_fmaf((float)b.x, xa[t].y, acc[t]);
-        acc[t] = __builtin_fmaf((float)b.y, xb[t].y, acc[t]);
-        acc[t] = __builtin_fmaf((float)c.x, xa[t].z, acc[t]);
-        acc[t] = __builtin_fmaf((float)c.y, xb[t].z, acc[t]);
-        acc[t] = __builtin_fmaf((float)d.x, xa[t].w, acc[t]);
-        acc[t] = __builtin_fmaf((float)d.y, xb[t].w, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[0].x, xa[t].x, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[0].y, xa[t].y, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[1].x, xa[t].z, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[1].y, xa[t].w, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[2].x, xb[t].x, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[2].y, xb[t].y, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[3].x, xb[t].z, acc[t]);
+        acc[t] = __builtin_fmaf((float)p[3].y, xb[t].w, acc[t]);
     }
 }
 

@@ -86,7 +86,7 @@ struct Fp4Rows {
                     fp4_dot8<NT>(d[blk * 4 + j], xa, xb, a);
                 }
 #pragma unroll
-                for (int t = 0; t < NT; ++t) acc[t] = __builtin_fmaf(scale, a[t] * 16384.0f, acc[t]);
+                for (int t = 0; t < NT; ++t) acc[t] = __builtin_fmaf(scale, a[t], acc[t]);
             } else {
                 // the reference's w = table[q] * scale per weight (deepseek.rs:866-918)
                 for (int i = 0; i < 32; ++i) {

@@ -23,10 +23,12 @@
 // tolerance of the reference's sequential sums (not bit-identical: the order of
 // the additions differs, as in every parallel kernel here).
 //
-// Layout trick: within each 8-element k group the weights come out of the nibble
-// unpacking as (w0,w4),(w1,w5),(w2,w6),(w3,w7); the split activations are stored
-// in that same order, so no unpacking shuffle is needed (a k permutation applied
-// to both operands leaves the products unchanged).
+// Layout trick: within each 8-element k group the weights of the block formats come
+// out of the nibble unpacking as (w0,w4),(w1,w5),(w2,w6),(w3,w7); for them the split
+// activations are stored in that same order, so no unpacking shuffle is needed (a k
+// permutation applied to both operands leaves the products unchanged). FP4 (the
+// hardware conversion's pairs) and FP8 weights come in element order, and so do
+// their split activations.
 //
 // MFMA roles (D = A B, 16x16x32): A = activation parts, row m = 2 * token + part
 // (8 tokens per instruction); B = weights, column n = output row. Lane l holds
@@ -213,10 +215,10 @@ __device__ void group_assignments(const uint32_t* __restrict__ ids, uint32_t n_a
 // ------------------------------------------------------------- split rows
 // One workgroup per row: scale = 2^s with |x 2^s| < 2^14, then hi = fp16(x 2^s),
 // lo = fp16(x 2^s - hi), stored in the (w0,w4),(w1,w5),.. order of each group of
-// 8; mult[row] = 2^-s restores the products. A non-finite row keeps s = 0 (its
-// infinities and NaNs propagate).
+// 8 when perm is set, else in element order; mult[row] = 2^-s restores the
+// products. A non-finite row keeps s = 0 (its infinities and NaNs propagate).
 __device__ void split_row(const float* __restrict__ src, uint32_t cols, _Float16* __restrict__ hi,
-                          _Float16* __restrict__ lo, float* __restrict__ mult, uint32_t row) {
+                          _Float16* __restrict__ lo, float* __restrict__ mult, uint32_t row, uint32_t perm) {
     __shared__ float red[4];
     const float* x = src + static_cast<size_t>(row) * cols;
     float m = 0.0f;
@@ -242,7 +244,7 @@ __device__ void split_row(const float* __restrict__ src, uint32_t cols, _Float16
         half8 vh, vl;
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
-            const float xs = ldexpf(v[kPerm[d]], s);
+            const float xs = ldexpf(v[perm ? kPerm[d] : d], s);
             const _Float16 th = static_cast<_Float16>(xs);
             vh[d] = th;
             vl[d] = static_cast<_Float16>(xs - static_cast<float>(th));
@@ -260,16 +262,17 @@ __global__ __launch_bounds__(256) void moe_prepare_kernel(const uint32_t* __rest
                                                           uint32_t n_tokens, GroupWs w, GroupWs wsh,
                                                           uint32_t* __restrict__ err, const float* __restrict__ x,
                                                           uint32_t cols, _Float16* __restrict__ xh,
-                                                          _Float16* __restrict__ xl, float* __restrict__ xmult) {
+                                                          _Float16* __restrict__ xl, float* __restrict__ xmult,
+                                                          uint32_t perm) {
     if (blockIdx.x == 0) group_assignments(ids, n_assign, n_table, table, shared, n_tokens, w, wsh, err);
-    else split_row(x, cols, xh, xl, xmult, blockIdx.x - 1);
+    else split_row(x, cols, xh, xl, xmult, blockIdx.x - 1, perm);
 }
 
 // One workgroup per row.
 __global__ __launch_bounds__(256) void moe_split_kernel(const float* __restrict__ src, uint32_t cols,
                                                         _Float16* __restrict__ hi, _Float16* __restrict__ lo,
-                                                        float* __restrict__ mult) {
-    split_row(src, cols, hi, lo, mult, blockIdx.x);
+                                                        float* __restrict__ mult, uint32_t perm) {
+    split_row(src, cols, hi, lo, mult, blockIdx.x, perm);
 }
 
 
@@ -346,6 +349,7 @@ struct Tile;
 template <int F>
 struct Tile<QRows<F>> {
     static constexpr int kBB = Fmt<F>::kBlockBytes;
+    static constexpr bool kPermuted = true;  // weights in the (w0,w4),(w1,w5),.. order
     static constexpr bool kScales = false;
     static constexpr bool kTileScale = false;
     static constexpr uint32_t kChunkGU = 512, kChunkDn = 256;
@@ -377,6 +381,7 @@ struct Tile<QRows<F>> {
 
 template <>
 struct Tile<Fp4Rows> {
+    static constexpr bool kPermuted = false;
     static constexpr bool kScales = true;
     static constexpr bool kTileScale = false;
     static constexpr uint32_t kChunkGU = 512, kChunkDn = 256;
@@ -390,16 +395,13 @@ struct Tile<Fp4Rows> {
     static __device__ __forceinline__ const uint8_t* wrow(const Fp4Rows& m, uint32_t c0) { return m.w + c0 / 2; }
     static __device__ __forceinline__ const uint8_t* srow(const Fp4Rows& m, uint32_t c0) { return m.s + c0 / 32; }
     static __device__ __forceinline__ uint32_t tile_scales(const Fp4Rows&, uint32_t, uint32_t, uint32_t) { return 0; }
+    // the 8 weights in element order (the hardware conversion's pairs)
     static __device__ __forceinline__ half8 get(const uint8_t* w, const uint8_t* sc, uint32_t, uint32_t b, uint32_t kg,
                                                 float& scale) {
-        scale = e8m0_to_f32(sc[b]) * 16384.0f;
+        scale = e8m0_to_f32(sc[b]);
         const uint32_t n = *reinterpret_cast<const uint32_t*>(w + 16 * b + 4 * kg);
         h2 p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // E2M1 code c -> fp16 bits ((c & 7) << 9) | ((c & 8) << 12) = value * 2^-14
-            const uint32_t t = (n >> (4 * i)) & 0x000F000Fu;
-            p[i] = as_h2(((t & 0x00070007u) << 9) | ((t & 0x00080008u) << 12));
-        }
+        fp4_to_h2x4(n, p);
         return pack8(p[0], p[1], p[2], p[3]);
     }
 };
@@ -411,6 +413,7 @@ struct Tile<Fp4Rows> {
 // one byte per 128 columns for all of its rows.
 template <>
 struct Tile<Fp8Rows> {
+    static constexpr bool kPermuted = false;
     static constexpr bool kScales = false;
     static constexpr bool kTileScale = true;
     static constexpr uint32_t kChunkGU = 256, kChunkDn = 256;
@@ -439,9 +442,9 @@ struct Tile<Fp8Rows> {
         const uint32_t d1 = *reinterpret_cast<const uint32_t*>(w + 32 * b + 8 * kg + 4);
         half8 h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // (w_i, w_{i+4}): the order of the split activations
-            h[2 * i] = static_cast<_Float16>(rules::f8e4m3_to_f32((d0 >> (8 * i)) & 0xFFu));
-            h[2 * i + 1] = static_cast<_Float16>(rules::f8e4m3_to_f32((d1 >> (8 * i)) & 0xFFu));
+        for (int i = 0; i < 4; ++i) {  // element order
+            h[i] = static_cast<_Float16>(rules::f8e4m3_to_f32((d0 >> (8 * i)) & 0xFFu));
+            h[4 + i] = static_cast<_Float16>(rules::f8e4m3_to_f32((d1 >> (8 * i)) & 0xFFu));
         }
         return h;
     }
@@ -708,7 +711,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const void* __restrict__
                 half8 vh, vl;
 #pragma unroll
                 for (int d = 0; d < 8; ++d) {
-                    const float xv = ldexpf(v[8 * g + kPerm[d]], sh);
+                    const float xv = ldexpf(v[8 * g + (Tile<R>::kPermuted ? kPerm[d] : d)], sh);
                     const _Float16 th = static_cast<_Float16>(xv);
                     vh[d] = th;
                     vl[d] = static_cast<_Float16>(xv - static_cast<float>(th));
@@ -823,7 +826,8 @@ hipError_t launch_grouped(hipStream_t s, GroupWs gw, const _Float16* xh, const _
                           uint32_t hidden, uint32_t inter, uint32_t out_dim, float limit, uint32_t cus) {
     launch_grouped_products<R, true>(s, gw, xh, xl, xmult, act, hidden, inter, k, n_assign, limit, false, max_sets,
                                      cus);
-    hipLaunchKernelGGL(moe_split_kernel, dim3(n_rows), dim3(256), 0, s, act, inter, ah, al, amult);
+    hipLaunchKernelGGL(moe_split_kernel, dim3(n_rows), dim3(256), 0, s, act, inter, ah, al, amult,
+                       Tile<R>::kPermuted ? 1u : 0u);
     launch_grouped_products<R, false>(s, gw, ah, al, amult, part, inter, out_dim, k, n_assign, 0.0f, false, max_sets,
                                       cus);
     return hipGetLastError();
@@ -947,8 +951,10 @@ int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t 
     float* part = reinterpret_cast<float*>(b + o_part);
     uint32_t* err = ctx->err_word;
     const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    // the split order follows the weights' order (element order for FP4)
+    const bool perm = format == OBJETA_HIP_FP4_E2M1 ? Tile<Fp4Rows>::kPermuted : Tile<QRows<kQ4>>::kPermuted;
     hipLaunchKernelGGL(moe_prepare_kernel, dim3(1 + T), dim3(256), 0, s, ids, A, static_cast<uint32_t>(n_table), table,
-                       shared, T, gw, GroupWs{nullptr, nullptr}, err, x, H, xh, xl, xmult);
+                       shared, T, gw, GroupWs{nullptr, nullptr}, err, x, H, xh, xl, xmult, perm ? 1u : 0u);
     hipError_t e;
     const uint32_t kk = static_cast<uint32_t>(k);
     switch (format) {
@@ -997,6 +1003,8 @@ int32_t launch_moe_official_grouped(objeta_hip_context* ctx, hipStream_t s, cons
                                     uint64_t hidden, uint64_t inter, uint64_t out_dim, float limit,
                                     uint8_t* inter_values, uint8_t* inter_scales, const OfficialMarks* marks) {
     const char* action = "launch official FP4 MoE (grouped)";
+    // the routed FP4 and the shared FP8 sets multiply the same split activations
+    static_assert(Tile<Fp4Rows>::kPermuted == Tile<Fp8Rows>::kPermuted, "one activation order for both tiles");
     if (!official_grouped_supported(n_table, n_tokens, k, hidden, inter, out_dim))
         OBJ_FAIL(kUnsupported, action, "shape outside the grouped official path");
     const uint32_t T = static_cast<uint32_t>(n_tokens), A = static_cast<uint32_t>(n_tokens * k);
@@ -1040,7 +1048,8 @@ int32_t launch_moe_official_grouped(objeta_hip_context* ctx, hipStream_t s, cons
     };
     OBJ_TRY(launch_act_quant(s, x, T, H, nullptr, nullptr, xd));
     hipLaunchKernelGGL(moe_prepare_kernel, dim3(1 + T), dim3(256), 0, s, ids, A, static_cast<uint32_t>(n_table), table,
-                       shared, T, gw, shared ? gws : GroupWs{nullptr, nullptr}, err, xd, H, xh, xl, xmult);
+                       shared, T, gw, shared ? gws : GroupWs{nullptr, nullptr}, err, xd, H, xh, xl, xmult,
+                       Tile<Fp4Rows>::kPermuted ? 1u : 0u);
     launch_grouped_products<Fp4Rows, true>(s, gw, xh, xl, xmult, act, H, I, kk, A, limit, true, A, cus);
     OBJ_HIP(hipGetLastError(), action);
     OBJ_TRY(mark(marks ? marks->gate_up_end : nullptr));
@@ -1051,7 +1060,8 @@ int32_t launch_moe_official_grouped(objeta_hip_context* ctx, hipStream_t s, cons
     OBJ_TRY(mark(marks ? marks->shared_gate_up_end : nullptr));
     OBJ_TRY(launch_act_quant(s, act, NR, I, inter_values, inter_scales, act));
     OBJ_TRY(mark(marks ? marks->act_quant_end : nullptr));
-    hipLaunchKernelGGL(moe_split_kernel, dim3(NR), dim3(256), 0, s, act, I, ah, al, amult);
+    hipLaunchKernelGGL(moe_split_kernel, dim3(NR), dim3(256), 0, s, act, I, ah, al, amult,
+                       Tile<Fp4Rows>::kPermuted ? 1u : 0u);
     launch_grouped_products<Fp4Rows, false>(s, gw, ah, al, amult, part, I, O, kk, A, 0.0f, false, A, cus);
     OBJ_HIP(hipGetLastError(), action);
     OBJ_TRY(mark(marks ? marks->down_end : nullptr));
