@@ -339,8 +339,9 @@ constexpr uint32_t kSlab = 16;      // rows per workgroup (one MFMA tile)
 // the E8M0 scales) of columns [c0, c0 + kc), row stride padded by one dword so the
 // lanes of different rows read different banks. kChunkGU / kChunkDn: columns per
 // staged chunk for gate and up together / for down (16 and 8 blocks of 32 for the
-// 4-bit layouts, the widths that measured fastest: narrower chunks keep more
-// workgroups resident; 8 blocks of FP8 bytes fill the same LDS). kTileScale: one
+// block formats, 16 and 16 for split FP4: the widths that measured fastest, as
+// narrower chunks keep more workgroups resident; 8 blocks of FP8 bytes fill the
+// same LDS). kTileScale: one
 // E8M0 byte per 128 x 128 tile (FP8), taken per chunk into a register by
 // tile_scales instead of being staged per row.
 template <class R>
@@ -384,7 +385,7 @@ struct Tile<Fp4Rows> {
     static constexpr bool kPermuted = false;
     static constexpr bool kScales = true;
     static constexpr bool kTileScale = false;
-    static constexpr uint32_t kChunkGU = 512, kChunkDn = 256;
+    static constexpr uint32_t kChunkGU = 512, kChunkDn = 512;
     static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 8; }   // kc / 2 bytes
     static constexpr __host__ __device__ uint32_t sdw(uint32_t kc) { return kc / 128; }  // kc / 32 bytes (kc % 128 == 0)
     static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) {

@@ -510,6 +510,12 @@ hipError_t launch_down_rows(hipStream_t s, const objeta_hip_expert_ptrs* table, 
                 default: return down_fast<R, 1, 4, 2>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
             }
         }
+        // long rows (32 lanes per row, two rows per wave): four rows per lane group, so
+        // each wave's staged activations (inter floats) serve 8 rows instead of 2
+        // (DeepSeek down at one token: 29 -> 21 us); only with the slots spread evenly
+        // over the four SIMDs (with 9 waves the WG waits for the SIMD holding three)
+        if (ch == 1 && lpr >= 32 && sh.kk() % 4 == 0)
+            return down_fast<R, 4, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
         switch (ch) {
             case 1: return down_fast<R, 1, 1, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
             case 2: return down_fast<R, 1, 2, 1>(s, table, ids, wts, act, resid, out, sh, lpr, err, sel);
