@@ -60,16 +60,17 @@ __device__ __forceinline__ void stage_vec_wave(float* __restrict__ dst, const fl
 // pairs lp + c * lpr, c < CH (pairs == CH * lpr). A token has kk slots: k routed
 // ones (ids, sel and wts have stride k) and, when kk > k, the shared expert in
 // slot k; assignment a = t * kk + j indexes the activations.
+// The rows of block `bid` of that grid (the body of moe_gate_up_kernel).
 template <class R, int U, int CH>
-__global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
-    const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
+__device__ __forceinline__ void gate_up_block(
+    uint32_t bid, const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
     uint32_t lpr, uint32_t blocks_per_assign, float limit, uint32_t* __restrict__ err,
     const objeta_hip_expert_ptrs* __restrict__ sel, uint32_t kk, const objeta_hip_expert_ptrs* __restrict__ shared,
     uint32_t official) {
     extern __shared__ float lds[];
-    const uint32_t a = blockIdx.x / blocks_per_assign;
-    const uint32_t rb = blockIdx.x - a * blocks_per_assign;
+    const uint32_t a = bid / blocks_per_assign;
+    const uint32_t rb = bid - a * blocks_per_assign;
     const uint32_t t = a / kk;
     const uint32_t j = a - t * kk;
     const bool is_shared = j >= k;
@@ -138,6 +139,36 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
         if (slot < gs && lp == 0 && r < inter)
             act[static_cast<size_t>(a) * inter + r] = ok ? swiglu(g, v, limit, official) : __builtin_nanf("");
     }
+}
+
+template <class R, int U, int CH>
+__global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
+    const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
+    const float* __restrict__ x, float* __restrict__ act, uint32_t hidden, uint32_t inter, uint32_t k,
+    uint32_t lpr, uint32_t blocks_per_assign, float limit, uint32_t* __restrict__ err,
+    const objeta_hip_expert_ptrs* __restrict__ sel, uint32_t kk, const objeta_hip_expert_ptrs* __restrict__ shared,
+    uint32_t official) {
+    gate_up_block<R, U, CH>(blockIdx.x, table, n_table, ids, x, act, hidden, inter, k, lpr, blocks_per_assign, limit, err,
+                            sel, kk, shared, official);
+}
+
+// The official layer's routed gate/up (format R, kk = k) and its shared expert's
+// (format RS, one slot per token, act rows act_sh) in one launch: blocks
+// [0, nb_routed) are the routed assignments', the rest the shared expert's, so the
+// shared expert's rows stream while the routed ones do (in two launches the second
+// waits for the first).
+template <class R, int U, int CH, class RS, int US, int CHS>
+__global__ __launch_bounds__(kThreads) void moe_gate_up_pair_kernel(
+    const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
+    const float* __restrict__ x, float* __restrict__ act, float* __restrict__ act_sh, uint32_t hidden, uint32_t inter,
+    uint32_t k, uint32_t lpr, uint32_t bpa_routed, uint32_t bpa_shared, uint32_t nb_routed, float limit,
+    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ shared, uint32_t official) {
+    if (blockIdx.x < nb_routed)
+        gate_up_block<R, U, CH>(blockIdx.x, table, n_table, ids, x, act, hidden, inter, k, lpr, bpa_routed, limit, err,
+                                nullptr, k, nullptr, official);
+    else
+        gate_up_block<RS, US, CHS>(blockIdx.x - nb_routed, shared, 1, nullptr, x, act_sh, hidden, inter, 0, lpr,
+                                   bpa_shared, limit, err, nullptr, 1, shared, official);
 }
 
 // -------------------------------------------------------------------- down
@@ -578,6 +609,43 @@ MoeShape shape_of(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidd
 
 }  // namespace
 
+// The official layer's routed FP4 gate/up and its FP8 shared expert's in one launch
+// (moe_gate_up_pair_kernel): the routed rows as launch_gate_up_rows<Fp4Rows> blocks
+// them, the shared expert's one row per slot. Returns false (nothing launched) when a
+// lane would take more than two 64-column chunks of a row (FP8 rows spill there).
+bool launch_gate_up_pair(objeta_hip_context* ctx, hipStream_t s, const objeta_hip_expert_ptrs* table,
+                         const uint32_t* ids, const float* x, float* act, float* act_sh, const MoeShape& sh,
+                         const objeta_hip_expert_ptrs* shared, float limit, hipError_t& e) {
+    const uint32_t pairs = sh.hidden >> 6;
+    const uint32_t lpr = pick_lpr(pairs);
+    if (!fast_shape(sh.hidden) || lpr == 0 || pairs / lpr > 2 ||
+        static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 16 > max_lds(ctx))
+        return false;
+    const uint32_t ch = pairs / lpr, gs = 64 / lpr;
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
+    const uint64_t routed = static_cast<uint64_t>(sh.n_tokens) * sh.k;
+    const bool u2 = routed * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2)) >= 2ull * cus;
+    const uint32_t bpa_r = (sh.inter + kWaves * gs * (u2 ? 2 : 1) - 1) / (kWaves * gs * (u2 ? 2 : 1));
+    const uint32_t bpa_s = (sh.inter + kWaves * gs - 1) / (kWaves * gs);
+    const uint32_t nb_r = static_cast<uint32_t>(routed) * bpa_r;
+    const dim3 grid(nb_r + sh.n_tokens * bpa_s);
+    const size_t lds = static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 4 * sizeof(float);
+#define OBJ_PAIR(U, CH)                                                                                             \
+    hipLaunchKernelGGL((moe_gate_up_pair_kernel<Fp4Rows, U, CH, Fp8Rows, 1, CH>), grid, dim3(kThreads), lds, s, table, \
+                       sh.n_table, ids, x, act, act_sh, sh.hidden, sh.inter, sh.k, lpr, bpa_r, bpa_s, nb_r, limit,     \
+                       ctx->err_word, shared, 1u)
+    if (u2) {
+        if (ch == 1) OBJ_PAIR(2, 1);
+        else OBJ_PAIR(2, 2);
+    } else {
+        if (ch == 1) OBJ_PAIR(1, 1);
+        else OBJ_PAIR(1, 2);
+    }
+#undef OBJ_PAIR
+    e = hipGetLastError();
+    return true;
+}
+
 int32_t launch_moe_gate_up(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const uint32_t* ids, uint64_t n_tokens, uint64_t k, const float* x,
                            float* act, uint64_t hidden, uint64_t inter, float limit,
@@ -730,15 +798,26 @@ int32_t launch_moe_official_fp4(objeta_hip_context* ctx, hipStream_t s, const ob
         return 0;
     };
     OBJ_TRY(launch_act_quant(s, x, n_tokens, hidden, nullptr, nullptr, xd));
-    if (k)
-        OBJ_TRY(launch_moe_gate_up(ctx, OBJETA_HIP_FP4_E2M1, s, table, n_table, ids, n_tokens, k, xd, act, hidden,
-                                   inter, limit, nullptr, nullptr, true));
-    OBJ_TRY(mark(marks ? marks->gate_up_end : nullptr));
-    if (shared) {
-        const hipError_t e = launch_gate_up_rows<Fp8Rows>(s, shared, nullptr, xd, act_sh, ssh, limit, err, cus, nullptr);
-        if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+    // routed and shared gate/up in one launch, unless the executor times them apart
+    bool paired = false;
+    if (k && shared && !marks) {
+        MoeShape rsh = shape_of(n_table, n_tokens, k, hidden, inter, out_dim);
+        rsh.official = true;
+        hipError_t e = hipSuccess;
+        paired = launch_gate_up_pair(ctx, s, table, ids, xd, act, act_sh, rsh, shared, limit, e);
+        if (paired && e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
     }
-    OBJ_TRY(mark(marks ? marks->shared_gate_up_end : nullptr));
+    if (!paired) {
+        if (k)
+            OBJ_TRY(launch_moe_gate_up(ctx, OBJETA_HIP_FP4_E2M1, s, table, n_table, ids, n_tokens, k, xd, act, hidden,
+                                       inter, limit, nullptr, nullptr, true));
+        OBJ_TRY(mark(marks ? marks->gate_up_end : nullptr));
+        if (shared) {
+            const hipError_t e = launch_gate_up_rows<Fp8Rows>(s, shared, nullptr, xd, act_sh, ssh, limit, err, cus, nullptr);
+            if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+        }
+        OBJ_TRY(mark(marks ? marks->shared_gate_up_end : nullptr));
+    }
     if (kk) OBJ_TRY(launch_act_quant(s, act, n_tokens * kk, inter, inter_values, inter_scales, act));
     OBJ_TRY(mark(marks ? marks->act_quant_end : nullptr));
     if (k)
