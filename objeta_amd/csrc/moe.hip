@@ -154,21 +154,21 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_kernel(
 
 // The official layer's routed gate/up (format R, kk = k) and its shared expert's
 // (format RS, one slot per token, act rows act_sh) in one launch: blocks
-// [0, nb_routed) are the routed assignments', the rest the shared expert's, so the
-// shared expert's rows stream while the routed ones do (in two launches the second
-// waits for the first).
+// [0, nb_shared) are the shared expert's (dispatched first: its FP8 rows take the
+// longest per block), the rest the routed assignments', so both stream together (in
+// two launches the second waits for the first).
 template <class R, int U, int CH, class RS, int US, int CHS>
 __global__ __launch_bounds__(kThreads) void moe_gate_up_pair_kernel(
     const objeta_hip_expert_ptrs* __restrict__ table, uint32_t n_table, const uint32_t* __restrict__ ids,
     const float* __restrict__ x, float* __restrict__ act, float* __restrict__ act_sh, uint32_t hidden, uint32_t inter,
-    uint32_t k, uint32_t lpr, uint32_t bpa_routed, uint32_t bpa_shared, uint32_t nb_routed, float limit,
+    uint32_t k, uint32_t lpr, uint32_t bpa_routed, uint32_t bpa_shared, uint32_t nb_shared, float limit,
     uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ shared, uint32_t official) {
-    if (blockIdx.x < nb_routed)
-        gate_up_block<R, U, CH>(blockIdx.x, table, n_table, ids, x, act, hidden, inter, k, lpr, bpa_routed, limit, err,
-                                nullptr, k, nullptr, official);
+    if (blockIdx.x < nb_shared)
+        gate_up_block<RS, US, CHS>(blockIdx.x, shared, 1, nullptr, x, act_sh, hidden, inter, 0, lpr, bpa_shared, limit,
+                                   err, nullptr, 1, shared, official);
     else
-        gate_up_block<RS, US, CHS>(blockIdx.x - nb_routed, shared, 1, nullptr, x, act_sh, hidden, inter, 0, lpr,
-                                   bpa_shared, limit, err, nullptr, 1, shared, official);
+        gate_up_block<R, U, CH>(blockIdx.x - nb_shared, table, n_table, ids, x, act, hidden, inter, k, lpr, bpa_routed,
+                                limit, err, nullptr, k, nullptr, official);
 }
 
 // -------------------------------------------------------------------- down
@@ -627,12 +627,12 @@ bool launch_gate_up_pair(objeta_hip_context* ctx, hipStream_t s, const objeta_hi
     const bool u2 = routed * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2)) >= 2ull * cus;
     const uint32_t bpa_r = (sh.inter + kWaves * gs * (u2 ? 2 : 1) - 1) / (kWaves * gs * (u2 ? 2 : 1));
     const uint32_t bpa_s = (sh.inter + kWaves * gs - 1) / (kWaves * gs);
-    const uint32_t nb_r = static_cast<uint32_t>(routed) * bpa_r;
-    const dim3 grid(nb_r + sh.n_tokens * bpa_s);
+    const uint32_t nb_s = sh.n_tokens * bpa_s;
+    const dim3 grid(static_cast<uint32_t>(routed) * bpa_r + nb_s);
     const size_t lds = static_cast<size_t>(sh.hidden >> 6) * kPad * sizeof(float) + 4 * sizeof(float);
 #define OBJ_PAIR(U, CH)                                                                                             \
     hipLaunchKernelGGL((moe_gate_up_pair_kernel<Fp4Rows, U, CH, Fp8Rows, 1, CH>), grid, dim3(kThreads), lds, s, table, \
-                       sh.n_table, ids, x, act, act_sh, sh.hidden, sh.inter, sh.k, lpr, bpa_r, bpa_s, nb_r, limit,     \
+                       sh.n_table, ids, x, act, act_sh, sh.hidden, sh.inter, sh.k, lpr, bpa_r, bpa_s, nb_s, limit,     \
                        ctx->err_word, shared, 1u)
     if (u2) {
         if (ch == 1) OBJ_PAIR(2, 1);
