@@ -558,7 +558,12 @@ int32_t objeta_hip_fp8_act_fp8_weight_gemv_device(objeta_hip_context* ctx, objet
  * are multiples of 128. d_inter_values [n_tokens*kk][intermediate] and
  * d_inter_scales [n_tokens*kk][intermediate/128] (nullable; kk = k + 1 with a
  * shared expert, else k) receive the intermediates' FP8 codes: rows t*k + j for
- * the routed slots, then n_tokens*k + t for the shared expert. */
+ * the routed slots, then n_tokens*k + t for the shared expert. From 12 tokens
+ * (and up to 1024 (token, slot) assignments over at most 1024 experts) the layer
+ * runs on the grouped-token products of objeta_hip_moe_grouped_device: each selected
+ * expert, and the shared expert, read once per set of up to 8 of its tokens. The
+ * results agree with the per-token kernels within the fp32 tolerance (the sums run
+ * in another order), so an intermediate code near a rounding boundary can differ. */
 int32_t objeta_hip_moe_official_fp4_device(objeta_hip_context* ctx, objeta_hip_stream stream,
                                            const objeta_hip_expert_ptrs* d_table, uint64_t n_table,
                                            const objeta_hip_expert_ptrs* d_shared_fp8, const uint32_t* d_ids,
