@@ -558,7 +558,7 @@ int32_t objeta_hip_fp8_act_fp8_weight_gemv_device(objeta_hip_context* ctx, objet
  * are multiples of 128. d_inter_values [n_tokens*kk][intermediate] and
  * d_inter_scales [n_tokens*kk][intermediate/128] (nullable; kk = k + 1 with a
  * shared expert, else k) receive the intermediates' FP8 codes: rows t*k + j for
- * the routed slots, then n_tokens*k + t for the shared expert. From 12 tokens
+ * the routed slots, then n_tokens*k + t for the shared expert. From 6 tokens
  * (and up to 1024 (token, slot) assignments over at most 1024 experts) the layer
  * runs on the grouped-token products of objeta_hip_moe_grouped_device: each selected
  * expert, and the shared expert, read once per set of up to 8 of its tokens. The

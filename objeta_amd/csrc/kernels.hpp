@@ -68,8 +68,10 @@ int32_t launch_moe_official_fp4(objeta_hip_context* ctx, hipStream_t s, const ob
                                 uint8_t* inter_values, uint8_t* inter_scales, const OfficialMarks* marks);
 
 // The same layer on the grouped-token products (grouped.hip), for batches of at
-// least kOfficialGroupedMinTokens tokens in the grouped path's limits.
-constexpr uint64_t kOfficialGroupedMinTokens = 12;
+// least kOfficialGroupedMinTokens tokens in the grouped path's limits (at the
+// DeepSeek shape the per-token kernels are faster up to 4 tokens, the grouped ones
+// from 6: the per-token path reads the FP8 shared expert once per token).
+constexpr uint64_t kOfficialGroupedMinTokens = 6;
 bool official_grouped_supported(uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden, uint64_t inter,
                                 uint64_t out_dim);
 int32_t launch_moe_official_grouped(objeta_hip_context* ctx, hipStream_t s, const objeta_hip_expert_ptrs* table,

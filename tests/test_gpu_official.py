@@ -340,9 +340,9 @@ def test_official_layer_deepseek_shape(backend, T, k, with_shared):
     check_official(out, q, s, experts, shared, selections, xs, hidden, inter, out_dim)
 
 
-@pytest.mark.parametrize("T,k,with_shared", [(12, 4, True), (33, 3, True), (16, 4, False)])
+@pytest.mark.parametrize("T,k,with_shared", [(6, 4, True), (12, 4, True), (33, 3, True), (16, 4, False)])
 def test_official_layer_batch_grouped(backend, T, k, with_shared):
-    """From 12 tokens on, the layer runs on the grouped-token products: the routed FP4
+    """From 6 tokens on, the layer runs on the grouped-token products: the routed FP4
     experts grouped by expert (about 20 assignments per expert at T=33, so groups span
     several member sets of 8), the FP8 shared expert as one group of all tokens with
     launches of its own. Same bar as the per-token path."""
