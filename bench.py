@@ -485,9 +485,10 @@ def run_deepseek(env: Env, args, seed):
     res = {"hidden": H, "intermediate": I, "experts": E, "shared_experts": 1, "top_k": K, "format": "DeepSeekFp4E2M1",
            "expert_bytes": eb, "path": "objeta_hip_moe_layer_shared_device replayed from a hipGraph: batch 1 on the "
                                        "per-assignment kernels (router, gate/up + SiLU, down + combine, shared "
-                                       "expert last with weight 1), batch 32 on the grouped-token products with the "
-                                       "shared expert as one more group"}
-    for T in (1, 32):
+                                       "expert last with weight 1), batch 4 and 32 on the grouped-token products "
+                                       "(from 2 tokens at this expert size) with the shared expert as one more "
+                                       "group"}
+    for T in (1, 4, 32):
         P = 8
         xs = be.alloc(4 * P * T * H)
         env.fill_gauss(xs.ptr, P * T * H, seed + 10 + T, 1.0)

@@ -344,7 +344,9 @@ int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, obje
  * from 17 tokens on the grouped-token products of objeta_hip_moe_grouped_device
  * whenever that path takes the shape (on MI355X at hidden 2048, 128 experts,
  * top-8 with uniformly spread selections the per-assignment kernels are faster up
- * to 16 tokens, the grouped ones from 18 on). The two agree within the fp32
+ * to 16 tokens, the grouped ones from 18 on). When one expert's three matrices
+ * take 8 MiB or more (hidden 7168, intermediate 2048) the grouped products run
+ * from 2 tokens. The two agree within the fp32
  * tolerance, not bit for bit. No host
  * synchronisation; graph-capturable. No reference counterpart as one call: the
  * reference routes on the host (deepseek_single_layer_moe.rs:687-743) and then

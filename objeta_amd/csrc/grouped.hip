@@ -902,6 +902,16 @@ bool grouped_supported(int32_t format, uint64_t n_table, uint64_t n_tokens, uint
     return format != OBJETA_HIP_FP4_E2M1 || (hidden % 128 == 0 && inter % 128 == 0);
 }
 
+bool grouped_preferred(int32_t format, uint64_t n_tokens, uint64_t hidden, uint64_t inter, uint64_t out_dim) {
+    if (n_tokens >= kGroupedMinTokens) return true;
+    if (n_tokens < 2) return false;
+    // bytes per 32 weights of each format
+    const uint64_t per32 = format == OBJETA_HIP_Q4_0 ? 18 : format == OBJETA_HIP_Q5_0 ? 22
+                         : format == OBJETA_HIP_IQ3_0 ? 14 : 17;
+    const uint64_t bytes = (2 * inter * hidden + out_dim * inter) / 32 * per32;
+    return bytes >= kGroupedLargeExpertBytes;
+}
+
 int32_t launch_moe_grouped(objeta_hip_context* ctx, int32_t format, hipStream_t s, const objeta_hip_expert_ptrs* table,
                            uint64_t n_table, const objeta_hip_expert_ptrs* shared, const uint32_t* ids, const float* wts, uint64_t n_tokens, uint64_t k,
                            const float* x, const float* resid, float* out, uint64_t hidden, uint64_t inter,

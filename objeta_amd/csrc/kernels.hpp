@@ -108,6 +108,14 @@ int32_t launch_gemv_mfma(objeta_hip_context* ctx, hipStream_t s, int32_t format,
 // points (measured on MI355X at hidden 2048, 128 experts, top-8: per-assignment
 // faster at 8 tokens, grouped at 16 and beyond).
 constexpr uint64_t kGroupedMinTokens = 17;
+// From 2 tokens when one expert's three matrices take at least this many bytes: at
+// hidden 7168 / intermediate 2048 (23 MB FP4 experts, a shared expert) the grouped
+// path takes 160 / 258 / 314 us at 2 / 3 / 4 tokens against 218 / 360 / 459 on the
+// per-assignment kernels; the Qwen3-A3B shape's 2.6 MB experts keep the 17-token
+// switch.
+constexpr uint64_t kGroupedLargeExpertBytes = uint64_t(8) << 20;
+// Whether the layer entry points run a batch of n_tokens on the grouped path.
+bool grouped_preferred(int32_t format, uint64_t n_tokens, uint64_t hidden, uint64_t inter, uint64_t out_dim);
 // Whether launch_moe_grouped takes this shape.
 bool grouped_supported(int32_t format, uint64_t n_table, uint64_t n_tokens, uint64_t k, uint64_t hidden,
                        uint64_t inter, uint64_t out_dim);

@@ -971,7 +971,7 @@ int32_t objeta_hip_moe_layer_shared_device(objeta_hip_context* ctx, int32_t form
     if (!d_ids_out || !d_weights_out) OBJ_FAIL(kInvalidInput, "moe_layer_device", "NULL routing output");
     // a batch whose tokens share experts: each selected expert's matrices once for
     // all of its tokens
-    if (out_dim > 0 && n_tokens >= kGroupedMinTokens && d_table &&
+    if (out_dim > 0 && d_table && grouped_preferred(format, n_tokens, hidden, intermediate, out_dim) &&
         grouped_supported(format, n_experts, n_tokens, k, hidden, intermediate, out_dim)) {
         OBJ_TRY(launch_router(ctx, s, d_router_w, d_router_bias, d_x, n_tokens, n_experts, hidden, k, renormalize,
                               d_ids_out, d_weights_out, nullptr, nullptr));

@@ -175,7 +175,8 @@ def _sample_tokens(T):
     return sorted({0, T // 2, T - 1})
 
 
-@pytest.mark.parametrize("T", [1, 32])
+# 4 tokens: the grouped path, which the layer entry takes from 2 tokens at this shape
+@pytest.mark.parametrize("T", [1, 4, 32])
 def test_deepseek_fp4_layer_with_shared_expert(backend, ds_layer, T):
     d = ds_layer
     H, I, E, K = d["H"], d["I"], d["E"], d["K"]
