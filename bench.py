@@ -351,11 +351,13 @@ def run_kernels(env: Env, st: QwenStack, layer_io, reps: int):
 def run_batch(env: Env, st: QwenStack, args, seed):
     """Batches of args.batch and 2 * args.batch tokens through every layer: the layer
     entry point (router, then the grouped-token products from 17 tokens on) against
-    the router followed by the per-assignment kernels on the same selections."""
+    the router followed by the per-assignment kernels, and the router followed by the
+    grouped-token products at every batch size."""
     L, H, E, K, I = st.layers, st.H, st.E, st.K, st.I
     be = env.be
     out = {"path": "objeta_hip_moe_layer_device (router + grouped-token MFMA products from 17 tokens) vs "
-                   "router + objeta_hip_moe_selected_device (per-assignment kernels); one graph per pass of "
+                   "router + objeta_hip_moe_selected_device (per-assignment kernels) vs router + "
+                   "objeta_hip_moe_grouped_device (grouped-token products); one graph per pass of "
                    f"{L} layers"}
     for B in (args.batch, 2 * args.batch):
         xb = be.alloc(4 * B * H)
@@ -364,41 +366,48 @@ def run_batch(env: Env, st: QwenStack, args, seed):
         idsb = be.alloc(4 * L * B * K)
         wtsb = be.alloc(4 * L * B * K)
 
-        def enqueue(layer_entry: bool, B=B, xb=xb, hb=hb, idsb=idsb, wtsb=wtsb):
+        def enqueue(mode: str, B=B, xb=xb, hb=hb, idsb=idsb, wtsb=wtsb):
             for l in range(L):
                 src = xb.addr() if l == 0 else hb.addr()
                 li, lw = idsb.addr(4 * l * B * K), wtsb.addr(4 * l * B * K)
-                if layer_entry:
+                if mode == "entry":
                     env.moe.layer_device(st.fmt, st.tables[l], st.router_w[l], st.router_b[l], K, B, src, src,
                                          hb.addr(), li, lw, H, I, H, stream=env.stream)
+                    continue
+                env.check(env.lib.objeta_hip_router_topk_device(env.ctx, env.stream, st.router_w[l].addr(),
+                                                                st.router_b[l].addr(), src, B, E, H, K, 1, li, lw))
+                if mode == "grouped":
+                    env.moe.grouped_device(st.fmt, st.tables[l], li, lw, B, K, src, src, hb.addr(), H, I, H,
+                                           stream=env.stream)
                 else:
-                    env.check(env.lib.objeta_hip_router_topk_device(env.ctx, env.stream, st.router_w[l].addr(),
-                                                                    st.router_b[l].addr(), src, B, E, H, K, 1, li,
-                                                                    lw))
                     env.moe.selected_device(st.fmt, st.tables[l], li, lw, B, K, src, src, hb.addr(), H, I, H,
                                             stream=env.stream)
 
         res = {}
-        for layer_entry in (True, False):
-            enqueue(layer_entry)
+        for mode in ("entry", "per_assignment", "grouped"):
+            enqueue(mode)
             be.synchronize(env.stream)
-            g = env.capture(lambda le=layer_entry: enqueue(le))
+            g = env.capture(lambda m=mode: enqueue(m))
             for _ in range(3):
                 env.launch(g)
             be.synchronize(env.stream)
             _, per = env.per_step(lambda i: env.launch(g), max(5, args.steps // 20))
-            res[layer_entry] = stats(per)
+            res[mode] = stats(per)
             env.destroy([g])
         ids_all = idsb.download(np.uint32, L * B * K).reshape(L, B * K)
         uniq = [len(set(int(v) for v in ids_all[l])) for l in range(L)]
         ub = sum(uniq) * st.expert_bytes
         out[f"batch{B}"] = {
-            "tokens": B, "us_per_step": rnd(res[True], 1), "us_per_token_layer": round(res[True]["avg"] / (L * B), 3),
-            "per_assignment_us_per_step": rnd(res[False], 1),
-            "speedup_vs_per_assignment": round(res[False]["avg"] / res[True]["avg"], 3),
+            "tokens": B, "us_per_step": rnd(res["entry"], 1),
+            "us_per_token_layer": round(res["entry"]["avg"] / (L * B), 3),
+            "per_assignment_us_per_step": rnd(res["per_assignment"], 1),
+            "grouped_us_per_step": rnd(res["grouped"], 1),
+            "speedup_vs_per_assignment": round(res["per_assignment"]["avg"] / res["entry"]["avg"], 3),
+            "grouped_speedup_vs_per_assignment": round(res["per_assignment"]["avg"] / res["grouped"]["avg"], 3),
             "unique_experts_per_layer": round(sum(uniq) / L, 1), "unique_expert_bytes_per_step": ub,
-            "expert_hbm_gbps": round(ub / (res[True]["avg"] * 1e-6) / 1e9, 1),
-            "per_assignment_expert_hbm_gbps": round(ub / (res[False]["avg"] * 1e-6) / 1e9, 1)}
+            "expert_hbm_gbps": round(ub / (res["entry"]["avg"] * 1e-6) / 1e9, 1),
+            "per_assignment_expert_hbm_gbps": round(ub / (res["per_assignment"]["avg"] * 1e-6) / 1e9, 1),
+            "grouped_expert_hbm_gbps": round(ub / (res["grouped"]["avg"] * 1e-6) / 1e9, 1)}
         for b in (xb, hb, idsb, wtsb):
             b.free()
     return out
