@@ -113,6 +113,24 @@ def test_grouped_out_of_table_id_is_reported(backend):
         assert_moe_close(g[t], orc.selected_moe(fmt, oe, sel[t], xs[t], H, I, O))
 
 
+def test_grouped_all_ids_out_of_table_and_repeated_expert(backend):
+    """The combine runs in the down launch: a token none of whose assignments reaches
+    a set (every id out of the table) still gets its NaN row, and a token that selects
+    one expert twice is counted once per slot."""
+    fmt, E, K, T, H, I, O = Q4, 4, 2, 3, 256, 128, 264  # 264: a last slab of 8 rows
+    experts = make_experts(fmt, E, H, I, O, seed=9, gen="gauss")
+    sel = [[(E + 1, 0.5), (E + 2, 0.5)], [(1, 0.6), (1, 0.4)], [(0, 0.5), (2, 0.5)]]
+    xs = orc.gauss(T * H, 2, 1.0).reshape(T, H)
+    res = np.zeros((T, O), np.float32)
+    g, s, err = run_grouped(backend, fmt, experts, sel, xs, H, I, O, res)
+    assert err & 1
+    assert np.all(np.isnan(g[0]))
+    oe = oracle_experts(fmt, experts)
+    for t in (1, 2):
+        assert_moe_close(g[t], orc.selected_moe(fmt, oe, sel[t], xs[t], H, I, O))
+        assert_moe_close(g[t], s[t])
+
+
 def test_grouped_rejects_unsupported_shapes(backend):
     moe = MoeExecutor(backend)
     experts = make_experts(Q4, 2, 96, 64, 64, seed=1, gen="gauss")
