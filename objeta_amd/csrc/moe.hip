@@ -705,6 +705,41 @@ int32_t launch_moe_down(objeta_hip_context* ctx, int32_t format, hipStream_t s, 
         else if (jw1) jw = 1;
     }
     hipError_t e;
+    // one token with a shared expert as slot k: when the k routed slots spread evenly
+    // over the four SIMDs with four rows per lane group, they run in one launch and the
+    // shared expert is added by a second (out = (resid + routed sum) + shared, the
+    // order of the one-launch form), instead of nine waves of one row each (DeepSeek
+    // shape: 31.9 us in one launch)
+    if (jw == 1 && shared && sh.n_tokens == 1 && sh.k % 4 == 0) {
+        const uint32_t pairs = sh.inter >> 6, lpr = pick_lpr(pairs);
+        if (lpr >= 32 && pairs / lpr == 1) {
+            MoeShape rsh = sh;
+            rsh.shared = nullptr;
+            MoeShape ssh = shape_of(1, 1, 0, 32, inter, out_dim);
+            ssh.shared = shared;
+            const float* act_sh = act + static_cast<size_t>(sh.k) * sh.inter;
+            switch (format) {
+                case OBJETA_HIP_Q4_0:
+                    e = launch_down_rows<QRows<kQ4>>(s, table, ids, wts, act, resid, out, rsh, 1, err, sel);
+                    if (e == hipSuccess) e = launch_down_rows<QRows<kQ4>>(s, shared, nullptr, nullptr, act_sh, out, out, ssh, 1, err, nullptr);
+                    break;
+                case OBJETA_HIP_Q5_0:
+                    e = launch_down_rows<QRows<kQ5>>(s, table, ids, wts, act, resid, out, rsh, 1, err, sel);
+                    if (e == hipSuccess) e = launch_down_rows<QRows<kQ5>>(s, shared, nullptr, nullptr, act_sh, out, out, ssh, 1, err, nullptr);
+                    break;
+                case OBJETA_HIP_IQ3_0:
+                    e = launch_down_rows<QRows<kIQ3>>(s, table, ids, wts, act, resid, out, rsh, 1, err, sel);
+                    if (e == hipSuccess) e = launch_down_rows<QRows<kIQ3>>(s, shared, nullptr, nullptr, act_sh, out, out, ssh, 1, err, nullptr);
+                    break;
+                default:
+                    e = launch_down_rows<Fp4Rows>(s, table, ids, wts, act, resid, out, rsh, 1, err, sel);
+                    if (e == hipSuccess) e = launch_down_rows<Fp4Rows>(s, shared, nullptr, nullptr, act_sh, out, out, ssh, 1, err, nullptr);
+                    break;
+            }
+            if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
+            return 0;
+        }
+    }
     if (jw) {
         switch (format) {
             case OBJETA_HIP_Q4_0: e = launch_down_rows<QRows<kQ4>>(s, table, ids, wts, act, resid, out, sh, jw, err, sel); break;

@@ -182,3 +182,12 @@ def test_layer_batch_runs_grouped_with_shared_expert(backend, fmt, E, K, T, H, I
     scale = float(np.max(np.abs(per)))
     assert float(np.max(np.abs(out - per))) <= 1e-4 * scale
     del keep, keep_s
+
+
+@pytest.mark.parametrize("fmt,K", [(Q4, 4), (Q5, 8), (IQ3, 4), (FP4, 8)])
+def test_layer_one_token_shared_expert_second_down_launch(backend, fmt, K):
+    """One token, intermediate 2048 (32 lanes per row), k % 4 == 0 and a shared
+    expert: the routed down runs four rows per lane group and the shared expert is
+    added by a second launch; the token matches the oracle's routing and selected_moe
+    with the shared expert."""
+    test_layer_batch_runs_grouped_with_shared_expert(backend, fmt, 12, K, 1, 256, 2048, 0.0)
