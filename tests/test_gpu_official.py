@@ -19,6 +19,7 @@ import pytest
 from objeta_amd import ExpertCache, ExpertTable, HipError, MoeExecutor
 from objeta_amd.workloads import fp4_random_expert, fp8_random_expert, fp8_random_tiles, fp4_random_split
 from oracle import oracle as orc
+from tests.ref_fixtures import lcg_draws, reference_fp4_fixture  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
@@ -33,44 +34,6 @@ def _oracle_threads():
 
 
 # ------------------------------------------------------------------ helpers
-def lcg_draws(n: int, seed: int) -> np.ndarray:
-    """The reference tests' rand_next (quant.rs:1519-1524), n draws: state = state *
-    6364136223846793005 + 1442695040888963407 (mod 2^64); (state >> 33) as f32 /
-    u32::MAX as f32 * 2 - 1, all in f32. Vectorised with jump-ahead blocks."""
-    a, c, mask = 6364136223846793005, 1442695040888963407, (1 << 64) - 1
-    blk = 4096
-    A, Cc = np.empty(blk, np.uint64), np.empty(blk, np.uint64)
-    ak, ck = 1, 0
-    for k in range(blk):  # state_{i+k+1} = A[k] * state_i + C[k]
-        ak, ck = (ak * a) & mask, (ck * a + c) & mask
-        A[k], Cc[k] = ak, ck
-    out = np.empty(n, np.uint64)
-    s = np.uint64(seed)
-    with np.errstate(over="ignore"):
-        for i in range(0, n, blk):
-            m = min(blk, n - i)
-            st = A[:m] * s + Cc[:m]
-            out[i:i + m] = st
-            s = st[m - 1]
-    bits = (out >> np.uint64(33)).astype(np.uint32)
-    return (bits.astype(F32) / F32(4294967295.0)) * F32(2.0) - F32(1.0)
-
-
-def reference_fp4_fixture(rows: int, cols: int, seed: int):
-    """make_fp8_act_fp4_wt_fixture (quant.rs:1517-1540): the activation (cols draws *
-    100, quantized by cpu_act_quant), packed nibbles ((|r| * 15) as u8 for lo then hi)
-    and scales (127u8.saturating_add((r * 10) as i8 as u8))."""
-    r = lcg_draws(cols + rows * cols + rows * cols // 32, seed)
-    x = r[:cols] * F32(100.0)
-    nib = (np.abs(r[cols:cols + rows * cols]) * F32(15.0)).astype(np.uint8)
-    packed = ((nib[1::2] << 4) | (nib[0::2] & 15)).astype(np.uint8)
-    t = np.trunc(r[cols + rows * cols:] * F32(10.0)).astype(np.int64)
-    wrapped = (np.clip(t, -128, 127) & 0xFF).astype(np.int64)
-    scales = np.minimum(127 + wrapped, 255).astype(np.uint8)
-    av, asc = orc.act_quant(x)
-    return av, asc, packed, scales, x
-
-
 def assert_gemv_close(out, ref):
     out, ref = np.asarray(out, F32), np.asarray(ref, F32)
     assert np.array_equal(np.isnan(out), np.isnan(ref))
