@@ -1136,6 +1136,7 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
                                   OBJETA_HIP_TENSOR_SHARED_UP_WEIGHT,   OBJETA_HIP_TENSOR_SHARED_UP_SCALE,
                                   OBJETA_HIP_TENSOR_SHARED_DOWN_WEIGHT, OBJETA_HIP_TENSOR_SHARED_DOWN_SCALE};
         const void* p[6] = {};
+        uint64_t sz[6] = {};
         int q = 0;
         for (; q < 6 && rc == 0; ++q) {
             const Key key{layer_id, 0, kinds[q], OBJETA_HIP_FP4_E2M1};
@@ -1145,7 +1146,25 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
             b->refs += 1;
             st.held.push_back({cache, b});
             p[q] = b->ptr;
-            sh_cached_bytes += cache->map.find(key)->second.size;
+            sz[q] = cache->map.find(key)->second.size;
+            sh_cached_bytes += sz[q];
+        }
+        if (rc == 0 && q == 6) {
+            // the FP8 shared expert of this shape: E4M3 codes [rows][cols] and E8M0
+            // scales on the 128 x 128 tile grid; entries preloaded for another shape
+            // would be read past their ends
+            const uint64_t ti = (intermediate + 127) / 128, th = (hidden + 127) / 128, to = (out_dim + 127) / 128;
+            const uint64_t want[6] = {intermediate * hidden, ti * th, intermediate * hidden, ti * th,
+                                      out_dim * intermediate, to * ti};
+            const char* names[6] = {"gate weight", "gate scale", "up weight", "up scale", "down weight", "down scale"};
+            for (int i = 0; i < 6 && rc == 0; ++i)
+                if (sz[i] != want[i])
+                    rc = set_error(kInvalidInput, __FILE__, __LINE__, __func__, "resolve cached shared expert",
+                                   strf("layer %llu shared %s holds %llu bytes, expected %llu for hidden %llu, "
+                                        "intermediate %llu, out_dim %llu",
+                                        (unsigned long long)layer_id, names[i], (unsigned long long)sz[i],
+                                        (unsigned long long)want[i], (unsigned long long)hidden,
+                                        (unsigned long long)intermediate, (unsigned long long)out_dim));
         }
         if (rc == 0 && q == 6) {
             h_tab[k] = {p[0], p[2], p[4], p[1], p[3], p[5]};

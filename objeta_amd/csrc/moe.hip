@@ -514,8 +514,7 @@ hipError_t launch_gate_up_rows(hipStream_t s, const objeta_hip_expert_ptrs* tabl
         switch (ch) {
             case 1: return u2 ? gate_up_fast<R, 2, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel)
                               : gate_up_fast<R, 1, 1>(s, table, ids, x, act, sh, lpr, limit, err, sel);
-            case 2: return u2 ? gate_up_fast<R, 2, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel)
-                              : gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel);
+            case 2: return gate_up_fast<R, 1, 2>(s, table, ids, x, act, sh, lpr, limit, err, sel);
             case 3: return gate_up_fast<R, 1, 3>(s, table, ids, x, act, sh, lpr, limit, err, sel);
             default: return gate_up_fast<R, 1, 4>(s, table, ids, x, act, sh, lpr, limit, err, sel);
         }
@@ -626,7 +625,8 @@ bool launch_gate_up_pair(objeta_hip_context* ctx, hipStream_t s, const objeta_hi
     const uint32_t ch = pairs / lpr, gs = 64 / lpr;
     const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
     const uint64_t routed = static_cast<uint64_t>(sh.n_tokens) * sh.k;
-    const bool u2 = routed * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2)) >= 2ull * cus;
+    // two rows per slot only with one chunk per lane, as in launch_gate_up_rows
+    const bool u2 = routed * ((sh.inter + kWaves * gs * 2 - 1) / (kWaves * gs * 2)) >= 2ull * cus && ch == 1;
     const uint32_t bpa_r = (sh.inter + kWaves * gs * (u2 ? 2 : 1) - 1) / (kWaves * gs * (u2 ? 2 : 1));
     const uint32_t bpa_s = (sh.inter + kWaves * gs - 1) / (kWaves * gs);
     const uint32_t nb_s = sh.n_tokens * bpa_s;
@@ -636,13 +636,9 @@ bool launch_gate_up_pair(objeta_hip_context* ctx, hipStream_t s, const objeta_hi
     hipLaunchKernelGGL((moe_gate_up_pair_kernel<Fp4Rows, U, CH, Fp8Rows, 1, CH>), grid, dim3(kThreads), lds, s, table, \
                        sh.n_table, ids, x, act, act_sh, sh.hidden, sh.inter, sh.k, lpr, bpa_r, bpa_s, nb_s, limit,     \
                        ctx->err_word, shared, 1u)
-    if (u2) {
-        if (ch == 1) OBJ_PAIR(2, 1);
-        else OBJ_PAIR(2, 2);
-    } else {
-        if (ch == 1) OBJ_PAIR(1, 1);
-        else OBJ_PAIR(1, 2);
-    }
+    if (u2) OBJ_PAIR(2, 1);
+    else if (ch == 1) OBJ_PAIR(1, 1);
+    else OBJ_PAIR(1, 2);
 #undef OBJ_PAIR
     e = hipGetLastError();
     return true;

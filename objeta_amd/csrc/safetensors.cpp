@@ -483,6 +483,17 @@ void fill_info(const Tensor& t, objeta_hip_st_info* out) {
 
 const void* data_of(const objeta_hip_st_model* m, const Tensor& t) { return m->files[t.file].base + t.offset; }
 
+// The expert tensors are one byte per element (I8/U8 nibble pairs, F8_E4M3 codes,
+// F8_E8M0 scales): a tensor must hold exactly as many bytes as its shape has
+// elements, or the kernels would read past the end of a truncated tensor.
+int32_t check_byte_count(const Tensor& t, const char* action, const char* what) {
+    if (t.nbytes != t.nelem)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("%s: %llu bytes for %llu one-byte elements", what, (unsigned long long)t.nbytes,
+                      (unsigned long long)t.nelem));
+    return 0;
+}
+
 std::string shape_str(const std::vector<uint64_t>& s) {
     std::string r = "[";
     for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
@@ -667,6 +678,8 @@ int32_t objeta_hip_st_deepseek_expert(const objeta_hip_st_model* m, uint64_t lay
             OBJ_FAIL(kInvalidInput, "validate fp4 expert tensor",
                      strf("%s scale: dtype %s shape %s, expected F8_E8M0 [%llu, %llu]", kinds[k], dtype_name(s.dtype),
                           shape_str(s.shape).c_str(), (unsigned long long)rows, (unsigned long long)(cols / 32)));
+        OBJ_TRY(check_byte_count(w, "validate fp4 expert tensor", (std::string(kinds[k]) + " weight").c_str()));
+        OBJ_TRY(check_byte_count(s, "validate fp4 expert tensor", (std::string(kinds[k]) + " scale").c_str()));
         dims[k][0] = rows;
         dims[k][1] = cols;
     }
@@ -724,6 +737,8 @@ int32_t objeta_hip_st_deepseek_shared_expert(const objeta_hip_st_model* m, uint6
                      strf("%s scale: dtype %s shape %s, expected F8_E8M0 [%llu, %llu]", kinds[k], dtype_name(s.dtype),
                           shape_str(s.shape).c_str(), (unsigned long long)((rows + 127) / 128),
                           (unsigned long long)((cols + 127) / 128)));
+        OBJ_TRY(check_byte_count(w, "validate shared expert tensor", (std::string(kinds[k]) + " weight").c_str()));
+        OBJ_TRY(check_byte_count(s, "validate shared expert tensor", (std::string(kinds[k]) + " scale").c_str()));
         dims[k][0] = rows;
         dims[k][1] = cols;
     }

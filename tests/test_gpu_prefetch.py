@@ -169,3 +169,27 @@ def test_preload_shared_and_official_executor_from_cache(backend):
     assert cache.stats()["miss_count"] - m0 == 12 + 1  # two routed experts' six tensors, then one shared key
     assert tg["shared_fp8_bytes_reused"] == 0 and tg["shared_fp8_bytes_loaded"] > 0
     cache.close()
+
+
+def test_official_executor_rejects_cached_shared_expert_of_another_shape(backend):
+    """Shared entries preloaded for intermediate 256 and an executor call at 384: the
+    cached blocks are shorter than the kernels would read, so the call fails with
+    InvalidInput before any launch, and a call at the preloaded shape still works."""
+    from objeta_amd import HipError
+
+    hidden, inter, out_dim = 512, 256, 512
+    cache = ExpertCache(1 << 30, backend)
+    cache.preload_shared([fp8_random_expert(hidden, inter, out_dim, 91)])
+    moe = MoeExecutor(backend)
+    x = orc.gauss(hidden, 13, 1.0)
+    wide = [fp4_random_expert(hidden, 384, out_dim, 400 + e) for e in range(2)]
+    with pytest.raises(HipError) as e:
+        moe.execute_selected_moe_official_routed_fp4(None, None, wide, [(0, 0.5), (1, 0.5)], x, hidden, 384, out_dim,
+                                                     0, cache, None, 10.0, shared_from_cache=True)
+    assert e.value.status == 5 and "shared gate weight holds 131072 bytes, expected 196608" in str(e.value)
+    narrow = [fp4_random_expert(hidden, inter, out_dim, 500 + e) for e in range(2)]
+    got, _ = moe.execute_selected_moe_official_routed_fp4(None, None, narrow, [(0, 0.5), (1, 0.5)], x, hidden, inter,
+                                                          out_dim, 0, cache, None, 10.0, shared_from_cache=True)
+    assert np.isfinite(got).all()
+    assert moe.device_error() == 0
+    cache.close()

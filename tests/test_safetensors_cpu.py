@@ -255,6 +255,28 @@ def test_deepseek_lookup_errors_follow_the_reference(tmp_path):
     assert "gate scale" in str(e.value)
 
 
+@pytest.mark.parametrize("name,kind", [("layers.0.ffn.experts.1.w2.weight", "routed"),
+                                       ("layers.0.ffn.experts.2.w1.scale", "routed"),
+                                       ("layers.0.ffn.shared_experts.w3.weight", "shared"),
+                                       ("layers.0.ffn.shared_experts.w2.scale", "shared")])
+def test_truncated_expert_tensor_fails_before_use(tmp_path, name, kind):
+    """A tensor whose data holds fewer bytes than its shape has one-byte elements (a
+    truncated checkpoint) is rejected by the expert lookups, so no kernel is handed a
+    block shorter than the shape it reads."""
+    t = deepseek_checkpoint(tmp_path / "ok.safetensors", layers=(0,), mtp=False)
+    dtype, shape, data = t[name]
+    t[name] = (dtype, shape, data[:-1])
+    write_mock(tmp_path / "trunc.safetensors", t)
+    m = ModelWeights(tmp_path / "trunc.safetensors")
+    with pytest.raises(HipError) as e:
+        if kind == "routed":
+            m.deepseek_expert(0, int(name.split(".")[4]))
+        else:
+            m.deepseek_shared_expert(0)
+    assert e.value.status == 5 and "one-byte elements" in str(e.value)  # OBJETA_HIP_ERR_INVALID_INPUT
+    assert f"{len(data) - 1} bytes for {len(data)}" in str(e.value)
+
+
 def test_views_keep_the_mapping_alive(tmp_path):
     p = tmp_path / "ds.safetensors"
     t = deepseek_checkpoint(p, layers=(0,), mtp=False)
