@@ -661,6 +661,60 @@ int32_t objeta_hip_moe_execute_official_fp4(objeta_hip_context* ctx, objeta_hip_
                                             const objeta_hip_expert_ptrs* shared_fp8, int32_t shared_from_cache,
                                             float swiglu_limit, float* out, objeta_hip_moe_telemetry* tel);
 
+/* One layer of a cached decode stack: its routed experts in host memory (pinned,
+ * so that cache misses copy asynchronously) and its router on the device. */
+typedef struct {
+    const objeta_hip_host_expert* experts; /* [n_experts] */
+    uint64_t n_experts;
+    const float* d_router_w;    /* [n_experts][hidden] device */
+    const float* d_router_bias; /* [n_experts] device, or NULL */
+    uint64_t layer_id;          /* the layer of the cache keys */
+} objeta_hip_cached_layer;
+
+/* Accounting of one objeta_hip_moe_stack_cached call, summed over its layers.
+ * logical = loaded + reused (the byte invariant of moe.rs:743-748, per layer over
+ * the union of the batch's selected experts). */
+typedef struct {
+    uint64_t layers;
+    uint64_t tokens;
+    uint64_t logical_expert_bytes_requested;
+    uint64_t actual_expert_bytes_loaded;  /* copied on the copy stream for the layers' own selections */
+    uint64_t resident_cache_bytes_reused; /* cache hits, prefetched tensors included */
+    uint64_t distinct_experts;            /* sum over layers of the union's size */
+    uint64_t prefetch_experts_predicted;  /* (token, slot) predictions made for the next layer */
+    uint64_t prefetch_experts_correct;    /* of those, selected by the next layer's router */
+    uint64_t prefetch_tensors_issued;     /* tensors copied ahead by the predictions */
+    uint64_t prefetch_bytes_issued;
+    float total_ms;     /* the call's work on its stream, first router to last layer */
+    float copy_ms;      /* copy-stream time of the layers' own misses */
+    float host_wait_ms; /* host time blocked on the routers' results */
+    float reserved;
+} objeta_hip_stack_telemetry;
+
+/* A decode stack with the experts behind the expert cache: n_tokens tokens through
+ * n_layers layers, the hidden state d_h [n_tokens][hidden] updated in place (h +=
+ * MoE(h) per layer, the residual stream). No counterpart in the reference as one
+ * call: it is the loop its drivers run over execute_selected_moe_cuda
+ * (moe.rs:352-751; bench_selected_moe.rs:292-299, deepseek_single_layer_moe.rs
+ * 2160-2207) with the hidden state kept on the device. Per layer: the router on
+ * the device (softmax -> top-k, renormalised when renormalize != 0), its ids to the
+ * host, the cache resolving the union of the batch's selected experts (get, then
+ * insert with a copy on the copy stream for misses: the reference's admission and
+ * counters), and the expert kernels waiting for that layer's copies only; batches
+ * of 17 tokens and more run the grouped-token products. prefetch_next != 0 also
+ * evaluates layer l+1's router on layer l's input and starts copying its predicted
+ * experts' absent tensors behind layer l's own (objeta_hip_cache_prefetch).
+ * ids_out / weights_out (host, [n_layers][n_tokens][k], nullable) receive the
+ * selections; d_trace (device, [n_layers][n_tokens][hidden], nullable) the hidden
+ * state after each layer. Returns after the last layer completed. Experts of every
+ * layer are validated against (hidden, intermediate) before any launch. */
+int32_t objeta_hip_moe_stack_cached(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                    const objeta_hip_cached_layer* layers, uint64_t n_layers, uint64_t k,
+                                    int32_t renormalize, uint64_t n_tokens, float* d_h, uint64_t hidden,
+                                    uint64_t intermediate, objeta_hip_expert_cache* cache, int32_t prefetch_next,
+                                    uint32_t* ids_out, float* weights_out, float* d_trace,
+                                    objeta_hip_stack_telemetry* tel);
+
 /* ------------------------------------------------------ checkpoint ingest */
 /* Memory-mapped safetensors files: ModelWeights (crates/objeta-parser/src/lib.rs:
  * 88-293). A path names one file or a directory whose *.safetensors shards are

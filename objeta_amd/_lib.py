@@ -87,6 +87,18 @@ class MoeTelemetry(C.Structure):
                 [(n, U64) for n in _TEL_U64_TAIL])
 
 
+class CachedLayer(C.Structure):
+    _fields_ = [("experts", P), ("n_experts", U64), ("d_router_w", P), ("d_router_bias", P), ("layer_id", U64)]
+
+
+class StackTelemetry(C.Structure):
+    _fields_ = [(n, U64) for n in (
+        "layers", "tokens", "logical_expert_bytes_requested", "actual_expert_bytes_loaded",
+        "resident_cache_bytes_reused", "distinct_experts", "prefetch_experts_predicted", "prefetch_experts_correct",
+        "prefetch_tensors_issued", "prefetch_bytes_issued")] + [(n, F32) for n in (
+        "total_ms", "copy_ms", "host_wait_ms", "reserved")]
+
+
 class QGemvTelemetry(C.Structure):
     _fields_ = [("h2d_ms", F32), ("kernel_ms", F32), ("d2h_ms", F32), ("unaccounted_ms", F32),
                 ("total_ms", F32), ("effective_gbps", F32), ("bytes_read", U64)]
@@ -172,6 +184,7 @@ SIGNATURES = {
     "objeta_hip_moe_execute_official_fp4": (I32, [P, P, P, U64, P, P, U64, P, U64, U64, U64, U64, U64, P, P,
                                                   I32, F32, P, P]),
     "objeta_hip_cache_prefetch": (I32, [P, P, P, P, U64, P]),
+    "objeta_hip_moe_stack_cached": (I32, [P, I32, P, P, U64, U64, I32, U64, P, U64, U64, P, I32, P, P, P, P]),
     "objeta_hip_cache_preload_shared": (I32, [P, P, U64, U64, P, P, P]),
     "objeta_hip_st_open": (I32, [C.c_char_p, P]),
     "objeta_hip_st_close": (I32, [P]),

@@ -634,6 +634,31 @@ def _telemetry_moe(t: MoeTelemetry) -> dict:
     return d
 
 
+def _moe_stack_cached(self, fmt, layers, k: int, n_tokens: int, d_h, hidden: int, inter: int,
+                      cache: "ExpertCache | None" = None, prefetch_next: bool = False, renormalize: bool = True,
+                      d_trace=None, stream=None):
+    """objeta_hip_moe_stack_cached: n_tokens tokens through len(layers) layers with the
+    experts behind the cache, the hidden state d_h updated in place. layers = [(host
+    experts or HostExpertSet, d_router_w, d_router_bias or None, layer_id)]. Returns
+    (ids [L][T][k], weights [L][T][k], telemetry dict)."""
+    from ._lib import CachedLayer, StackTelemetry
+    sets = [lay[0] if isinstance(lay[0], HostExpertSet) else HostExpertSet(lay[0]) for lay in layers]
+    arr = (CachedLayer * len(layers))()
+    for i, (lay, hs) in enumerate(zip(layers, sets)):
+        _, w, b, lid = lay
+        arr[i] = CachedLayer(C.cast(hs.arr, C.c_void_p), hs.n, _addr(w).value, None if b is None else _addr(b).value,
+                             lid)
+    L = len(layers)
+    ids = np.zeros((L, n_tokens, k), np.uint32)
+    ws = np.zeros((L, n_tokens, k), np.float32)
+    tel = StackTelemetry()
+    check(self.L.objeta_hip_moe_stack_cached(
+        self.backend.ctx, int(fmt), stream, arr, L, k, 1 if renormalize else 0, n_tokens, _addr(d_h), hidden, inter,
+        cache.h if cache is not None else None, 1 if prefetch_next else 0, ids.ctypes.data_as(C.c_void_p),
+        ws.ctypes.data_as(C.c_void_p), _addr_or_none(d_trace), C.byref(tel)))
+    return ids, ws, {n: getattr(tel, n) for n, _ in StackTelemetry._fields_ if n != "reserved"}
+
+
 class HostExpertSet:
     """A layer's host expert tensors marshalled once for the executor entry points
     (the reference passes &[ExpertWeights]; rebuilding the C array on every call costs
@@ -731,5 +756,6 @@ MoeExecutor.execute_selected_moe_official_routed_fp4 = _moe_execute_official_fp4
 MoeExecutor.execute_selected_moe_official_routed_fp4_cuda = _moe_execute_official_fp4
 MoeExecutor.execute_selected_moe = _moe_execute_selected
 MoeExecutor.execute_selected_moe_cuda = _moe_execute_selected
+MoeExecutor.stack_cached = _moe_stack_cached
 MoeExecutor.execute_selected_moe_native_fp4 = _moe_execute_native_fp4
 MoeExecutor.execute_selected_moe_native_fp4_cuda = _moe_execute_native_fp4

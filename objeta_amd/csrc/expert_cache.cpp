@@ -1261,3 +1261,220 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
     return 0;
     OBJ_GUARD_END
 }
+
+// ------------------------------------------------------------ cached decode stack
+// The loop the reference's drivers run over execute_selected_moe_cuda, with the
+// hidden state on the device: per layer one host wait (the router's ids), the
+// union of the batch's experts resolved through the cache, the layer's kernels
+// behind its own copies. Scratch (device and pinned host, one layout):
+// [ids | weights | predicted ids | predicted weights | remapped ids | table].
+extern "C" int32_t objeta_hip_moe_stack_cached(objeta_hip_context* ctx, int32_t format, objeta_hip_stream stream,
+                                               const objeta_hip_cached_layer* layers, uint64_t n_layers, uint64_t k,
+                                               int32_t renormalize, uint64_t n_tokens, float* d_h, uint64_t hidden,
+                                               uint64_t intermediate, objeta_hip_expert_cache* cache,
+                                               int32_t prefetch_next, uint32_t* ids_out, float* weights_out,
+                                               float* d_trace, objeta_hip_stack_telemetry* tel) {
+    OBJ_GUARD_BEGIN
+    using namespace objeta;
+    const char* action = "moe_stack_cached";
+    OBJ_TRY(check_ctx(ctx, action));
+    if (format < OBJETA_HIP_Q4_0 || format > OBJETA_HIP_FP4_E2M1)
+        OBJ_FAIL(kUnsupported, action, strf("unsupported MoE format %d", format));
+    if (cache && cache->ctx && cache->ctx != ctx) OBJ_FAIL(kInvalidInput, action, "cache belongs to another context");
+    if (tel) *tel = objeta_hip_stack_telemetry{};
+    if (n_layers == 0 || n_tokens == 0) return 0;
+    if (!layers || !d_h) OBJ_FAIL(kInvalidInput, action, "NULL layers or hidden state");
+    if (k == 0 || k > 32) OBJ_FAIL(kInvalidInput, action, strf("k %llu must be in 1..=32", (unsigned long long)k));
+    if (n_tokens > 256) OBJ_FAIL(kInvalidInput, action, "at most 256 tokens per call");
+    if (hidden == 0 || intermediate == 0 || hidden % 32 || intermediate % 32)
+        OBJ_FAIL(kInvalidInput, action,
+                 strf("hidden %llu and intermediate %llu must be non-zero multiples of block_size 32",
+                      (unsigned long long)hidden, (unsigned long long)intermediate));
+    const bool fp4 = format == OBJETA_HIP_FP4_E2M1;
+    const int32_t bb = objeta_hip_block_bytes(format);
+    const uint64_t gu_w = fp4 ? intermediate * (hidden / 2) : intermediate * (hidden / 32) * bb;
+    const uint64_t gu_s = fp4 ? intermediate * (hidden / 32) : 0;
+    const uint64_t dn_w = fp4 ? hidden * (intermediate / 2) : hidden * (intermediate / 32) * bb;
+    const uint64_t dn_s = fp4 ? hidden * (intermediate / 32) : 0;
+    // every layer's experts against the shape, before anything is enqueued
+    for (uint64_t l = 0; l < n_layers; ++l) {
+        const objeta_hip_cached_layer& L = layers[l];
+        if (!L.experts || !L.d_router_w)
+            OBJ_FAIL(kInvalidInput, action, strf("layer %llu: NULL experts or router", (unsigned long long)l));
+        if (L.n_experts < k)
+            OBJ_FAIL(kInvalidInput, action,
+                     strf("layer %llu: %llu experts for top-%llu", (unsigned long long)l,
+                          (unsigned long long)L.n_experts, (unsigned long long)k));
+        std::vector<uint64_t> all(L.n_experts);
+        for (uint64_t e = 0; e < L.n_experts; ++e) all[e] = e;
+        OBJ_TRY(validate_selected(L.experts, L.n_experts, all.data(), L.n_experts, fp4, gu_w, gu_s, dn_w, dn_s));
+    }
+    OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = resolve_stream(ctx, stream);
+    const uint64_t T = n_tokens, tk = n_tokens * k;
+    auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
+    const size_t o_ids = 0, o_w = up(tk * 4), o_pids = o_w + up(tk * 4), o_pw = o_pids + up(tk * 4);
+    const size_t o_rids = o_pw + up(tk * 4), o_tab = o_rids + up(tk * 4);
+    const size_t total = o_tab + tk * sizeof(objeta_hip_expert_ptrs);
+    void* dws = nullptr;
+    OBJ_TRY(ensure_workspace(ctx, s, kWsStack, total, &dws));
+    void* hst = nullptr;
+    OBJ_TRY(ensure_host_stage(ctx, total, &hst));
+    char* d0 = static_cast<char*>(dws);
+    char* h0 = static_cast<char*>(hst);
+    uint32_t* d_ids = reinterpret_cast<uint32_t*>(d0 + o_ids);
+    float* d_w = reinterpret_cast<float*>(d0 + o_w);
+    uint32_t* d_pids = reinterpret_cast<uint32_t*>(d0 + o_pids);
+    float* d_pw = reinterpret_cast<float*>(d0 + o_pw);
+    const uint32_t* d_rids = reinterpret_cast<const uint32_t*>(d0 + o_rids);
+    const objeta_hip_expert_ptrs* d_tab = reinterpret_cast<const objeta_hip_expert_ptrs*>(d0 + o_tab);
+    const uint32_t* h_ids = reinterpret_cast<const uint32_t*>(h0 + o_ids);
+    const float* h_w = reinterpret_cast<const float*>(h0 + o_w);
+    const uint32_t* h_pids = reinterpret_cast<const uint32_t*>(h0 + o_pids);
+    uint32_t* h_rids = reinterpret_cast<uint32_t*>(h0 + o_rids);
+    objeta_hip_expert_ptrs* h_tab = reinterpret_cast<objeta_hip_expert_ptrs*>(h0 + o_tab);
+
+    const size_t ev_t0 = 0, ev_t1 = 1, ev_route = 2, ev_c = 3;  // then (c0, c1) per layer
+    EventSet evs(3 + 2 * n_layers);
+    OBJ_TRY(evs.create());
+    hipEvent_t* ev = evs.e.data();
+    objeta_hip_stack_telemetry t{};
+    t.layers = n_layers;
+    t.tokens = T;
+    double wait_ms = 0.0;
+    std::vector<uint32_t> predicted;  // this layer's experts as the previous layer predicted them
+    std::vector<uint64_t> uni;
+    std::vector<char> seen;
+    OBJ_HIP(hipEventRecord(ev[ev_t0], s), "record event");
+    for (uint64_t l = 0; l < n_layers; ++l) {
+        const objeta_hip_cached_layer& L = layers[l];
+        const bool pf = prefetch_next && cache && cache->ctx && l + 1 < n_layers;
+        // ---- routing: this layer's router, and the next layer's on the same input
+        OBJ_TRY(launch_router(ctx, s, L.d_router_w, L.d_router_bias, d_h, T, L.n_experts, hidden, k, renormalize,
+                              d_ids, d_w, nullptr, nullptr));
+        if (pf) {
+            const objeta_hip_cached_layer& N = layers[l + 1];
+            OBJ_TRY(launch_router(ctx, s, N.d_router_w, N.d_router_bias, d_h, T, N.n_experts, hidden, k, renormalize,
+                                  d_pids, d_pw, nullptr, nullptr));
+        }
+        OBJ_HIP(hipMemcpyAsync(h0, d0, pf ? o_rids : o_pids, hipMemcpyDeviceToHost, s), "stack_ids_d2h");
+        OBJ_HIP(hipEventRecord(ev[ev_route], s), "record event");
+        const auto w0 = std::chrono::steady_clock::now();
+        OBJ_HIP(hipEventSynchronize(ev[ev_route]), "wait for the router");
+        wait_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - w0).count();
+        for (uint64_t i = 0; i < tk; ++i)
+            if (h_ids[i] >= L.n_experts)
+                OBJ_FAIL(kInternal, action, strf("router id %u out of range at layer %llu", h_ids[i],
+                                                 (unsigned long long)l));
+        if (ids_out) std::memcpy(ids_out + l * tk, h_ids, tk * 4);
+        if (weights_out) std::memcpy(weights_out + l * tk, h_w, tk * 4);
+        if (!predicted.empty()) {  // the previous layer's prediction of these selections, per token
+            for (uint64_t tt = 0; tt < T; ++tt)
+                for (uint64_t a = 0; a < k; ++a)
+                    for (uint64_t b = 0; b < k; ++b)
+                        if (predicted[tt * k + a] == h_ids[tt * k + b]) {
+                            t.prefetch_experts_correct += 1;
+                            break;
+                        }
+            t.prefetch_experts_predicted += tk;
+        }
+        // ---- the union of the batch's experts through the cache
+        uni.assign(h_ids, h_ids + tk);
+        std::sort(uni.begin(), uni.end());
+        uni.erase(std::unique(uni.begin(), uni.end()), uni.end());
+        for (uint64_t i = 0; i < tk; ++i)
+            h_rids[i] = static_cast<uint32_t>(std::lower_bound(uni.begin(), uni.end(), h_ids[i]) - uni.begin());
+        hipEvent_t c0 = ev[ev_c + 2 * l], c1 = ev[ev_c + 2 * l + 1];
+        OBJ_HIP(hipEventRecord(c0, ctx->copy_stream), "record event");
+        StagedExperts st;
+        int32_t rc = stage_selected(ctx, cache, L.experts, uni.data(), uni.size(), format, L.layer_id, true, s, h_tab,
+                                    st);
+        if (rc == 0 && hipEventRecord(c1, ctx->copy_stream) != hipSuccess) {
+            (void)hipGetLastError();
+            rc = set_error(kDriver, __FILE__, __LINE__, __func__, "record event", "copy-stream event failed");
+        }
+        // ---- the next layer's predicted experts, copied behind this layer's misses
+        if (rc == 0 && pf) {
+            const objeta_hip_cached_layer& N = layers[l + 1];
+            predicted.assign(h_pids, h_pids + tk);
+            seen.assign(N.n_experts, 0);
+            for (uint64_t i = 0; i < tk && rc == 0; ++i) {
+                const uint32_t p = h_pids[i];
+                if (p >= N.n_experts || seen[p]) continue;
+                seen[p] = 1;
+                TensorRef tr[6];
+                const int nt = tensors_of(N.experts[p], fp4, tr);
+                for (int q = 0; q < nt && rc == 0; ++q) {
+                    const Key key{N.layer_id, p, tr[q].kind, format};
+                    if (cache->map.count(key) || tr[q].len > cache->st.capacity_bytes) continue;
+                    Block* b = nullptr;
+                    if ((rc = stage_tensor(cache, tr[q].h, tr[q].len, nullptr, &b))) break;
+                    if (!insert_block(cache, key, b, tr[q].len)) {
+                        retire_block(cache, b);
+                        continue;
+                    }
+                    t.prefetch_tensors_issued += 1;
+                    t.prefetch_bytes_issued += tr[q].len;
+                }
+            }
+        } else {
+            predicted.clear();
+        }
+        // ---- the layer, after its own copies
+        do {
+            if (rc) break;
+            hipError_t e = hipMemcpyAsync(d0 + o_rids, h0 + o_rids,
+                                          (o_tab - o_rids) + uni.size() * sizeof(objeta_hip_expert_ptrs),
+                                          hipMemcpyHostToDevice, s);
+            for (size_t j = 0; j < uni.size() && e == hipSuccess; ++j)
+                if (st.ready[j]) e = hipStreamWaitEvent(s, st.ready[j], 0);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                rc = set_error(kDriver, __FILE__, __LINE__, __func__, "stack_table_h2d", hipGetErrorString(e));
+                break;
+            }
+            if (grouped_preferred(format, T, hidden, intermediate, hidden) &&
+                grouped_supported(format, uni.size(), T, k, hidden, intermediate, hidden)) {
+                rc = launch_moe_grouped(ctx, format, s, d_tab, uni.size(), nullptr, d_rids, d_w, T, k, d_h, d_h, d_h,
+                                        hidden, intermediate, hidden, 0.f);
+            } else {
+                float* act = nullptr;
+                if ((rc = moe_act_scratch(ctx, s, T, k, intermediate, &act))) break;
+                rc = launch_moe_gate_up(ctx, format, s, d_tab, uni.size(), d_rids, T, k, d_h, act, hidden,
+                                        intermediate, 0.f);
+                if (!rc)
+                    rc = launch_moe_down(ctx, format, s, d_tab, uni.size(), d_rids, d_w, T, k, act, d_h, d_h,
+                                         intermediate, hidden);
+            }
+            if (rc == 0 && d_trace) {
+                e = hipMemcpyAsync(d_trace + l * T * hidden, d_h, T * hidden * 4, hipMemcpyDeviceToDevice, s);
+                if (e != hipSuccess) {
+                    (void)hipGetLastError();
+                    rc = set_error(kDriver, __FILE__, __LINE__, __func__, "stack_trace_d2d", hipGetErrorString(e));
+                }
+            }
+        } while (false);
+        // the blocks stay valid for the kernels enqueued above: a block evicted from
+        // now on is fenced behind them before it is reused
+        st.release();
+        if (rc) {
+            (void)hipStreamSynchronize(s);
+            (void)hipStreamSynchronize(ctx->copy_stream);
+            return rc;
+        }
+        t.logical_expert_bytes_requested += st.logical;
+        t.actual_expert_bytes_loaded += st.w_loaded + st.s_loaded;
+        t.resident_cache_bytes_reused += st.w_reused + st.s_reused;
+        t.distinct_experts += uni.size();
+    }
+    OBJ_HIP(hipEventRecord(ev[ev_t1], s), "record event");
+    OBJ_HIP(hipEventSynchronize(ev[ev_t1]), "wait for the stack");
+    if (t.logical_expert_bytes_requested != t.actual_expert_bytes_loaded + t.resident_cache_bytes_reused)
+        OBJ_FAIL(kInternal, "MoE byte invariant", "logical_expert_bytes_requested != loaded + reused");
+    t.total_ms = elapsed(ev[ev_t0], ev[ev_t1]);
+    for (uint64_t l = 0; l < n_layers; ++l) t.copy_ms += elapsed(ev[ev_c + 2 * l], ev[ev_c + 2 * l + 1]);
+    t.host_wait_ms = static_cast<float>(wait_ms);
+    if (tel) *tel = t;
+    return 0;
+    OBJ_GUARD_END
+}

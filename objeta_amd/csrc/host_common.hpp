@@ -79,7 +79,8 @@ enum WsSlot : int {
     kWsSelTab = 4,
     kWsOfficial = 5,  // dequantized FP8 activations of the official path
     kWsGemv = 6,      // split activations and partial sums of the batched MFMA GEMV
-    kWsSlots = 7
+    kWsStack = 7,     // routing results and expert tables of the cached decode stack
+    kWsSlots = 8
 };
 
 // The scratch of one stream. Calls on different streams of a context may be in
