@@ -20,14 +20,18 @@ Also measured in the same run (each in its own object of the JSON line):
   per-assignment kernels;
 - gemv: Q4_0 [1024 x 4096] batch 1, and Q4_0 / Q5_0 / IQ3_0 at [4096 x 4096] and
   [14336 x 4096], batch 1 and 8, each over a >= 4 GB rotated working set;
+- stack4: the 4-layer x 8-expert top-2 Q4_0 stack (hidden 2048, intermediate 1024),
+  batch 1, over >= 4 GB of rotated replicas (its 113 MB would sit in the MALL);
 - deepseek: one H 7168 / 256 routed + 1 shared / top-8 / I 2048 FP4 layer at
   batch 1 and 32;
 - official: the same routed experts through the FP8-activation ("official
   arithmetic") layer with an FP8 shared expert, batch 1 and 32;
 - router: the router alone at the DeepSeek and Qwen3-A3B shapes for 1 to 32 tokens;
-- misses: the headline stack through the host-in/host-out executor with the expert
-  cache at 25% of the expert bytes, experts in pinned host memory: end-to-end
-  us/token including the PCIe copies of the misses, and the copies' GB/s;
+- misses: the headline stack with the experts in pinned host memory behind the
+  expert cache at 25% of the expert bytes (objeta_hip_moe_stack_cached), batch 1
+  and a 16-token batch, without and with next-layer prefetch: end-to-end us per
+  token including the PCIe copies of the misses, against the PCIe floor of the
+  bytes loaded;
 - cpu_baseline: the oracle's C restatement of the reference CPU path
   (cpu_router + selected_moe_cpu) on the box's host cores, one pinned core and all
   cores, median of 5 runs over a bounded sample of the same layers.
@@ -58,7 +62,7 @@ from objeta_amd.workloads import zipf_bias  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 ROTATE_BYTES = 4 << 30  # working set of the rotated GEMV measurements (>> 256 MB MALL)
-SECTIONS = ("headline", "kernels", "batch", "gemv", "deepseek", "official", "router", "misses", "cpu")
+SECTIONS = ("headline", "kernels", "batch", "gemv", "stack4", "deepseek", "official", "router", "misses", "cpu")
 # not in the default run: kernels of known traffic for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE
 EXTRA_SECTIONS = ("calibrate",)
 TRAFFIC_PROFILE = "profiles/moe_layer_q4_qwen3a3b_hbm_traffic.md"
@@ -528,6 +532,77 @@ def run_deepseek(env: Env, args, seed):
     return res
 
 
+# ------------------------------------------- four-layer eight-expert stack
+def run_stack4(env: Env, args, seed):
+    """The 4-layer x 8-expert top-2 Q4_0 stack (hidden 2048, intermediate 1024, W_r
+    [8 x 2048] ~N(0, 0.02), softmax -> top-2 -> renormalised, batch 1). The whole model
+    is 113 MB and would sit in the 256 MB MALL, so it is replicated over >= 4 GB (the
+    generated layers copied into every replica) and step i runs one token through the
+    four layers of replica i mod R: the expert bytes come from HBM. One hipGraph per
+    replica (12 launches: router, gate/up, down per layer)."""
+    from objeta_amd import ExpertTable
+    be = env.be
+    L, H, E, K, I = 4, 2048, 8, 2, 1024
+    gu = I * (H // 32) * 18
+    dn = H * (I // 32) * 18
+    eb = 2 * gu + dn
+    model = L * (E * eb + 4 * E * H)
+    R = max(1, -(-ROTATE_BYTES // model))
+    arena = be.alloc(R * model)
+    layer_b = E * eb + 4 * E * H
+    for l in range(L):
+        base = arena.ptr + l * layer_b
+        for e in range(E):
+            env.fill_q(0, base + e * eb, 2 * I, H, seed + 100 * l + 3 * e)
+            env.fill_q(0, base + e * eb + 2 * gu, H, I, seed + 100 * l + 3 * e + 2)
+        env.fill_gauss(base + E * eb, E * H, seed + 100 * l + 99, 0.02)
+    for r in range(1, R):
+        env.check(env.lib.objeta_hip_copy_d2d(env.ctx, env.stream, arena.addr(r * model), arena.addr(), model))
+    be.synchronize(env.stream)
+    tables = []
+    for r in range(R):
+        row = []
+        for l in range(L):
+            base = arena.ptr + r * model + l * layer_b
+            row.append((ExpertTable(be, [(base + e * eb, base + e * eb + gu, base + e * eb + 2 * gu)
+                                         for e in range(E)]), base + E * eb))
+        tables.append(row)
+    P = 16
+    xs = be.alloc(4 * P * H)
+    env.fill_gauss(xs.ptr, P * H, seed + 7, 1.0)
+    h = be.alloc(4 * H)
+    ids, wts = be.alloc(4 * L * K), be.alloc(4 * L * K)
+
+    def enq(r):
+        x0 = xs.addr(4 * (r % P) * H)
+        for l in range(L):
+            src = x0 if l == 0 else h.addr()
+            tab, wr = tables[r][l]
+            env.moe.layer_device(0, tab, C.c_void_p(wr), None, K, 1, src, src, h.addr(), ids.addr(4 * l * K),
+                                 wts.addr(4 * l * K), H, I, H, stream=env.stream)
+    enq(0)
+    be.synchronize(env.stream)
+    graphs = [env.capture(lambda r=r: enq(r)) for r in range(R)]
+    for i in range(min(R, 10)):
+        env.launch(graphs[i])
+    be.synchronize(env.stream)
+    steps = max(2 * R, args.steps)
+    total, per = env.per_step(lambda i: env.launch(graphs[i % R]), steps)
+    env.destroy(graphs)
+    s = stats(per)
+    tok_us = total / steps
+    layer_bytes = K * eb
+    arena.free()
+    return {"layers": L, "hidden": H, "experts": E, "top_k": K, "intermediate": I, "format": "Q4_0",
+            "expert_bytes": eb, "expert_bytes_per_layer": layer_bytes, "replicas": R,
+            "rotated_bytes": R * model,
+            "path": "objeta_hip_moe_layer_device per layer (router, gate/up + SiLU, down + combine), one hipGraph "
+                    "per replica",
+            "us_per_token": round(tok_us, 3), "us_per_token_stats": rnd(s), "us_per_layer": round(tok_us / L, 3),
+            "expert_hbm_gbps": round(L * layer_bytes / (tok_us * 1e-6) / 1e9, 1),
+            "expert_hbm_frac_of_peak": round(L * layer_bytes / (tok_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 # ------------------------------------------------------------- router alone
 def run_router(env: Env, args, seed):
     """objeta_hip_router_topk_device alone at the DeepSeek (256 experts, hidden 7168)
@@ -646,13 +721,19 @@ def run_official(env: Env, args, seed):
 
 # ------------------------------------------------------------- cache misses
 def run_misses(env: Env, st: QwenStack, args, xs, P, report):
-    """The stack through the host-in/host-out executor with the expert cache at 25% of
-    the expert bytes and every expert in pinned host memory; routing on the device.
-    Two runs from an empty cache: the executor alone, and with a speculative
-    cross-layer prefetch (after layer l's call, layer l+1's router evaluated on layer
-    l's input predicts its experts, whose absent tensors start copying while the host
-    routes layer l+1)."""
-    from objeta_amd import ExpertCache, ExpertCacheKey, ExpertTensorKind, HostExpertSet, PinnedHostBuffer, QuantFormat
+    """The stack with every expert in pinned host memory behind the expert cache at 25%
+    of the expert bytes, through objeta_hip_moe_stack_cached: per layer the router on
+    the device, its ids to the host once, the union of the step's selected experts
+    resolved by the cache (misses copied on the copy stream), the layer's kernels after
+    its own copies; the hidden state stays on the device. Batch 1 and a 16-token batch,
+    each from an empty cache, without and with next-layer prefetch (layer l+1's router
+    evaluated on layer l's input; its predicted experts' absent tensors copied behind
+    layer l's misses). Two warm-up steps fill the cache; then `miss_tokens` steps are
+    timed end to end on the host clock. The PCIe floor of a step is its loaded bytes at
+    the rate of a 256 MiB pinned-host copy measured in the same run. With a report
+    directory, a few tokens also go through execute_selected_moe_cuda per layer (the
+    reference's executor, host x in and host out) for the MoeStatsReport."""
+    from objeta_amd import ExpertCache, HostExpertSet, PinnedHostBuffer
     be = env.be
     L, H, E, K, I = st.layers, st.H, st.E, st.K, st.I
     eb = st.expert_bytes
@@ -672,7 +753,7 @@ def run_misses(env: Env, st: QwenStack, args, xs, P, report):
                 host[base + d:base + d + st.dn_bytes])
     experts = [[tensors(l, e) for e in range(E)] for l in range(L)]
     sets = [HostExpertSet(experts[l]) for l in range(L)]
-    kinds = (ExpertTensorKind.Gate, ExpertTensorKind.Up, ExpertTensorKind.Down)
+    layers = [(sets[l], st.router_w[l], st.router_b[l], l) for l in range(L)]
     # PCIe probe: one 256 MiB pinned -> device copy
     probe = be.alloc(256 << 20)
     ev0, ev1 = env.event(), env.event()
@@ -684,76 +765,82 @@ def run_misses(env: Env, st: QwenStack, args, xs, P, report):
     env.drop_events([ev0, ev1])
     probe.free()
     capacity = (L * E * eb) // 4
-    d_h = be.alloc(4 * H)
-    d_ids, d_w = be.alloc(4 * K), be.alloc(4 * K)
-    p_ids, p_w = be.alloc(4 * K), be.alloc(4 * K)
-    n_tok = args.miss_tokens
+    n_steps = args.miss_tokens
 
-    def route(l, ids, ws):
-        env.check(env.lib.objeta_hip_router_topk_device(env.ctx, None, st.router_w[l].addr(), st.router_b[l].addr(),
-                                                        d_h.addr(), 1, E, H, K, 1, ids.addr(), ws.addr()))
-
-    def run(prefetch: bool):
+    def run(T: int, prefetch: bool):
         cache = ExpertCache(capacity, be)
-        tok_us, h2d_ms, loaded, logical, tel_runs, last = [], 0.0, 0, 0, [], None
-        predicted, correct, issued = 0, 0, 0
-        pred_next = None
-        for t in range(n_tok + 2):  # two warm-up tokens fill the cache
-            h = xs.download(np.float32, H, offset=4 * (t % P) * H)
+        d_h = be.alloc(4 * T * H)
+        wall, tels = [], []
+        for step in range(n_steps + 2):
+            for t in range(T):
+                env.check(env.lib.objeta_hip_copy_d2d(env.ctx, env.stream, d_h.addr(4 * t * H),
+                                                      xs.addr(4 * ((step * T + t) % P) * H), 4 * H))
             c0 = time.perf_counter()
-            for l in range(L):
-                d_h.upload(h)
-                route(l, d_ids, d_w)
-                if prefetch and l + 1 < L:
-                    route(l + 1, p_ids, p_w)  # layer l+1's router on layer l's input
-                ids = d_ids.download(np.uint32, K)
-                ws = d_w.download(np.float32, K)
-                if pred_next is not None and t >= 2:
-                    predicted += K
-                    correct += len(set(int(i) for i in ids) & pred_next)
-                sel = [(int(i), float(w)) for i, w in zip(ids, ws)]
-                out, tel = env.moe.execute_selected_moe_cuda(None, None, sets[l], sel, h, H, I, H, l, cache)
-                pred_next = None
-                if prefetch and l + 1 < L:
-                    pred = [int(i) for i in p_ids.download(np.uint32, K)]
-                    pred_next = set(pred)
-                    issued += cache.prefetch([(ExpertCacheKey(l + 1, e, kd, QuantFormat.Q4_0), a)
-                                              for e in pred for kd, a in zip(kinds, experts[l + 1][e])])
-                last = (l, sel, h.copy(), out.copy())
-                h = (h + out).astype(np.float32)
-                if t >= 2:
-                    h2d_ms += tel["h2d_ms"]
-                    loaded += tel["actual_expert_bytes_loaded"]
-                    logical += tel["logical_expert_bytes_requested"]
-                    tel_runs.append(tel)
-            if t >= 2:
-                tok_us.append((time.perf_counter() - c0) * 1e6)
+            _, _, tel = env.moe.stack_cached(0, layers, K, T, d_h, H, I, cache=cache, prefetch_next=prefetch,
+                                             stream=env.stream)
+            if step >= 2:
+                wall.append((time.perf_counter() - c0) * 1e6)
+                tels.append(tel)
         cst = cache.stats()
         cache.close()
-        s = stats(tok_us)
-        res = {"us_per_token_end_to_end": rnd(s, 1), "us_per_token_layer": round(s["avg"] / L, 2),
+        d_h.free()
+        s = stats(wall)
+        loaded = sum(t["actual_expert_bytes_loaded"] for t in tels) / len(tels)
+        logical = sum(t["logical_expert_bytes_requested"] for t in tels) / len(tels)
+        pf_bytes = sum(t["prefetch_bytes_issued"] for t in tels) / len(tels)
+        copy_ms = sum(t["copy_ms"] for t in tels) / len(tels)
+        floor_us = (loaded + pf_bytes) / (probe_gbps * 1e9) * 1e6
+        res = {"tokens_per_step": T, "us_per_step_end_to_end": rnd(s, 1), "us_per_token": round(s["avg"] / T, 1),
+               "us_per_token_layer": round(s["avg"] / T / L, 2),
                "hit_rate_bytes": round(1.0 - loaded / logical, 4) if logical else None,
-               "expert_bytes_loaded_per_token": loaded // max(1, n_tok),
-               "pcie_gbps_on_misses": round(loaded / (h2d_ms * 1e-3) / 1e9, 1) if h2d_ms > 0 else None,
+               "expert_bytes_loaded_per_step": int(loaded), "prefetch_bytes_per_step": int(pf_bytes),
+               "distinct_experts_per_layer": round(sum(t["distinct_experts"] for t in tels) / len(tels) / L, 1),
+               "pcie_floor_us_per_step": round(floor_us, 1),
+               "end_to_end_over_pcie_floor": round(s["avg"] / floor_us, 3) if floor_us > 0 else None,
+               "copy_stream_gbps": round((loaded / (copy_ms * 1e-3) / 1e9), 1) if copy_ms > 0 else None,
+               "host_wait_ms_per_step": round(sum(t["host_wait_ms"] for t in tels) / len(tels), 3),
+               "device_ms_per_step": round(sum(t["total_ms"] for t in tels) / len(tels), 3),
                "cache": {k: cst[k] for k in ("hit_count", "miss_count", "eviction_count", "resident_bytes",
                                               "cache_insert_accept_count")}}
         if prefetch:
-            res["prediction_accuracy"] = round(correct / predicted, 4) if predicted else None
-            res["prefetch_tensors_issued_per_token"] = round(issued / (n_tok + 2), 1)
-        return res, tel_runs, last
+            pred = sum(t["prefetch_experts_predicted"] for t in tels)
+            res["prediction_accuracy"] = round(sum(t["prefetch_experts_correct"] for t in tels) / pred, 4) if pred else None
+        return res
 
-    base, tel_runs, last = run(False)
-    pre, _, _ = run(True)
-    res = {"tokens": n_tok, "layers": L, "cache_capacity_bytes": capacity, "expert_bytes_total": L * E * eb,
-           **base, "pcie_probe_gbps": round(probe_gbps, 1), "host_staging_s": round(stage_s, 1),
-           "path": "router on the device, ids to the host, execute_selected (host x in, host out), one call per "
-                   "layer; host experts marshalled once per layer (HostExpertSet)",
-           "with_prefetch": pre}
+    res = {"layers": L, "cache_capacity_bytes": capacity, "expert_bytes_total": L * E * eb, "steps": n_steps,
+           "pcie_probe_gbps": round(probe_gbps, 1), "host_staging_s": round(stage_s, 1),
+           "path": "objeta_hip_moe_stack_cached: router on the device, ids to the host once per layer, the union of "
+                   "the step's experts resolved through the 25% cache (misses copied on the copy stream from pinned "
+                   "host memory), the layer's kernels after its own copies; hidden state on the device"}
+    for T in (1, args.batch):
+        res[f"batch{T}"] = run(T, False)
+        res[f"batch{T}_prefetch"] = run(T, True)
     if report is not None:
+        # the reference's executor, one call per layer, for the MoeStatsReport
+        cache = ExpertCache(capacity, be)
+        d_h = be.alloc(4 * H)
+        d_ids, d_w = be.alloc(4 * K), be.alloc(4 * K)
+        tel_runs, last = [], None
+        for t in range(3):
+            h = xs.download(np.float32, H, offset=4 * (t % P) * H)
+            for l in range(L):
+                d_h.upload(h)
+                env.check(env.lib.objeta_hip_router_topk_device(env.ctx, None, st.router_w[l].addr(),
+                                                                st.router_b[l].addr(), d_h.addr(), 1, E, H, K, 1,
+                                                                d_ids.addr(), d_w.addr()))
+                ids = d_ids.download(np.uint32, K)
+                ws = d_w.download(np.float32, K)
+                sel = [(int(i), float(w)) for i, w in zip(ids, ws)]
+                out, tel = env.moe.execute_selected_moe_cuda(None, None, sets[l], sel, h, H, I, H, l, cache)
+                last = (l, sel, h.copy(), out.copy())
+                h = (h + out).astype(np.float32)
+                if t >= 1:
+                    tel_runs.append(tel)
+        cache.close()
         report["moe_tel"] = tel_runs
         report["moe_shape"] = (H, I, H, K)
         report["moe_last"] = last
-    del experts, host, sets
+    del experts, host, sets, layers
     pin.free()
     return res
 
@@ -923,7 +1010,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20251201)
     ap.add_argument("--batch", type=int, default=16, help="tokens of the batched side measurement")
     ap.add_argument("--kernel-reps", type=int, default=10, help="replays of each kernel's rotation graph")
-    ap.add_argument("--miss-tokens", type=int, default=16, help="tokens timed through the 25%% cache")
+    ap.add_argument("--miss-tokens", type=int, default=16, help="steps timed through the 25%% cache (each of 1 and --batch tokens)")
     ap.add_argument("--cpu-layers", type=int, default=8, help="layer calls in the CPU-baseline sample")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--sections", default=",".join(SECTIONS), help="comma list of " + ", ".join(SECTIONS))
@@ -972,6 +1059,10 @@ def main() -> int:
     if "gemv" in sections:
         stage("gemv")
         gemv = run_gemv(env, max(8, args.kernel_reps // 4), gemv_checks if args.report_dir else None)
+    stack4 = None
+    if "stack4" in sections:
+        stage("stack4")
+        stack4 = run_stack4(env, args, args.seed + 3000)
     deepseek = None
     if "deepseek" in sections:
         stage("deepseek")
@@ -1037,6 +1128,7 @@ def main() -> int:
         "kernels": kernels,
         "batch": batch,
         "gemv": gemv,
+        "stack4": stack4,
         "deepseek": deepseek,
         "official": official,
         "router": router,

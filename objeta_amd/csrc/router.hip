@@ -40,6 +40,7 @@ __device__ void router_select(const float* __restrict__ w_r, const float* __rest
                               objeta_hip_expert_ptrs* sel_tab = nullptr) {
     __shared__ SelectLds<kMaxExperts> s;
     __shared__ int s_pending;
+    stage_exptab(s);  // the softmax exps' table, in LDS before the ranking needs it
     for (uint32_t spin = 0;; ++spin) {
         if (threadIdx.x == 0) s_pending = 0;
         __syncthreads();
@@ -89,13 +90,16 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
     const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 
     if (e < n_experts) {
+        // the bias requested without a branch (a load under `if (bias)` is waited for at
+        // the branch's end, before the row loads), its value selected where it is used
+        const float bias_raw = *(bias ? bias + e : w_r);
         const float* row = w_r + static_cast<size_t>(e) * hidden;
         double total, abs_prefix;
         if constexpr (VEC) exact_logit_vec(row, xt, hidden, lane, total, abs_prefix);
         else exact_logit_scalar(row, xt, hidden, lane, total, abs_prefix);
         if (lane == 0) {
             float lhat, bnd;
-            finish_logit(total, abs_prefix, bias, e, hidden, lhat, bnd);
+            finish_logit(total, abs_prefix, bias ? bias_raw : 0.0f, hidden, lhat, bnd);
             __hip_atomic_store(&ws_logit[e], tag(lhat, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&ws_bound[e], tag(bnd, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -129,6 +133,9 @@ __global__ __launch_bounds__(kRThreads) void router_lanes_kernel(
     const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     const uint32_t n4 = hidden >> 8;  // float4 per lane
     const uint32_t ec = e < n_experts ? e : n_experts - 1;
+    // the bias requested without a branch (a load under `if (bias)` is waited for at the
+    // branch's end, before the row loads), its value selected where it is used
+    const float bias_raw = *(bias ? bias + ec : w_r);
     float4 wr[NB];
     {
         typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -149,7 +156,7 @@ __global__ __launch_bounds__(kRThreads) void router_lanes_kernel(
         exact_logit_lanes<NB>(wr, xs, n4, lane, total, abs_bound);
         if (lane == 0) {
             float lhat, bnd;
-            finish_logit(total, abs_bound, bias, e, hidden, lhat, bnd);
+            finish_logit(total, abs_bound, bias ? bias_raw : 0.0f, hidden, lhat, bnd);
             __hip_atomic_store(&ws_logit[e], tag(lhat, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&ws_bound[e], tag(bnd, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -197,6 +204,9 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
     uint64_t* ws_bound = ws_logit + kMaxExperts;
     const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     const uint32_t n4 = hidden >> 10;  // float4 per lane
+    // the bias requested without a branch (a load under `if (bias)` is waited for at the
+    // branch's end, before the row loads), its value selected where it is used
+    const float bias_raw = *(bias ? bias + e : w_r);
     // the lane's row elements and the matching activations, straight into registers
     float4 wr[NB], xv[NB];
     {
@@ -217,16 +227,23 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
     exact_logit_split<NB>(wr, xv, n4, lane, wave, red, total, abs_bound);
     if (threadIdx.x == 0) {
         float lhat, bnd;
-        finish_logit(total, abs_bound, bias, e, hidden, lhat, bnd);
+        finish_logit(total, abs_bound, bias ? bias_raw : 0.0f, hidden, lhat, bnd);
         __hip_atomic_store(&ws_logit[e], tag(lhat, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&ws_bound[e], tag(bnd, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (blockIdx.x != 0) return;
-    // workgroup 0 selects; x in LDS serves the recomputation of close calls (staged
-    // while the other workgroups still publish), the table its resolution
-    for (uint32_t i = threadIdx.x; i < (hidden >> 2); i += kRThreads) {
-        const uint32_t c = i << 2;
-        *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = reinterpret_cast<const float4*>(xt)[i];
+    // workgroup 0 selects; x in LDS serves the recomputation of close calls (written
+    // from the registers that hold it for the logit: the lanes' float4s cover all of
+    // x), the table its resolution
+    {
+        const uint32_t q0 = wave * n4 * 64u + lane * n4;
+#pragma unroll
+        for (int g = 0; g < NB; ++g) {
+            if (static_cast<uint32_t>(g) < n4) {
+                const uint32_t c = (q0 + static_cast<uint32_t>(g)) << 2;
+                *reinterpret_cast<float4*>(xs + (c >> 6) * kPadX + (c & 63)) = xv[g];
+            }
+        }
     }
     const uint32_t x_floats = (hidden / 64) * kPadX;
     auto* tab_lds = reinterpret_cast<objeta_hip_expert_ptrs*>(xs + x_floats + kRefineScratch);
@@ -266,6 +283,9 @@ __global__ __launch_bounds__(kRThreads) void router_logits_batch_kernel(
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t n4 = hidden >> 10;  // float4 per lane
     const uint32_t q0 = wave * n4 * 64u + lane * n4;
+    // the bias requested without a branch (a load under `if (bias)` is waited for at the
+    // branch's end, before the row loads), its value selected where it is used
+    const float bias_raw = *(bias ? bias + e : w_r);
     float4 wr[NB], xv[NB], xn[NB];
     auto load_x = [&](uint32_t t, float4 (&dst)[NB]) {
         const gptr<f32x4> x4 = as_global(reinterpret_cast<const f32x4*>(x + static_cast<size_t>(t) * hidden));
@@ -294,7 +314,7 @@ __global__ __launch_bounds__(kRThreads) void router_logits_batch_kernel(
             const uint32_t epoch = __hip_atomic_load(&counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
             uint64_t* ws_logit = ws + static_cast<size_t>(t) * 2 * kMaxExperts;
             float lhat, bnd;
-            finish_logit(total, abs_bound, bias, e, hidden, lhat, bnd);
+            finish_logit(total, abs_bound, bias ? bias_raw : 0.0f, hidden, lhat, bnd);
             __hip_atomic_store(&ws_logit[e], tag(lhat, epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&ws_logit[kMaxExperts + e], tag(bnd, epoch), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);

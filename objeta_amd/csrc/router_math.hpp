@@ -48,7 +48,10 @@ static __device__ const uint64_t kExpTab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-__device__ __forceinline__ float expf_glibc(float x) {
+// The table is read per lane at an index that depends on x; a caller on a latency
+// path passes a copy staged in LDS (tab), others read the file-scope table.
+template <class Tab>
+__device__ __forceinline__ float expf_glibc_tab(float x, Tab tab) {
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {  // |x| >= 88, inf or nan
@@ -65,13 +68,17 @@ __device__ __forceinline__ float expf_glibc(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd = __dsub_rn(kd, kShift);
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    const double sc = __builtin_bit_cast(double, kExpTab[ki % 32] + (ki << 47));
+    const double sc = __builtin_bit_cast(double, tab[ki % 32] + (ki << 47));
     const double z = __builtin_fma(kC0, r, kC1);
     const double r2 = __dmul_rn(r, r);
     double y = __builtin_fma(kC2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return static_cast<float>(__dmul_rn(y, sc));
 }
+
+__device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_tab(x, kExpTab); }
+
+typedef const __attribute__((address_space(3))) uint64_t* LdsTab;
 
 // Wave-wide double scans through DPP row shifts and lane reads, not shuffles: a
 // shuffle goes through the LDS crossbar (over 100 cycles a step, 12 dependent
@@ -273,9 +280,9 @@ constexpr uint32_t kSpinLimit = 1u << 20;  // bounded waits (about a second), th
 // ------------------------------------------------------------ logits and bounds
 // Rounds the exact sum to the logit the device reports and bounds its distance to
 // the reference's sequential fp32 logit (+ bias), for one expert.
-__device__ __forceinline__ void finish_logit(double total, double abs_prefix, const float* bias, uint32_t e,
-                                             uint32_t hidden, float& lhat, float& bnd) {
-    const double b = bias ? static_cast<double>(bias[e]) : 0.0;
+__device__ __forceinline__ void finish_logit(double total, double abs_prefix, float bias_e, uint32_t hidden,
+                                             float& lhat, float& bnd) {
+    const double b = static_cast<double>(bias_e);
     lhat = static_cast<float>(total + b);
     const double u = 5.9604644775390625e-08;  // 2^-24
     const double n = static_cast<double>(hidden);
@@ -488,7 +495,19 @@ struct SelectLds {
     int need[MAXE];
     int nlist[64];
     int ncount;
+    uint64_t exptab[32];  // kExpTab staged by the selecting workgroup (stage_exptab)
 };
+
+// Copies kExpTab into s.exptab; visible after the caller's next barrier.
+template <int MAXE>
+__device__ __forceinline__ void stage_exptab(SelectLds<MAXE>& s) {
+    if (threadIdx.x < 32) s.exptab[threadIdx.x] = kExpTab[threadIdx.x];
+}
+
+template <int MAXE>
+__device__ __forceinline__ LdsTab exptab_of(const SelectLds<MAXE>& s) {
+    return (LdsTab)(s.exptab);
+}
 
 // With s.val / s.bnd holding all n logits and bounds (visible to the block):
 // ranks the experts and checks that every decision the top-k depends on is
@@ -560,11 +579,11 @@ __device__ bool select_certain(SelectLds<MAXE>& s, uint32_t n, uint32_t k, int r
     float z = 1.0f;
     if (!renormalize) {
         float part = 0.0f;
-        for (uint32_t j = tid; j < n; j += kRThreads) part += expf_glibc(__fsub_rn(s.val[j], mx));
+        for (uint32_t j = tid; j < n; j += kRThreads) part += expf_glibc_tab(__fsub_rn(s.val[j], mx), exptab_of(s));
         z = block_sum(part, s.red);
     }
     if (tid < k) {
-        const float ev = expf_glibc(__fsub_rn(s.sv[tid], mx));
+        const float ev = expf_glibc_tab(__fsub_rn(s.sv[tid], mx), exptab_of(s));
         s.e[tid] = renormalize ? ev : __fdiv_rn(ev, z);
     }
     __syncthreads();
@@ -752,7 +771,7 @@ __device__ void softmax_rank(SelectLds<MAXE>& s, uint32_t n, uint32_t k) {
     for (uint32_t j = threadIdx.x; j < n; j += kRThreads) mx = fmaxf(mx, s.val[j]);
     mx = block_max(mx, s.red);
     for (uint32_t j = threadIdx.x; j < n; j += kRThreads)
-        s.bnd[j] = expf_glibc(__fsub_rn(s.val[j], mx));
+        s.bnd[j] = expf_glibc_tab(__fsub_rn(s.val[j], mx), exptab_of(s));
     __syncthreads();
     if (threadIdx.x == 0) {
         float sum = 0.0f;
