@@ -638,64 +638,121 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
 // ------------------------------------------------------ batched GEMV on MFMA
 // y[b][r] = sum_c W[r][c] x[b][c] for up to 8 vectors at once: the grouped
 // products' down form with the matrix as the one expert and the vectors as the
-// members, so every weight is decoded once for all of them. A workgroup covers 16
-// rows over the column range [y * kGemvRange, (y + 1) * kGemvRange): it splits that
-// slice of every vector into two fp16 parts in LDS itself (with the slice's own
-// power of two, which the partial sums take back), and writes its partial sums to
-// part[range][b][r]; gemv_reduce_kernel adds the ranges in order.
-constexpr uint32_t kGemvChunk = 256;
-constexpr uint32_t kGemvRange = 512;             // columns per workgroup (two chunks)
+// members, so every weight is decoded once for all of them. A workgroup covers
+// S slabs of 16 rows over the column range [y * kGemvRange, (y + 1) * kGemvRange):
+//   1. every thread issues its share of the tile's weight loads (the whole tile is
+//      in flight at once: an 8-vector GEMV is a few MB to a few tens of MB, and the
+//      loads in flight, not the arithmetic, set its time at these sizes);
+//   2. meanwhile it splits that slice of every vector into two fp16 parts in LDS
+//      (with the slice's own power of two, which the partial sums take back): the
+//      split is shared by the 16 S rows of the workgroup;
+//   3. the weights go to LDS, one row per padded LDS row;
+//   4. wave w multiplies slabs w, w + 4, ... over every block of the range (no
+//      barrier inside the loop, no cross-wave sum) and writes the partial sums of
+//      its rows to part[range][b][r]; gemv_reduce_kernel adds the ranges in order.
+constexpr uint32_t kGemvRange = 512;               // columns per workgroup
 constexpr uint32_t kGemvXStride = kGemvRange + 8;  // halves per staged vector part (padded)
 
-template <class R>
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(16)));
+
+// LDS layout of a tile: 16 S rows of kWStride dwords (a full range's row segment,
+// padded to keep 16-byte rows), then, for the split FP4 layout, 16 S rows of
+// kSStride dwords of E8M0 scales.
+template <class R, int S>
+struct GemvTile {
+    static constexpr uint32_t kRows = 16u * S;
+    static constexpr uint32_t kWdw = Tile<R>::wdw(kGemvRange);
+    static constexpr uint32_t kWStride = kWdw + 4;
+    static constexpr uint32_t kSdw = Tile<R>::kScales ? Tile<R>::sdw(kGemvRange) : 0u;
+    static constexpr uint32_t kSStride = Tile<R>::kScales ? kSdw + 1 : 0u;
+    static constexpr size_t lds_bytes() { return 4ull * kRows * (kWStride + kSStride); }
+};
+
+// Weight units of V dwords (V = 4: 16-byte rows and range starts, every range full;
+// V = 1: any 4-byte aligned layout, the last range possibly short).
+template <int V>
+struct WUnit;
+template <>
+struct WUnit<4> {
+    typedef u32x4a T;
+    static __device__ __forceinline__ T load(gptr<uint32_t> p) { return *(gptr<u32x4a>)(p); }
+};
+template <>
+struct WUnit<1> {
+    typedef uint32_t T;
+    static __device__ __forceinline__ T load(gptr<uint32_t> p) { return *p; }
+};
+
+template <class R, int S, int V>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(const void* __restrict__ w, const void* __restrict__ ws,
                                                         const float* __restrict__ x, float* __restrict__ part,
                                                         uint32_t rows, uint32_t cols, uint32_t n_vec) {
-    extern __shared__ uint32_t tl[];
+    using TL = GemvTile<R, S>;
+    using U = typename WUnit<V>::T;
+    extern __shared__ __align__(16) uint32_t tl[];
     __shared__ __align__(16) _Float16 xs[2][8][kGemvXStride];  // [hi / lo][vector][column of the range]
     __shared__ float xmul[8];
-    constexpr uint32_t kChunk = kGemvChunk;
-    constexpr int kB = kChunk / 32 / 4;  // blocks per wave and chunk
-    auto red = reinterpret_cast<f32x4(*)[64]>(tl);
+    constexpr uint32_t kUpr = TL::kWdw / V;                  // units per row of a full range
+    constexpr uint32_t kNU = (TL::kRows * kUpr + 255) / 256;  // units per thread
+    constexpr uint32_t kSUpr = TL::kSdw;                      // scale dwords per row (FP4)
+    constexpr uint32_t kNS = (TL::kRows * kSUpr + 255) / 256;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t r0 = blockIdx.x * kSlab;
-    const uint32_t lr = lane & 15, kg = lane >> 4, row = r0 + lr;
+    const uint32_t r0 = blockIdx.x * TL::kRows;
     const uint32_t k0 = blockIdx.y * kGemvRange, k1 = k0 + kGemvRange < cols ? k0 + kGemvRange : cols;
-    const uint32_t nchunks = (k1 - k0 + kChunk - 1) / kChunk;
-    const uint32_t buf_dw = Tile<R>::lds_dw(kChunk);
+    const uint32_t kc = k1 - k0;
+    const uint32_t wdw = Tile<R>::wdw(kc);  // dwords of this range's row segments
     const R mt = RowsOf<R>::make(w, ws, cols);
-    const size_t wpitch = Tile<R>::wpitch(mt), spitch = Tile<R>::spitch(mt);
-    auto span = [&](uint32_t kc0) { return k1 - kc0 < kChunk ? k1 - kc0 : kChunk; };
-    auto stage = [&](uint32_t kc0, Staged<R, 1, kChunk>& st) {
-        const uint32_t kc = span(kc0);
-        slab_load(Tile<R>::wrow(mt, kc0), wpitch, r0, rows, Tile<R>::wdw(kc), st.w[0]);
-        if constexpr (Tile<R>::kScales) slab_load(Tile<R>::srow(mt, kc0), spitch, r0, rows, Tile<R>::sdw(kc), st.s[0]);
-        if constexpr (Tile<R>::kTileScale) st.ts[0] = Tile<R>::tile_scales(mt, r0, kc0, kc);
-    };
-    uint32_t ts_cur = 0;  // the tile scales of the chunk being multiplied
-    auto commit = [&](uint32_t kc0, uint32_t buf, const Staged<R, 1, kChunk>& st) {
-        const uint32_t kc = span(kc0);
-        uint32_t* base = tl + buf * buf_dw;
-        slab_store(base, Tile<R>::wdw(kc), st.w[0]);
-        if constexpr (Tile<R>::kScales) slab_store(base + kSlab * (Tile<R>::wdw(kc) + 1), Tile<R>::sdw(kc), st.s[0]);
-        ts_cur = st.ts[0];
-    };
-    Staged<R, 1, kChunk> st;
-    stage(k0, st);  // the first weights travel while x is split
+    // 1. the vectors' slices (32 threads per vector, 16 consecutive columns each), then
+    // the tile's weight (and scale) loads, all in flight together (the split below
+    // waits for the slices alone)
+    const uint32_t xb = threadIdx.x >> 5, xc = (threadIdx.x & 31) * 16;
+    const bool xlive = xb < n_vec && k0 + xc < k1;
+    float v[16];
+    if (xlive) {
+        const gptr<f32x4> src = as_global(reinterpret_cast<const f32x4*>(x + static_cast<size_t>(xb) * cols + k0 + xc));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 f = src[q];
+            v[4 * q] = f[0]; v[4 * q + 1] = f[1]; v[4 * q + 2] = f[2]; v[4 * q + 3] = f[3];
+        }
+    }
+    // rows past `rows` read the last row, units past the range's end are not read
+    U wv[kNU];
     {
-        // 32 threads per vector, 16 consecutive columns (two groups of 8) each
-        const uint32_t b = threadIdx.x >> 5, c = (threadIdx.x & 31) * 16;
-        const bool live = b < n_vec && k0 + c < k1;
-        float v[16];
+        const uint8_t* wb = Tile<R>::wrow(mt, k0);
+        const size_t pitch = Tile<R>::wpitch(mt);
+#pragma unroll
+        for (uint32_t i = 0; i < kNU; ++i) {
+            const uint32_t u = threadIdx.x + 256u * i;
+            const uint32_t rr = u / kUpr, c = u - rr * kUpr;
+            if (rr < TL::kRows && c * V < wdw) {
+                const uint32_t r = r0 + rr < rows ? r0 + rr : rows - 1;
+                wv[i] = WUnit<V>::load(as_global(reinterpret_cast<const uint32_t*>(wb + static_cast<size_t>(r) * pitch)) + c * V);
+            }
+        }
+    }
+    uint32_t sv[kNS > 0 ? kNS : 1];
+    if constexpr (kNS > 0) {
+        const uint8_t* sb = Tile<R>::srow(mt, k0);
+        const size_t spitch = Tile<R>::spitch(mt);
+        const uint32_t sdw = Tile<R>::sdw(kc);
+#pragma unroll
+        for (uint32_t i = 0; i < kNS; ++i) {
+            const uint32_t u = threadIdx.x + 256u * i;
+            const uint32_t rr = u / kSUpr, c = u - rr * kSUpr;
+            if (rr < TL::kRows && c < sdw) {
+                const uint32_t r = r0 + rr < rows ? r0 + rr : rows - 1;
+                sv[i] = as_global(reinterpret_cast<const uint32_t*>(sb + static_cast<size_t>(r) * spitch))[c];
+            }
+        }
+    }
+    // 2. the slices split into two fp16 parts (the slice's power of two in xmul)
+    {
+        const uint32_t b = xb, c = xc;
+        const bool live = xlive;
         float m = 0.0f;
         bool finite = true;
         if (live) {
-            const gptr<f32x4> src = as_global(reinterpret_cast<const f32x4*>(x + static_cast<size_t>(b) * cols + k0 + c));
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f32x4 f = src[q];
-                v[4 * q] = f[0]; v[4 * q + 1] = f[1]; v[4 * q + 2] = f[2]; v[4 * q + 3] = f[3];
-            }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 finite = finite && __builtin_isfinite(v[i]);
@@ -723,59 +780,88 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const void* __restrict__
         }
         if (b < 8 && (threadIdx.x & 31) == 0) xmul[b] = ldexpf(1.0f, -sh);
     }
-    // A operand rows: vector lr / 2 (the last one repeated past n_vec), part lr & 1
-    const _Float16* xa_row = &xs[lane & 1][(lr >> 1) < n_vec ? (lr >> 1) : n_vec - 1][0];
-    commit(k0, 0, st);
-    __syncthreads();
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t c = 0; c < nchunks; ++c) {
-        const uint32_t kc0 = k0 + c * kChunk;
-        const uint32_t kc = span(kc0);
-        if (c + 1 < nchunks) stage(kc0 + kChunk, st);  // in flight during the products below
-        const uint32_t nb = kc / 32, per = (nb + 3) / 4;
-        const uint32_t b0 = wave * per < nb ? wave * per : nb, b1 = b0 + per < nb ? b0 + per : nb;
-        const uint32_t* base = tl + (c & 1) * buf_dw;
-        const uint8_t* wl = reinterpret_cast<const uint8_t*>(base + lr * (Tile<R>::wdw(kc) + 1));
-        const uint8_t* sl =
-            reinterpret_cast<const uint8_t*>(base + kSlab * (Tile<R>::wdw(kc) + 1) + lr * (Tile<R>::sdw(kc) + 1));
+    // 3. the weights (and scales) into LDS
 #pragma unroll
-        for (int i = 0; i < kB; ++i) {
-            if (b0 + static_cast<uint32_t>(i) >= b1) break;
-            const uint32_t bb = b0 + static_cast<uint32_t>(i);
-            const half8 xa = *reinterpret_cast<const half8*>(xa_row + (kc0 - k0) + 32 * bb + 8 * kg);
+    for (uint32_t i = 0; i < kNU; ++i) {
+        const uint32_t u = threadIdx.x + 256u * i;
+        const uint32_t rr = u / kUpr, c = u - rr * kUpr;
+        if (rr < TL::kRows && c * V < wdw) {
+            if constexpr (V == 4) *reinterpret_cast<u32x4a*>(tl + rr * TL::kWStride + 4 * c) = wv[i];
+            else tl[rr * TL::kWStride + c] = wv[i];
+        }
+    }
+    if constexpr (kNS > 0) {
+        const uint32_t sdw = Tile<R>::sdw(kc);
+#pragma unroll
+        for (uint32_t i = 0; i < kNS; ++i) {
+            const uint32_t u = threadIdx.x + 256u * i;
+            const uint32_t rr = u / kSUpr, c = u - rr * kSUpr;
+            if (rr < TL::kRows && c < sdw) tl[TL::kRows * TL::kWStride + rr * TL::kSStride + c] = sv[i];
+        }
+    }
+    __syncthreads();
+    // 4. A operand rows: vector lr / 2 (the last one repeated past n_vec), part lr & 1
+    const uint32_t lr = lane & 15, kg = lane >> 4;
+    const _Float16* xa_row = &xs[lane & 1][(lr >> 1) < n_vec ? (lr >> 1) : n_vec - 1][0];
+    constexpr int kSW = S / 4;  // slabs per wave
+    f32x4 acc[kSW];
+#pragma unroll
+    for (int j = 0; j < kSW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto step = [&](uint32_t bb) {
+        const half8 xa = *reinterpret_cast<const half8*>(xa_row + 32 * bb + 8 * kg);
+#pragma unroll
+        for (int j = 0; j < kSW; ++j) {
+            const uint32_t row_l = (wave + 4u * static_cast<uint32_t>(j)) * 16u + lr;
+            const uint8_t* wl = reinterpret_cast<const uint8_t*>(tl + row_l * TL::kWStride);
+            const uint8_t* sl = reinterpret_cast<const uint8_t*>(tl + TL::kRows * TL::kWStride + row_l * TL::kSStride);
             float sc;
-            const half8 bw = Tile<R>::get(wl, sl, ts_cur, bb, kg, sc);
+            const half8 bw = Tile<R>::get(wl, sl, 0u, bb, kg, sc);
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
             const f32x4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bw, z, 0, 0, 0);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(sc, r[q], acc[q]);
+            for (int q = 0; q < 4; ++q) acc[j][q] = __builtin_fmaf(sc, r[q], acc[j][q]);
         }
-        if (c + 1 < nchunks) commit(kc0 + kChunk, (c + 1) & 1, st);
-        __syncthreads();
-    }
-    if (wave > 0) red[wave - 1][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
+    };
+    if (kc == kGemvRange) {  // a full range: four blocks' loads and products interleave
+#pragma unroll 1
+        for (uint32_t b0 = 0; b0 < kGemvRange / 32; b0 += 4) {
 #pragma unroll
-        for (int v = 0; v < 3; ++v) acc += red[v][lane];
-        // lane: row `row`, vectors 2kg + q (q = 0, 1) as (hi, lo) in 2q, 2q+1
+            for (uint32_t i = 0; i < 4; ++i) step(b0 + i);
+        }
+    } else {
+        for (uint32_t bb = 0; bb < kc / 32; ++bb) step(bb);
+    }
+    // lane: row r0 + (wave + 4j) * 16 + lr, vectors 2kg + q (q = 0, 1) as (hi, lo) in 2q, 2q+1
+#pragma unroll
+    for (int j = 0; j < kSW; ++j) {
+        const uint32_t row = r0 + (wave + 4u * static_cast<uint32_t>(j)) * 16u + lr;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            const uint32_t j = 2 * kg + static_cast<uint32_t>(q);
-            if (j < n_vec && row < rows)
-                part[(static_cast<size_t>(blockIdx.y) * n_vec + j) * rows + row] = (acc[2 * q] + acc[2 * q + 1]) * xmul[j];
+            const uint32_t jv = 2 * kg + static_cast<uint32_t>(q);
+            if (jv < n_vec && row < rows)
+                part[(static_cast<size_t>(blockIdx.y) * n_vec + jv) * rows + row] =
+                    (acc[j][2 * q] + acc[j][2 * q + 1]) * xmul[jv];
         }
     }
 }
 
-// y[b][r] = sum over ranges s (in order) of part[s][b][r].
+// y[b][r] = sum over ranges s (in order) of part[s][b][r]; the loads of 8 ranges are
+// in flight together, the additions keep the range order.
 __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
                                                           uint32_t rows, uint32_t n_vec, uint32_t n_ranges) {
     const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
     const size_t n = static_cast<size_t>(n_vec) * rows;
     if (i >= n) return;
     float s = part[i];
-    for (uint32_t r = 1; r < n_ranges; ++r) s += part[static_cast<size_t>(r) * n + i];
+    for (uint32_t r0 = 1; r0 < n_ranges; r0 += 8) {
+        float v[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j)
+            if (r0 + j < n_ranges) v[j] = part[static_cast<size_t>(r0 + j) * n + i];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j)
+            if (r0 + j < n_ranges) s += v[j];
+    }
     y[i] = s;
 }
 
@@ -845,20 +931,33 @@ bool gemv_mfma_supported(int32_t format, uint64_t rows, uint64_t cols, uint64_t 
 }
 
 namespace {
-template <class R>
-hipError_t launch_gemv_mfma_t(hipStream_t s, const void* w, const void* ws, const float* x, float* y, float* part,
-                              uint32_t rows, uint32_t cols, uint32_t nv, uint32_t ks) {
-    const uint32_t slabs = (rows + kSlab - 1) / kSlab;
-    const size_t lds = 2 * 4 * static_cast<size_t>(Tile<R>::lds_dw(kGemvChunk));
+template <class R, int S, int V>
+hipError_t launch_gemv_mfma_sv(hipStream_t s, const void* w, const void* ws, const float* x, float* y, float* part,
+                               uint32_t rows, uint32_t cols, uint32_t nv, uint32_t ks) {
+    const uint32_t groups = (rows + 16 * S - 1) / (16 * S);
+    const size_t lds = GemvTile<R, S>::lds_bytes();
     // one range: the partial sums are the result
-    hipLaunchKernelGGL((gemv_mfma_kernel<R>), dim3(slabs, ks), dim3(256), lds, s, w, ws, x, ks > 1 ? part : y, rows,
-                       cols, nv);
+    hipLaunchKernelGGL((gemv_mfma_kernel<R, S, V>), dim3(groups, ks), dim3(256), lds, s, w, ws, x,
+                       ks > 1 ? part : y, rows, cols, nv);
     if (ks > 1) {
         const size_t n = static_cast<size_t>(nv) * rows;
         hipLaunchKernelGGL(gemv_reduce_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, part, y,
                            rows, nv, ks);
     }
     return hipGetLastError();
+}
+
+// 8 slabs (128 rows) per workgroup when that still gives two workgroups per CU,
+// else 4; 16-byte weight units when every range is full and its rows 16-byte aligned.
+template <class R>
+hipError_t launch_gemv_mfma_t(hipStream_t s, const void* w, const void* ws, const float* x, float* y, float* part,
+                              uint32_t rows, uint32_t cols, uint32_t nv, uint32_t ks, uint32_t cus) {
+    const bool s8 = static_cast<uint64_t>((rows + 127) / 128) * ks >= 2ull * cus;
+    const bool v4 = cols % kGemvRange == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    if (s8) return v4 ? launch_gemv_mfma_sv<R, 8, 4>(s, w, ws, x, y, part, rows, cols, nv, ks)
+                      : launch_gemv_mfma_sv<R, 8, 1>(s, w, ws, x, y, part, rows, cols, nv, ks);
+    return v4 ? launch_gemv_mfma_sv<R, 4, 4>(s, w, ws, x, y, part, rows, cols, nv, ks)
+              : launch_gemv_mfma_sv<R, 4, 1>(s, w, ws, x, y, part, rows, cols, nv, ks);
 }
 }  // namespace
 
@@ -870,6 +969,7 @@ int32_t launch_gemv_mfma(objeta_hip_context* ctx, hipStream_t s, int32_t format,
     const uint32_t R = static_cast<uint32_t>(rows), K = static_cast<uint32_t>(cols);
     const uint32_t ks = (K + kGemvRange - 1) / kGemvRange;  // column ranges
     const uint32_t nvmax = static_cast<uint32_t>(batch < 8 ? batch : 8);
+    const uint32_t cus = ctx->info.compute_units > 0 ? static_cast<uint32_t>(ctx->info.compute_units) : 256u;
     float* part = nullptr;
     if (ks > 1) {
         void* wsp = nullptr;
@@ -882,10 +982,10 @@ int32_t launch_gemv_mfma(objeta_hip_context* ctx, hipStream_t s, int32_t format,
         float* yb = y + done * rows;
         hipError_t e;
         switch (format) {
-            case OBJETA_HIP_Q4_0: e = launch_gemv_mfma_t<QRows<kQ4>>(s, w, nullptr, xb, yb, part, R, K, nv, ks); break;
-            case OBJETA_HIP_Q5_0: e = launch_gemv_mfma_t<QRows<kQ5>>(s, w, nullptr, xb, yb, part, R, K, nv, ks); break;
-            case OBJETA_HIP_IQ3_0: e = launch_gemv_mfma_t<QRows<kIQ3>>(s, w, nullptr, xb, yb, part, R, K, nv, ks); break;
-            default: e = launch_gemv_mfma_t<Fp4Rows>(s, w, ws, xb, yb, part, R, K, nv, ks); break;
+            case OBJETA_HIP_Q4_0: e = launch_gemv_mfma_t<QRows<kQ4>>(s, w, nullptr, xb, yb, part, R, K, nv, ks, cus); break;
+            case OBJETA_HIP_Q5_0: e = launch_gemv_mfma_t<QRows<kQ5>>(s, w, nullptr, xb, yb, part, R, K, nv, ks, cus); break;
+            case OBJETA_HIP_IQ3_0: e = launch_gemv_mfma_t<QRows<kIQ3>>(s, w, nullptr, xb, yb, part, R, K, nv, ks, cus); break;
+            default: e = launch_gemv_mfma_t<Fp4Rows>(s, w, ws, xb, yb, part, R, K, nv, ks, cus); break;
         }
         if (e != hipSuccess) OBJ_FAIL(kDriver, action, hipGetErrorString(e));
     }

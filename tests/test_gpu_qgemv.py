@@ -220,7 +220,26 @@ def test_gemv_batched_mfma_column_ranges(backend, quant, fmt, rows, cols, batch)
         _assert_close(y[t], orc.gemv(int(fmt), q, xt, rows, cols), q, xt, fmt, rows, cols)
 
 
-@pytest.mark.parametrize("rows,cols,batch", [(100, 640, 5), (48, 1024, 8)])
+@pytest.mark.parametrize("fmt", FORMATS[:3])
+@pytest.mark.parametrize("cols", [4096, 4160])
+def test_gemv_batched_mfma_wide_tiles(backend, quant, fmt, cols):
+    """8200 rows over 8 or 9 column ranges give enough workgroups for 128-row tiles
+    (8 slabs per workgroup, the last tile 8 rows deep): 16-byte weight units when every
+    range is full (4096 columns), dword units with a 64-column last range (4160)."""
+    rows, batch = 8200, 8
+    m = orc.gauss(rows * cols, 50 + cols, 0.02)
+    q = orc.quantize_matrix(int(fmt), m, rows, cols)
+    xs = orc.gauss(batch * cols, 51 + cols, 1.0)
+    dy = backend.alloc(batch * rows * 4)
+    quant.launch_kernel(fmt, None, backend.to_device(q), backend.to_device(xs), dy, QGemvShape.new(fmt, rows, cols),
+                        batch=batch)
+    y = dy.download(np.float32, batch * rows).reshape(batch, rows)
+    for t in range(batch):
+        xt = xs[t * cols:(t + 1) * cols]
+        _assert_close(y[t], orc.gemv(int(fmt), q, xt, rows, cols), q, xt, fmt, rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(100, 640, 5), (48, 1024, 8), (8200, 4096, 8), (8200, 4224, 7)])
 def test_fp4_split_gemv_batched_mfma(backend, quant, rows, cols, batch):
     rng = np.random.default_rng(rows * cols)
     w = rng.integers(0, 256, size=rows * cols // 2, dtype=np.uint8)
