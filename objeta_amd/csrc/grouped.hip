@@ -356,7 +356,7 @@ struct Tile<QRows<F>> {
     static constexpr uint32_t kChunkGU = 512, kChunkDn = 256;
     static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 32 * kBB / 4; }  // dwords per row segment
     static constexpr __host__ __device__ uint32_t sdw(uint32_t) { return 0; }
-    static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) { return kSlab * (wdw(kc) + 1); }
+    static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) { return kSlab * (wdw(kc) + 4); }
     static __device__ __forceinline__ size_t wpitch(const QRows<F>& m) { return m.row_bytes; }
     static __device__ __forceinline__ size_t spitch(const QRows<F>&) { return 0; }
     static __device__ __forceinline__ const uint8_t* wrow(const QRows<F>& m, uint32_t c0) {
@@ -389,7 +389,7 @@ struct Tile<Fp4Rows> {
     static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 8; }   // kc / 2 bytes
     static constexpr __host__ __device__ uint32_t sdw(uint32_t kc) { return kc / 128; }  // kc / 32 bytes (kc % 128 == 0)
     static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) {
-        return kSlab * (wdw(kc) + 1) + kSlab * (sdw(kc) + 1);
+        return kSlab * (wdw(kc) + 4) + kSlab * (sdw(kc) + 1);
     }
     static __device__ __forceinline__ size_t wpitch(const Fp4Rows& m) { return m.wrow; }
     static __device__ __forceinline__ size_t spitch(const Fp4Rows& m) { return m.srow; }
@@ -420,7 +420,7 @@ struct Tile<Fp8Rows> {
     static constexpr uint32_t kChunkGU = 256, kChunkDn = 256;
     static constexpr __host__ __device__ uint32_t wdw(uint32_t kc) { return kc / 4; }  // kc bytes
     static constexpr __host__ __device__ uint32_t sdw(uint32_t) { return 0; }
-    static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) { return kSlab * (wdw(kc) + 1); }
+    static constexpr __host__ __device__ uint32_t lds_dw(uint32_t kc) { return kSlab * (wdw(kc) + 4); }
     static __device__ __forceinline__ size_t wpitch(const Fp8Rows& m) { return m.wrow; }
     static __device__ __forceinline__ size_t spitch(const Fp8Rows&) { return 0; }
     static __device__ __forceinline__ const uint8_t* wrow(const Fp8Rows& m, uint32_t c0) { return m.w + c0; }
@@ -451,41 +451,112 @@ struct Tile<Fp8Rows> {
     }
 };
 
-// This thread's share of a slab's row segments (seg dwords per row): thread t takes
-// row t / 16 and its dwords t % 16, t % 16 + 16, ... Rows past `rows` read the last
-// row.
-template <int N>
-__device__ __forceinline__ void slab_load(const uint8_t* base, size_t pitch, uint32_t r0, uint32_t rows, uint32_t seg,
-                                          uint32_t (&v)[N]) {
-    const uint32_t rr = threadIdx.x >> 4, c0 = threadIdx.x & 15;
-    const uint32_t r = r0 + rr < rows ? r0 + rr : rows - 1;
-    const gptr<uint32_t> src = as_global(reinterpret_cast<const uint32_t*>(base + static_cast<size_t>(r) * pitch));
+// A slab's row segments of a chunk (seg dwords per row, at most kSeg) move in 16-byte
+// units: unit c of a row covers dwords [min(4c, seg - 4), +4) (seg >= 4 for every
+// chunk width and format), so a short last chunk reads inside its rows; thread t takes
+// units t, t + 256, ... of the 16 rows in row order. Rows past `rows` read the last
+// row. In LDS a row takes kSeg + 4 dwords (16-byte rows; a stride of 12 mod 64 dwords
+// spreads the 16 rows x 4 k groups of an MFMA operand read over distinct banks).
+template <uint32_t kSeg>
+struct SlabUnits {
+    static constexpr uint32_t kUpr = (kSeg + 3) / 4;                 // units per row of a full chunk
+    static constexpr uint32_t kN = (kSlab * kUpr + 255) / 256;        // units per thread
+    static constexpr uint32_t kStride = kSeg + 4;                      // LDS dwords per row
+};
+// Buffer loads over one matrix: the per-lane offsets stay in registers of their own
+// from chunk to chunk (the chunk's offset is a scalar), so issuing the next chunk's
+// loads never waits on registers that earlier loads still write.
+// `base` is the same in every lane (a member set's matrix).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t matrix_rsrc(const void* base) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+    void* p = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, 0x7FFFFFFF, 0x00020000);
+}
+// This thread's units of a slab: row byte offsets (rows past `rows` read the last row)
+// and unit indices, fixed for a member set.
+template <uint32_t kSeg>
+struct SlabLanes {
+    uint32_t off[SlabUnits<kSeg>::kN];  // byte offset of the unit in a full chunk
+    uint32_t c[SlabUnits<kSeg>::kN];    // unit index in its row (0xFFFF: none)
+    __device__ __forceinline__ void init(uint32_t r0, uint32_t rows, size_t pitch) {
+        using SU = SlabUnits<kSeg>;
 #pragma unroll
-    for (int q = 0; q < N; ++q) {
-        if (static_cast<uint32_t>(q) * 16u >= seg) break;  // uniform: a short chunk needs fewer units
-        const uint32_t c = c0 + static_cast<uint32_t>(q) * 16u;
-        v[q] = src[c < seg ? c : seg - 1];
+        for (uint32_t i = 0; i < SU::kN; ++i) {
+            const uint32_t u = threadIdx.x + 256u * i;
+            const uint32_t rr = u / SU::kUpr;
+            c[i] = rr < kSlab ? u - rr * SU::kUpr : 0xFFFFu;
+            const uint32_t r = r0 + rr < rows ? r0 + rr : rows - 1;
+            off[i] = static_cast<uint32_t>(static_cast<size_t>(r) * pitch) + 16u * (c[i] & 0xFFFu);
+        }
+    }
+};
+template <uint32_t kSeg, bool FULL>
+__device__ __forceinline__ void slab_load4(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off, const SlabLanes<kSeg>& ln,
+                                           uint32_t seg, u32x4 (&v)[SlabUnits<kSeg>::kN]) {
+    using SU = SlabUnits<kSeg>;
+    if (FULL || seg == kSeg) {  // a full chunk: the precomputed offsets as they are
+#pragma unroll
+        for (uint32_t i = 0; i < SU::kN; ++i) {
+            if (SU::kN * 256u == kSlab * SU::kUpr || ln.c[i] < SU::kUpr) {
+                const auto q = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(ln.off[i]),
+                                                                     static_cast<int>(chunk_off), 0);
+                v[i] = u32x4{q[0], q[1], q[2], q[3]};
+            }
+        }
+        return;
+    }
+    const uint32_t upr = (seg + 3) / 4;
+#pragma unroll
+    for (uint32_t i = 0; i < SU::kN; ++i) {
+        if (ln.c[i] < upr) {
+            const uint32_t d = 4 * ln.c[i] < seg - 4 ? 4 * ln.c[i] : seg - 4;
+            const auto q = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(ln.off[i] - 16u * ln.c[i] + 4u * d),
+                                                                 static_cast<int>(chunk_off), 0);
+            v[i] = u32x4{q[0], q[1], q[2], q[3]};
+        }
     }
 }
-template <int N>
-__device__ __forceinline__ void slab_store(uint32_t* lds, uint32_t seg, const uint32_t (&v)[N]) {
-    const uint32_t rr = threadIdx.x >> 4, c0 = threadIdx.x & 15;
-    uint32_t* dst = lds + rr * (seg + 1);
+template <uint32_t kSeg, bool FULL>
+__device__ __forceinline__ void slab_store4(uint32_t* lds, uint32_t seg, const u32x4 (&v)[SlabUnits<kSeg>::kN]) {
+    using SU = SlabUnits<kSeg>;
+    const uint32_t upr = (seg + 3) / 4;
 #pragma unroll
-    for (int q = 0; q < N; ++q) {
-        if (static_cast<uint32_t>(q) * 16u >= seg) break;
-        const uint32_t c = c0 + static_cast<uint32_t>(q) * 16u;
-        if (c < seg) dst[c] = v[q];
+    for (uint32_t i = 0; i < SU::kN; ++i) {
+        const uint32_t u = threadIdx.x + 256u * i;
+        const uint32_t rr = u / SU::kUpr, c = u - rr * SU::kUpr;
+        if (rr < kSlab && c < upr) {
+            uint32_t* dst = lds + rr * SU::kStride;
+            if (FULL || seg == kSeg) {  // a full chunk: aligned 16-byte stores
+                typedef uint32_t u32x4s __attribute__((ext_vector_type(4), aligned(16)));
+                *reinterpret_cast<u32x4s*>(dst + 4 * c) = u32x4s{v[i].x, v[i].y, v[i].z, v[i].w};
+            } else {
+                const uint32_t d = 4 * c < seg - 4 ? 4 * c : seg - 4;
+                dst[d] = v[i].x; dst[d + 1] = v[i].y; dst[d + 2] = v[i].z; dst[d + 3] = v[i].w;
+            }
+        }
     }
+}
+// FP4 scale rows (seg <= 16 dwords): one dword per thread, thread t row t / 16.
+__device__ __forceinline__ void scale_load(const uint8_t* base, size_t pitch, uint32_t r0, uint32_t rows, uint32_t seg,
+                                           uint32_t& v) {
+    const uint32_t rr = threadIdx.x >> 4, c = threadIdx.x & 15;
+    const uint32_t r = r0 + rr < rows ? r0 + rr : rows - 1;
+    if (c < seg) v = as_global(reinterpret_cast<const uint32_t*>(base + static_cast<size_t>(r) * pitch))[c];
+}
+__device__ __forceinline__ void scale_store(uint32_t* lds, uint32_t stride, uint32_t seg, uint32_t v) {
+    const uint32_t rr = threadIdx.x >> 4, c = threadIdx.x & 15;
+    if (c < seg) lds[rr * stride + c] = v;
 }
 
 // One chunk's staged bytes of every matrix of the workgroup, in registers.
 template <class R, int M, uint32_t CH>
 struct Staged {
-    static constexpr int kUnits = (Tile<R>::wdw(CH) + 15) / 16;
-    uint32_t w[M][kUnits];
-    uint32_t s[M][1];  // FP4 scales: CH / 128 <= 16 dwords per row
-    uint32_t ts[M];    // FP8 tile scales of the chunk
+    static constexpr uint32_t kSeg = Tile<R>::wdw(CH);
+    u32x4 w[M][SlabUnits<kSeg>::kN];
+    uint32_t s[M];   // FP4 scales: CH / 128 <= 16 dwords per row
+    uint32_t ts[M];  // FP8 tile scales of the chunk
 };
 
 // grid = (ceil(rows / 16), gy), 256 threads; workgroup (x, y) takes member sets y,
@@ -493,7 +564,7 @@ struct Staged {
 // over the split x rows (cols = hidden), writes act (the official SwiGLU when
 // `official` is set); else rows = out_dim over the split act rows (cols = inter),
 // writes part. Dynamic LDS: two chunk buffers of every matrix.
-template <class R, bool GATEUP>
+template <class R, bool GATEUP, bool FULL>
 __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Float16* __restrict__ vh,
                                                           const _Float16* __restrict__ vl,
                                                           const float* __restrict__ vmult, float* __restrict__ out,
@@ -505,6 +576,11 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
     constexpr int kMats = GATEUP ? 2 : 1;
     constexpr uint32_t kChunk = GATEUP ? Tile<R>::kChunkGU : Tile<R>::kChunkDn;
     constexpr int kB = kChunk / 32 / 4;  // blocks per wave and chunk
+    constexpr uint32_t kSeg = Tile<R>::wdw(kChunk);           // weight dwords per row of a full chunk
+    constexpr uint32_t kWStride = SlabUnits<kSeg>::kStride;    // LDS dwords per staged weight row
+    constexpr uint32_t kSStride = Tile<R>::sdw(kChunk) + 1;    // LDS dwords per staged scale row (FP4)
+    static_assert(Tile<R>::lds_dw(kChunk) == kSlab * kWStride + (Tile<R>::kScales ? kSlab * kSStride : 0u),
+                  "LDS chunk layout");
     const uint32_t n_sets = gw.hdr[1];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t r0 = blockIdx.x * kSlab;
@@ -525,24 +601,30 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
         mt[0] = GATEUP ? RowsOf<R>::make(P.gate, P.gate_scale, cols) : RowsOf<R>::make(P.down, P.down_scale, cols);
         if constexpr (GATEUP) mt[kMats - 1] = RowsOf<R>::make(P.up, P.up_scale, cols);
         const size_t wpitch = Tile<R>::wpitch(mt[0]), spitch = Tile<R>::spitch(mt[0]);
+        SlabLanes<kSeg> lanes;
+        lanes.init(r0, rows, wpitch);
+        __amdgpu_buffer_rsrc_t rs[kMats];
+#pragma unroll
+        for (int t = 0; t < kMats; ++t) rs[t] = matrix_rsrc(Tile<R>::wrow(mt[t], 0));
         // A operand rows: member (lane&15)/2 of the set, part (lane&1)
         const uint32_t am = member((lane & 15) >> 1);
         // token row of x (routed or shared act row), or the act row itself
         auto xrow = [&](uint32_t a) { return a < n_assign ? a / k : a - n_assign; };
         const uint32_t vrow = GATEUP ? xrow(am) : am;
         auto stage = [&](uint32_t kc0, Staged<R, kMats, kChunk>& st) {
-            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
+            const uint32_t kc = FULL ? kChunk : (cols - kc0 < kChunk ? cols - kc0 : kChunk);
 #pragma unroll
             for (int t = 0; t < kMats; ++t) {
-                slab_load(Tile<R>::wrow(mt[t], kc0), wpitch, r0, rows, Tile<R>::wdw(kc), st.w[t]);
+                slab_load4<kSeg, FULL>(rs[t], static_cast<uint32_t>(Tile<R>::wrow(mt[t], kc0) - Tile<R>::wrow(mt[t], 0)), lanes,
+                                 Tile<R>::wdw(kc), st.w[t]);
                 if constexpr (Tile<R>::kScales)
-                    slab_load(Tile<R>::srow(mt[t], kc0), spitch, r0, rows, Tile<R>::sdw(kc), st.s[t]);
+                    scale_load(Tile<R>::srow(mt[t], kc0), spitch, r0, rows, Tile<R>::sdw(kc), st.s[t]);
                 if constexpr (Tile<R>::kTileScale) st.ts[t] = Tile<R>::tile_scales(mt[t], r0, kc0, kc);
             }
         };
         uint32_t ts_cur[kMats];  // the tile scales of the chunk being multiplied
         auto operands = [&](uint32_t kc0, half8 (&xr)[kB]) {
-            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
+            const uint32_t kc = FULL ? kChunk : (cols - kc0 < kChunk ? cols - kc0 : kChunk);
             const uint32_t nb = kc / 32, per = (nb + 3) / 4;
             const uint32_t b0 = wave * per < nb ? wave * per : nb, b1 = b0 + per < nb ? b0 + per : nb;
 #pragma unroll
@@ -553,13 +635,13 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
             }
         };
         auto commit = [&](uint32_t kc0, uint32_t buf, const Staged<R, kMats, kChunk>& st) {
-            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
+            const uint32_t kc = FULL ? kChunk : (cols - kc0 < kChunk ? cols - kc0 : kChunk);
 #pragma unroll
             for (int t = 0; t < kMats; ++t) {
                 uint32_t* base = tl + buf * buf_dw + t * Tile<R>::lds_dw(kChunk);
-                slab_store(base, Tile<R>::wdw(kc), st.w[t]);
+                slab_store4<kSeg, FULL>(base, Tile<R>::wdw(kc), st.w[t]);
                 if constexpr (Tile<R>::kScales)
-                    slab_store(base + kSlab * (Tile<R>::wdw(kc) + 1), Tile<R>::sdw(kc), st.s[t]);
+                    scale_store(base + kSlab * kWStride, kSStride, Tile<R>::sdw(kc), st.s[t]);
                 ts_cur[t] = st.ts[t];  // read only after the products of the previous chunk
             }
         };
@@ -574,16 +656,17 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(GroupWs gw, const _Flo
         __syncthreads();
         for (uint32_t c = 0; c < nchunks; ++c) {
             const uint32_t kc0 = c * kChunk;
-            const uint32_t kc = cols - kc0 < kChunk ? cols - kc0 : kChunk;
+            const uint32_t kc = FULL ? kChunk : (cols - kc0 < kChunk ? cols - kc0 : kChunk);
             if (c + 1 < nchunks) stage(kc0 + kChunk, st);  // in flight during the products below
+            asm volatile("" ::: "memory");  // the loads stay ahead of the products
+            __builtin_amdgcn_sched_barrier(0);
             const uint32_t nb = kc / 32, per = (nb + 3) / 4;
             const uint32_t b0 = wave * per < nb ? wave * per : nb, b1 = b0 + per < nb ? b0 + per : nb;
 #pragma unroll
             for (int t = 0; t < kMats; ++t) {
                 const uint32_t* base = tl + (c & 1) * buf_dw + t * Tile<R>::lds_dw(kChunk);
-                const uint8_t* wl = reinterpret_cast<const uint8_t*>(base + (lane & 15) * (Tile<R>::wdw(kc) + 1));
-                const uint8_t* sl = reinterpret_cast<const uint8_t*>(base + kSlab * (Tile<R>::wdw(kc) + 1) +
-                                                                     (lane & 15) * (Tile<R>::sdw(kc) + 1));
+                const uint8_t* wl = reinterpret_cast<const uint8_t*>(base + (lane & 15) * kWStride);
+                const uint8_t* sl = reinterpret_cast<const uint8_t*>(base + kSlab * kWStride + (lane & 15) * kSStride);
 #pragma unroll
                 for (int i = 0; i < kB; ++i) {
                     if (b0 + static_cast<uint32_t>(i) >= b1) break;
@@ -902,8 +985,13 @@ void launch_grouped_products(hipStream_t s, GroupWs gw, const _Float16* vh, cons
                              bool official, uint32_t max_sets, uint32_t cus) {
     const size_t lds = (GATEUP ? 2 : 1) * 2 * 4 *
                        static_cast<size_t>(Tile<R>::lds_dw(GATEUP ? Tile<R>::kChunkGU : Tile<R>::kChunkDn));
-    hipLaunchKernelGGL((moe_grouped_kernel<R, GATEUP>), dim3((rows + kSlab - 1) / kSlab, grouped_gy(rows, max_sets, cus)),
-                       dim3(256), lds, s, gw, vh, vl, vmult, dst, cols, rows, k, n_assign, limit, official ? 1u : 0u);
+    const dim3 grid((rows + kSlab - 1) / kSlab, grouped_gy(rows, max_sets, cus));
+    if (cols % (GATEUP ? Tile<R>::kChunkGU : Tile<R>::kChunkDn) == 0)
+        hipLaunchKernelGGL((moe_grouped_kernel<R, GATEUP, true>), grid, dim3(256), lds, s, gw, vh, vl, vmult, dst, cols,
+                           rows, k, n_assign, limit, official ? 1u : 0u);
+    else
+        hipLaunchKernelGGL((moe_grouped_kernel<R, GATEUP, false>), grid, dim3(256), lds, s, gw, vh, vl, vmult, dst, cols,
+                           rows, k, n_assign, limit, official ? 1u : 0u);
 }
 
 template <class R>
