@@ -16,7 +16,7 @@ Also measured in the same run (each in its own object of the JSON line):
   of launches that rotate over more weight bytes than the 256 MB MALL holds; one
   roofline entry each, and `roofline` names the one with the most time;
 - batch: 16 and 32 tokens per step through the same 48 layers: the layer entry
-  point (grouped-token MFMA products from 17 tokens) against the router plus the
+  point (grouped-token MFMA products from 12 tokens) against the router plus the
   per-assignment kernels;
 - gemv: Q4_0 [1024 x 4096] batch 1, and Q4_0 / Q5_0 / IQ3_0 at [4096 x 4096] and
   [14336 x 4096], batch 1 and 8, each over a >= 4 GB rotated working set;
@@ -354,12 +354,12 @@ def run_kernels(env: Env, st: QwenStack, layer_io, reps: int):
 # ------------------------------------------------------------------- batches
 def run_batch(env: Env, st: QwenStack, args, seed):
     """Batches of args.batch and 2 * args.batch tokens through every layer: the layer
-    entry point (router, then the grouped-token products from 17 tokens on) against
+    entry point (router, then the grouped-token products from 12 tokens on) against
     the router followed by the per-assignment kernels, and the router followed by the
     grouped-token products at every batch size."""
     L, H, E, K, I = st.layers, st.H, st.E, st.K, st.I
     be = env.be
-    out = {"path": "objeta_hip_moe_layer_device (router + grouped-token MFMA products from 17 tokens) vs "
+    out = {"path": "objeta_hip_moe_layer_device (router + grouped-token MFMA products from 12 tokens) vs "
                    "router + objeta_hip_moe_selected_device (per-assignment kernels) vs router + "
                    "objeta_hip_moe_grouped_device (grouped-token products); one graph per pass of "
                    f"{L} layers"}

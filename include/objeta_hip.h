@@ -340,11 +340,11 @@ int32_t objeta_hip_moe_down_device(objeta_hip_context* ctx, int32_t format, obje
 /* One MoE layer on the device: the router of objeta_hip_router_topk_device over
  * d_router_w [n_experts][hidden] (+ d_router_bias) writes d_ids_out/d_weights_out
  * [n_tokens][k], then the selected experts of d_table (n_experts entries) run:
- * below 17 tokens on the per-assignment kernels of objeta_hip_moe_selected_device,
- * from 17 tokens on the grouped-token products of objeta_hip_moe_grouped_device
+ * below 12 tokens on the per-assignment kernels of objeta_hip_moe_selected_device,
+ * from 12 tokens on the grouped-token products of objeta_hip_moe_grouped_device
  * whenever that path takes the shape (on MI355X at hidden 2048, 128 experts,
- * top-8 with uniformly spread selections the per-assignment kernels are faster up
- * to 16 tokens, the grouped ones from 18 on). When one expert's three matrices
+ * top-8 the per-assignment kernels are faster up to 10 tokens, the two are even at
+ * 12 and the grouped ones faster from 14 on). When one expert's three matrices
  * take 8 MiB or more (hidden 7168, intermediate 2048) the grouped products run
  * from 2 tokens. The two agree within the fp32
  * tolerance, not bit for bit. No host
@@ -701,7 +701,7 @@ typedef struct {
  * host, the cache resolving the union of the batch's selected experts (get, then
  * insert with a copy on the copy stream for misses: the reference's admission and
  * counters), and the expert kernels waiting for that layer's copies only; batches
- * of 17 tokens and more run the grouped-token products. prefetch_next != 0 also
+ * of 12 tokens and more run the grouped-token products. prefetch_next != 0 also
  * evaluates layer l+1's router on layer l's input and starts copying its predicted
  * experts' absent tensors behind layer l's own (objeta_hip_cache_prefetch).
  * ids_out / weights_out (host, [n_layers][n_tokens][k], nullable) receive the

@@ -105,13 +105,14 @@ bool gemv_mfma_supported(int32_t format, uint64_t rows, uint64_t cols, uint64_t 
 int32_t launch_gemv_mfma(objeta_hip_context* ctx, hipStream_t s, int32_t format, const void* w, const void* ws,
                          const float* x, float* y, uint64_t rows, uint64_t cols, uint64_t batch);
 // Batches from this many tokens run the grouped-token products in the layer entry
-// points (measured on MI355X at hidden 2048, 128 experts, top-8: per-assignment
-// faster at 8 tokens, grouped at 16 and beyond).
-constexpr uint64_t kGroupedMinTokens = 17;
+// points (measured on MI355X over 48 Qwen3-A3B-shaped layers, hidden 2048, 128
+// experts, top-8, us per layer per-assignment / grouped: 10 tokens 63.7 / 66.7, 12
+// tokens 73.3 / 72.0, 16 tokens 85.1 / 76.4, 32 tokens 146.8 / 104.4).
+constexpr uint64_t kGroupedMinTokens = 12;
 // From 2 tokens when one expert's three matrices take at least this many bytes: at
 // hidden 7168 / intermediate 2048 (23 MB FP4 experts, a shared expert) the grouped
 // path takes 160 / 258 / 314 us at 2 / 3 / 4 tokens against 218 / 360 / 459 on the
-// per-assignment kernels; the Qwen3-A3B shape's 2.6 MB experts keep the 17-token
+// per-assignment kernels; the Qwen3-A3B shape's 2.6 MB experts keep the 12-token
 // switch.
 constexpr uint64_t kGroupedLargeExpertBytes = uint64_t(8) << 20;
 // Whether the layer entry points run a batch of n_tokens on the grouped path.

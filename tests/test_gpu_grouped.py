@@ -143,7 +143,7 @@ def test_grouped_rejects_unsupported_shapes(backend):
 
 
 @pytest.mark.parametrize("fmt,E,K,T,H,I,limit", [
-    (Q4, 32, 4, 17, 512, 256, 0.0),     # the smallest batch the layer entry point groups
+    (Q4, 32, 4, 12, 512, 256, 0.0),     # the smallest batch the layer entry point groups
     (FP4, 16, 4, 20, 1024, 512, 0.0),
     (Q5, 24, 3, 40, 256, 128, 0.0),     # five shared-expert sets
     (Q4, 16, 2, 18, 256, 128, 0.05),    # SwiGLU clamp (against the per-assignment path)
