@@ -424,26 +424,26 @@ KERNEL_NAME = {0: "q4_gemv", 1: "q5_gemv", 2: "iq3_gemv", 3: "fp4_e2m1_gemv"}
 BB = {0: 18, 1: 22, 2: 14}
 
 
-def run_gemv(env: Env, reps: int, checks: list | None = None):
+def run_gemv(env: Env, reps: int, checks: list | None = None, calls: int = 512, rotate: int = ROTATE_BYTES):
     """Each case's matrix replicated over >= 4 GB (one fill of R * rows rows); graphs of
     launches cycle through the replicas, so the weights come from HBM. `checks`
     receives (format, rows, cols, seed, replica-0 bytes, x, y of token 0) per case for
     the numerics of the reports."""
     be = env.be
     out = []
-    big = be.alloc(ROTATE_BYTES + (64 << 20))
+    big = be.alloc(rotate + (64 << 20))
     xs = be.alloc(4 * 8 * 14336)
     env.fill_gauss(xs.ptr, 8 * 14336, 31337, 1.0)
     ys = be.alloc(4 * 8 * 14336)
     filled = None
     for fmt, rows, cols, B in GEMV_CASES:
         mb = rows * (cols // 32) * BB[fmt]
-        R = max(1, ROTATE_BYTES // mb)
+        R = max(1, rotate // mb)
         if filled != (fmt, rows):
             env.fill_q(fmt, big.ptr, R * rows, cols, 777 + fmt)
             be.synchronize()
             filled = (fmt, rows)
-        n = min(R, 512)
+        n = min(R, calls)  # calls per graph
 
         def launch(i, fmt=fmt, rows=rows, cols=cols, B=B, mb=mb, R=R):
             env.check(env.lib.objeta_hip_qgemv_device(env.ctx, fmt, env.stream, big.addr((i % R) * mb), xs.addr(),
@@ -1010,6 +1010,11 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20251201)
     ap.add_argument("--batch", type=int, default=16, help="tokens of the batched side measurement")
     ap.add_argument("--kernel-reps", type=int, default=10, help="replays of each kernel's rotation graph")
+    ap.add_argument("--gemv-calls", type=int, default=512,
+                    help="GEMV calls per graph in the gemv section (small values keep profiler runs short)")
+    ap.add_argument("--gemv-rotate-mb", type=int, default=ROTATE_BYTES >> 20,
+                    help="bytes of matrix replicas the gemv section cycles through, in MiB (>= 512 keeps "
+                         "the weights out of the 256 MB MALL)")
     ap.add_argument("--miss-tokens", type=int, default=16, help="steps timed through the 25%% cache (each of 1 and --batch tokens)")
     ap.add_argument("--cpu-layers", type=int, default=8, help="layer calls in the CPU-baseline sample")
     ap.add_argument("--cpu-runs", type=int, default=5)
@@ -1058,7 +1063,8 @@ def main() -> int:
     gemv, gemv_checks = None, []
     if "gemv" in sections:
         stage("gemv")
-        gemv = run_gemv(env, max(8, args.kernel_reps // 4), gemv_checks if args.report_dir else None)
+        gemv = run_gemv(env, max(8, args.kernel_reps // 4), gemv_checks if args.report_dir else None,
+                        calls=max(1, args.gemv_calls), rotate=max(64, args.gemv_rotate_mb) << 20)
     stack4 = None
     if "stack4" in sections:
         stage("stack4")
