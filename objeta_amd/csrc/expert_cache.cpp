@@ -215,7 +215,10 @@ int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t 
         if (r == hipSuccess) r = hipStreamWaitEvent(cs, e, 0);
         c->event_pool.push_back(e);
     }
-    if (r == hipSuccess) r = hipMemcpyAsync(b->ptr, h_src, n, hipMemcpyHostToDevice, cs);
+    // pinned sources by a kernel (a DMA copy behind a cross-stream wait starts late)
+    const void* dsrc = r == hipSuccess ? pinned_device_ptr(h_src, n) : nullptr;
+    if (dsrc) OBJ_TRY(launch_h2d_copy(cs, b->ptr, dsrc, n));
+    else if (r == hipSuccess) r = hipMemcpyAsync(b->ptr, h_src, n, hipMemcpyHostToDevice, cs);
     if (r == hipSuccess) {
         if (b->ready) c->event_pool.push_back(b->ready);
         b->ready = take_event(c);
@@ -1423,9 +1426,15 @@ extern "C" int32_t objeta_hip_moe_stack_cached(objeta_hip_context* ctx, int32_t 
         // ---- the layer, after its own copies
         do {
             if (rc) break;
-            hipError_t e = hipMemcpyAsync(d0 + o_rids, h0 + o_rids,
-                                          (o_tab - o_rids) + uni.size() * sizeof(objeta_hip_expert_ptrs),
-                                          hipMemcpyHostToDevice, s);
+            // the remapped ids and the table (from the pinned host stage, by a kernel when it can)
+            const size_t tb = (o_tab - o_rids) + uni.size() * sizeof(objeta_hip_expert_ptrs);
+            const void* hs = pinned_device_ptr(h0 + o_rids, tb);
+            hipError_t e = hipSuccess;
+            if (hs) {
+                if ((rc = launch_h2d_copy(s, d0 + o_rids, hs, tb))) break;
+            } else {
+                e = hipMemcpyAsync(d0 + o_rids, h0 + o_rids, tb, hipMemcpyHostToDevice, s);
+            }
             for (size_t j = 0; j < uni.size() && e == hipSuccess; ++j)
                 if (st.ready[j]) e = hipStreamWaitEvent(s, st.ready[j], 0);
             if (e != hipSuccess) {

@@ -19,6 +19,13 @@ int32_t launch_fp4_split(objeta_hip_context* ctx, hipStream_t s, const void* d_w
 
 int32_t launch_zero(hipStream_t s, void* d, uint64_t bytes);
 
+// The device address of pinned host bytes [h, h + n) when a kernel can copy them
+// (host memory from hipHostMalloc, h and n 16-byte multiples), else nullptr.
+const void* pinned_device_ptr(const void* h, size_t n);
+// dst[0, n) = the pinned host bytes at device address src_dev, by a kernel on `s`
+// (n, dst and src_dev 16-byte multiples).
+int32_t launch_h2d_copy(hipStream_t s, void* dst, const void* src_dev, size_t n);
+
 // GEMV over an FP8 E4M3 matrix with 128 x 128 E8M0 scale tiles (cols % 128 == 0).
 int32_t launch_fp8_rows(objeta_hip_context* ctx, hipStream_t s, const void* d_w, const void* d_s,
                         const float* d_x, float* d_y, uint64_t rows, uint64_t cols, uint64_t batch);

@@ -184,6 +184,72 @@ def test_layer_batch_runs_grouped_with_shared_expert(backend, fmt, E, K, T, H, I
     del keep, keep_s
 
 
+def test_layer_batch_calls_and_graph_replays(backend):
+    """The layer entry point at hidden 2048 (the router's two-launch batch form, then
+    the grouped products, whose workspace every call on the stream shares): layer
+    calls of different batch sizes in a row, a direct grouped call in between, and a
+    captured layer replayed with eager layer calls of other sizes between the
+    replays must each give the per-assignment path's result on the same selection
+    and the oracle router's ids; every replay must equal the eager call bit for
+    bit."""
+    import ctypes as C
+    from objeta_amd.api import check
+    E, K, H, I, TM = 32, 4, 2048, 256, 32
+    experts = make_experts(Q4, E, H, I, H, seed=71, gen="gauss")
+    table, keep = device_table(backend, Q4, experts)
+    w_r = orc.gauss(E * H, 72, 0.02)
+    d_wr = backend.to_device(w_r)
+    xs = orc.gauss(TM * H, 73, 1.0).reshape(TM, H)
+    d_x = backend.to_device(xs.ravel())
+    d_out, d_ref, d_out2 = backend.alloc(4 * TM * H), backend.alloc(4 * TM * H), backend.alloc(4 * TM * H)
+    d_ids, d_w = backend.alloc(4 * TM * K), backend.alloc(4 * TM * K)
+    d_ids2, d_w2 = backend.alloc(4 * TM * K), backend.alloc(4 * TM * K)
+    moe = MoeExecutor(backend)
+    st = backend.stream(0)
+
+    def layer(T, out=d_out, ids=d_ids, w=d_w):
+        moe.layer_device(Q4, table, d_wr, None, K, T, d_x, d_x, out, ids, w, H, I, H, stream=st)
+
+    def agrees(T, what):
+        moe.selected_device(Q4, table, d_ids, d_w, T, K, d_x, d_x, d_ref, H, I, H, stream=st)
+        backend.synchronize(st)
+        assert moe.device_error() == 0, what
+        ids = d_ids.download(np.uint32, T * K).reshape(T, K)
+        for t in (0, T // 2, T - 1):
+            rid, _, _, _ = orc.router(w_r, xs[t], E, H, K, renormalize=True)
+            assert np.array_equal(ids[t], rid), (what, t)
+        out = d_out.download(np.float32, T * H)
+        per = d_ref.download(np.float32, T * H)
+        assert float(np.max(np.abs(out - per))) <= 1e-4 * float(np.max(np.abs(per))), what
+
+    for T in (16, 12, 32, 13):
+        layer(T)
+        agrees(T, f"layer {T}")
+    # a grouped call on the ids of the last layer call, grouped by a launch of its own
+    moe.grouped_device(Q4, table, d_ids, d_w, 13, K, d_x, d_x, d_out, H, I, H, stream=st)
+    agrees(13, "grouped 13")
+    layer(16)
+    agrees(16, "layer 16 after grouped")
+    ref = d_out.download(np.float32, 16 * H)
+    check(backend.L.objeta_hip_graph_begin_capture(backend.ctx, st))
+    layer(16)
+    g = C.c_void_p()
+    check(backend.L.objeta_hip_graph_end_capture(backend.ctx, st, C.byref(g)))
+    try:
+        for rep in range(3):
+            d_out.upload(np.zeros(16 * H, np.float32), st)
+            check(backend.L.objeta_hip_graph_launch(backend.ctx, g, st))
+            backend.synchronize(st)
+            assert moe.device_error() == 0, rep
+            assert np.array_equal(d_out.download(np.float32, 16 * H), ref), rep
+            layer(12 + rep, out=d_out2, ids=d_ids2, w=d_w2)
+            backend.synchronize(st)
+    finally:
+        check(backend.L.objeta_hip_graph_destroy(backend.ctx, g))
+    agrees(16, "after the replays")
+    del keep
+
+
 @pytest.mark.parametrize("fmt,K", [(Q4, 4), (Q5, 8), (IQ3, 4), (FP4, 8)])
 def test_layer_one_token_shared_expert_second_down_launch(backend, fmt, K):
     """One token, intermediate 2048 (32 lanes per row), k % 4 == 0 and a shared
