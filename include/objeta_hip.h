@@ -370,8 +370,13 @@ int32_t objeta_hip_moe_layer_shared_device(objeta_hip_context* ctx, int32_t form
                                            uint32_t* d_ids_out, float* d_weights_out, uint64_t hidden,
                                            uint64_t intermediate, uint64_t out_dim, float swiglu_limit);
 
-/* Reads and clears the context's device error word (non-zero after a kernel met
- * an expert id outside its table). Synchronises the context's streams. */
+/* Reads and clears the context's device error word. Bit 0: a kernel met an expert
+ * id outside its table. Bit 1 (a report, not a failure): a router call's selecting
+ * workgroup found other workgroups' logits still missing after its spin limit (the
+ * device kept them from running, about a second by default) and computed every
+ * logit itself in the reference's order, so its result is exact. The spin limit is
+ * read at objeta_hip_init from the environment variable OBJETA_HIP_ROUTER_SPIN_LIMIT
+ * (polls; 0 = never wait). Synchronises the context's streams. */
 int32_t objeta_hip_device_error(objeta_hip_context* ctx, uint32_t* out);
 
 /* ------------------------------------------------------------ expert cache */

@@ -108,6 +108,9 @@ struct objeta_hip_context {
     std::vector<void*> caches;                    // live caches created on this context
     size_t host_stage_bytes = 0;
     uint32_t* err_word = nullptr;  // device error word (bits set by kernels, read by objeta_hip_device_error)
+    // polls of the router's selecting workgroup before it computes the missing logits
+    // itself (OBJETA_HIP_ROUTER_SPIN_LIMIT at init; default about a second)
+    uint32_t router_spin_limit = 1u << 20;
     float* static_act = nullptr;   // device address of this device's static activation scratch
     std::mutex mu;
 };

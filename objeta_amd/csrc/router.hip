@@ -29,19 +29,25 @@ using dev::gptr;
 using dev::as_global;
 
 // Workgroup 0 of token t: gathers the words of this epoch, selects, writes the
-// ids and weights and advances counters[t].
+// ids and weights and advances counters[t]. If some words have not arrived after
+// spin_limit polls (the other workgroups not yet scheduled: the device busy with
+// other work), it computes every logit itself in the reference's order, so the
+// result never depends on which workgroups are resident together, and sets bit 1
+// of the error word. spin_limit 0: it never waits.
 template <class XAt>
 __device__ void router_select(const float* __restrict__ w_r, const float* __restrict__ bias,
                               const float* __restrict__ xt, XAt xat, uint32_t n_experts, uint32_t hidden, uint32_t k,
                               int renormalize, uint32_t* __restrict__ ids, float* __restrict__ weights,
                               const uint64_t* ws_logit, const uint64_t* ws_bound, uint32_t epoch,
                               uint32_t* __restrict__ counter, uint32_t* __restrict__ err, float* scratch,
-                              uint32_t scratch_floats, const objeta_hip_expert_ptrs* tab_lds = nullptr,
+                              uint32_t scratch_floats, uint32_t spin_limit,
+                              const objeta_hip_expert_ptrs* tab_lds = nullptr,
                               objeta_hip_expert_ptrs* sel_tab = nullptr) {
     __shared__ SelectLds<kMaxExperts> s;
     __shared__ int s_pending;
     stage_exptab(s);  // the softmax exps' table, in LDS before the ranking needs it
-    for (uint32_t spin = 0;; ++spin) {
+    bool starved = spin_limit == 0;  // 0: never wait
+    for (uint32_t spin = 0; !starved; ++spin) {
         if (threadIdx.x == 0) s_pending = 0;
         __syncthreads();
         int pending = 0;
@@ -55,15 +61,16 @@ __device__ void router_select(const float* __restrict__ w_r, const float* __rest
         if (pending) s_pending = 1;
         __syncthreads();
         if (!s_pending) break;
-        if (spin >= kSpinLimit) {  // a producer never published: flag it and stop waiting
-            if (threadIdx.x == 0) atomicOr(err, 2u);
+        if (spin >= spin_limit) {  // uniform: every thread read the same s_pending
+            starved = true;
             break;
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    if (!select_certain(s, n_experts, k, renormalize) &&
-        !select_refine(s, w_r, bias, xat, n_experts, hidden, k, renormalize, scratch, scratch_floats) &&
-        !select_underflow(s, w_r, bias, xat, n_experts, hidden, k, scratch, scratch_floats))
+    if (starved && threadIdx.x == 0) atomicOr(err, 2u);  // reported; the result stays exact
+    if (starved || (!select_certain(s, n_experts, k, renormalize) &&
+                    !select_refine(s, w_r, bias, xat, n_experts, hidden, k, renormalize, scratch, scratch_floats) &&
+                    !select_underflow(s, w_r, bias, xat, n_experts, hidden, k, scratch, scratch_floats)))
         select_sequential(s, w_r, bias, xat, n_experts, hidden, k);
     write_selection(s, k, renormalize, ids, weights);
     // the selected experts' table entries (the table was staged in LDS while the
@@ -78,7 +85,7 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
     const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
     uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
     float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
-    uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ err, uint32_t spin_limit) {
     const uint32_t t = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t e = blockIdx.x * kRWaves + (threadIdx.x >> 6);
@@ -108,7 +115,7 @@ __global__ __launch_bounds__(kRThreads) void router_kernel(
     __shared__ float scratch[kRWaves * 256];
     router_select(w_r, bias, xt, [xt](uint32_t h) { return xt[h]; }, n_experts, hidden, k, renormalize,
                   ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit, ws_bound, epoch,
-                  &counters[t], err, scratch, kRWaves * 256);
+                  &counters[t], err, scratch, kRWaves * 256, spin_limit);
 }
 
 // hidden % 256 == 0, hidden <= 256 * NB: the row sits lane-contiguously in
@@ -122,7 +129,7 @@ __global__ __launch_bounds__(kRThreads) void router_lanes_kernel(
     const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
     uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
     float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
-    uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ err, uint32_t spin_limit) {
     extern __shared__ float xs[];  // x in the padded pair layout: (hidden / 64) * kPadX floats
     const uint32_t t = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63;
@@ -167,7 +174,7 @@ __global__ __launch_bounds__(kRThreads) void router_lanes_kernel(
     const float* xl = xs;
     router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,
                   renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit,
-                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch);
+                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch, spin_limit);
 }
 
 // hidden % 1024 == 0, hidden <= 1024 * NB: one workgroup per expert, the row split
@@ -179,7 +186,7 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
     const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
     uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
     float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
-    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ table,
+    uint32_t* __restrict__ err, uint32_t spin_limit, const objeta_hip_expert_ptrs* __restrict__ table,
     objeta_hip_expert_ptrs* __restrict__ sel_tab) {
     extern __shared__ float xs[];  // x in the padded pair layout: (hidden / 64) * kPadX floats
     __shared__ double red[8];
@@ -259,7 +266,7 @@ __global__ __launch_bounds__(kRThreads) void router_split_kernel(
     const float* xl = xs;
     router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,
                   renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit,
-                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch, tab_lds,
+                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch, spin_limit, tab_lds,
                   sel_tab ? sel_tab + static_cast<size_t>(t) * k : nullptr);
 }
 
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(kRThreads) void router_select_batch_kernel(
     const float* __restrict__ w_r, const float* __restrict__ bias, const float* __restrict__ x,
     uint32_t n_experts, uint32_t hidden, uint32_t k, int renormalize, uint32_t* __restrict__ ids,
     float* __restrict__ weights, uint64_t* __restrict__ ws, uint32_t* __restrict__ counters,
-    uint32_t* __restrict__ err, const objeta_hip_expert_ptrs* __restrict__ table,
+    uint32_t* __restrict__ err, uint32_t spin_limit, const objeta_hip_expert_ptrs* __restrict__ table,
     objeta_hip_expert_ptrs* __restrict__ sel_tab) {
     extern __shared__ float xs[];  // x in the padded pair layout, then the refinement scratch
     const uint32_t t = blockIdx.x;
@@ -349,7 +356,7 @@ __global__ __launch_bounds__(kRThreads) void router_select_batch_kernel(
     const float* xl = xs;
     router_select(w_r, bias, xt, [xl](uint32_t h) { return xl[(h >> 6) * kPadX + (h & 63)]; }, n_experts, hidden, k,
                   renormalize, ids + static_cast<size_t>(t) * k, weights + static_cast<size_t>(t) * k, ws_logit,
-                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch, table,
+                  ws_bound, epoch, &counters[t], err, xs + x_floats, kRefineScratch, spin_limit, table,
                   sel_tab ? sel_tab + static_cast<size_t>(t) * k : nullptr);
 }
 
@@ -388,6 +395,7 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
     const dim3 grid(static_cast<uint32_t>((n_experts + kRWaves - 1) / kRWaves), static_cast<uint32_t>(n_tokens));
     const bool vec = hidden % 4 == 0 && reinterpret_cast<uintptr_t>(w_r) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     uint32_t* err = ctx->err_word;
+    const uint32_t spin = ctx->router_spin_limit;
     const bool lanes = vec && hidden % 256 == 0 && hidden <= 256u * 32u;
     const bool split = vec && hidden % 1024 == 0 && hidden <= 1024u * 8u;
     // a batch of the split kernel's shapes: logits for groups of tokens, then one
@@ -413,7 +421,7 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
         const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
         hipLaunchKernelGGL(router_select_batch_kernel, dim3(static_cast<uint32_t>(n_tokens)), dim3(kRThreads), lds, s,
                            w_r, bias, x, static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                           static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err,
+                           static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err, spin,
                            st ? table : nullptr, st);
     } else if (split) {
         const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float) +
@@ -422,31 +430,31 @@ int32_t launch_router(objeta_hip_context* ctx, hipStream_t s, const float* w_r, 
         if (hidden <= 1024u * 2u)
             hipLaunchKernelGGL(router_split_kernel<2>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err,
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err, spin,
                                st ? table : nullptr, st);
         else
             hipLaunchKernelGGL(router_split_kernel<8>, sgrid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err,
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err, spin,
                                st ? table : nullptr, st);
     } else if (lanes) {
         const size_t lds = (static_cast<size_t>(hidden / 64) * kPadX + kRefineScratch) * sizeof(float);
         if (hidden <= 256u * 8u)
             hipLaunchKernelGGL(router_lanes_kernel<8>, grid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err);
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err, spin);
         else
             hipLaunchKernelGGL(router_lanes_kernel<32>, grid, dim3(kRThreads), lds, s, w_r, bias, x,
                                static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden),
-                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err);
+                               static_cast<uint32_t>(k), renormalize, ids, weights, ws, counters, err, spin);
     } else if (vec)
         hipLaunchKernelGGL(router_kernel<true>, grid, dim3(kRThreads), 0, s, w_r, bias, x,
                            static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden), static_cast<uint32_t>(k),
-                           renormalize, ids, weights, ws, counters, err);
+                           renormalize, ids, weights, ws, counters, err, spin);
     else
         hipLaunchKernelGGL(router_kernel<false>, grid, dim3(kRThreads), 0, s, w_r, bias, x,
                            static_cast<uint32_t>(n_experts), static_cast<uint32_t>(hidden), static_cast<uint32_t>(k),
-                           renormalize, ids, weights, ws, counters, err);
+                           renormalize, ids, weights, ws, counters, err, spin);
     OBJ_HIP(hipGetLastError(), action);
     return 0;
 }

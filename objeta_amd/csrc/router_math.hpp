@@ -269,7 +269,6 @@ __device__ __forceinline__ uint64_t tag(float v, uint32_t epoch) {
     return (static_cast<uint64_t>(epoch) << 32) | __builtin_bit_cast(uint32_t, v);
 }
 
-constexpr uint32_t kSpinLimit = 1u << 20;  // bounded waits (about a second), then the error word
 
 // grid = (ceil(E / 4), T). Wave w of block b handles expert b*4 + w of token y and
 // publishes {logit, epoch} and {bound, epoch}. Workgroup 0 of each token then

@@ -236,6 +236,11 @@ int32_t objeta_hip_init(const objeta_hip_init_options* opts, objeta_hip_context*
     auto* ctx = new objeta_hip_context();
     ctx->device = static_cast<int>(o.device_ordinal);
     ctx->info = info;
+    if (const char* v = std::getenv("OBJETA_HIP_ROUTER_SPIN_LIMIT")) {
+        char* end = nullptr;
+        const unsigned long n = std::strtoul(v, &end, 10);
+        if (end != v && *end == '\0' && n <= 0xFFFFFFFFul) ctx->router_spin_limit = static_cast<uint32_t>(n);
+    }
     auto fail_cleanup = [&](int32_t rc) {
         objeta_hip_destroy(ctx);
         return rc;

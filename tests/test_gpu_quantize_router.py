@@ -121,6 +121,32 @@ def test_router_near_ties_take_the_sequential_path(backend):
         assert np.allclose(ws[t], rw, rtol=2e-5, atol=1e-6)
 
 
+def test_router_selects_exactly_without_the_other_workgroups(monkeypatch):
+    """The router's selecting workgroup waits for the other workgroups' logits only up
+    to its spin limit; then (a device kept busy by other work) it computes every logit
+    itself in the reference's order. With the limit at 0 it never waits, on a context
+    of its own: the ids and weights still equal the oracle's for the one-launch shapes
+    (hidden 2048 and 7168, one workgroup per expert; hidden 512, one wave per expert)
+    and for a two-launch batch, and bit 1 of the device error word reports the path
+    (bit 0, a bad id, stays clear)."""
+    from objeta_amd import HipBackend, MoeExecutor
+    monkeypatch.setenv("OBJETA_HIP_ROUTER_SPIN_LIMIT", "0")
+    be = HipBackend(0, 1)
+    try:
+        for ne, k, hidden, tokens in [(128, 8, 2048, 1), (256, 8, 7168, 1), (64, 4, 512, 1), (128, 8, 2048, 4)]:
+            w = orc.gauss(ne * hidden, ne + hidden, 0.02)
+            x = orc.gauss(tokens * hidden, hidden + 7, 1.0)
+            bias = orc.gauss(ne, 11, 0.5)
+            ids, ws = _router(be, w, x, bias, ne, hidden, k, tokens)
+            for t in range(tokens):
+                rid, rw, _, _ = orc.router(w, x[t * hidden:(t + 1) * hidden], ne, hidden, k, bias=bias)
+                assert list(ids[t]) == list(rid), (ne, hidden, t)
+                assert np.allclose(ws[t], rw, rtol=2e-5, atol=1e-6), (ne, hidden, t)
+            assert MoeExecutor(be).device_error() == 2, (ne, hidden)
+    finally:
+        be.close()
+
+
 def test_router_validation(backend):
     from objeta_amd import HipError
     with pytest.raises(HipError) as e:
