@@ -129,7 +129,10 @@ int32_t objeta_hip_free(objeta_hip_context* ctx, void* d_ptr);
 int32_t objeta_hip_alloc_pinned_host(objeta_hip_context* ctx, uint64_t bytes, void** h_out);
 int32_t objeta_hip_free_pinned_host(objeta_hip_context* ctx, void* h_ptr);
 /* copy_from_slice / copy_to_vec / copy_dtod (stream.rs:104-201), asynchronous on
- * `stream` (pageable host memory makes the HIP runtime stage the copy). */
+ * `stream` (pageable host memory makes the HIP runtime stage the copy). A host to
+ * device copy from pinned memory (objeta_hip_alloc_pinned_host) whose source,
+ * destination and size are 16-byte multiples runs as a kernel reading the host
+ * memory through its device mapping, which on MI355X outruns the DMA engine. */
 int32_t objeta_hip_copy_h2d(objeta_hip_context* ctx, objeta_hip_stream stream, void* d_dst,
                             const void* h_src, uint64_t bytes);
 int32_t objeta_hip_copy_d2h(objeta_hip_context* ctx, objeta_hip_stream stream, void* h_dst,

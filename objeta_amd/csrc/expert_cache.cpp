@@ -68,6 +68,7 @@ struct Block {
     size_t bytes = 0;
     int refs = 0;          // executor references of a call in flight
     bool in_cache = false;  // owned by a cache entry
+    bool carved = false;    // inside one of the cache's chunks (freed with the chunk)
     std::vector<hipEvent_t> fence;
     hipEvent_t ready = nullptr;  // recorded on the copy stream after the fill; NULL once known complete
 };
@@ -90,7 +91,12 @@ struct objeta_hip_expert_cache {
     std::unordered_map<const void*, objeta::Block*> transients;
     std::vector<hipEvent_t> event_pool;
     size_t free_bytes = 0;
-    size_t device_bytes = 0;  // all blocks allocated by this cache
+    size_t device_bytes = 0;  // all device memory allocated by this cache
+    struct Chunk {
+        char* base;
+        size_t size, used;
+    };
+    std::vector<Chunk> chunks;  // blocks are carved from these (see acquire_block)
 };
 
 namespace objeta {
@@ -139,8 +145,10 @@ void destroy_block(Cache* c, Block* b) {
     if (c->ctx && b->ptr) {
         for (hipEvent_t e : b->fence) (void)hipEventSynchronize(e);
         if (b->ready) (void)hipEventSynchronize(b->ready);
-        (void)hipFree(b->ptr);
-        c->device_bytes -= b->bytes;
+        if (!b->carved) {  // a carved block's bytes stay with its chunk
+            (void)hipFree(b->ptr);
+            c->device_bytes -= b->bytes;
+        }
     }
     for (hipEvent_t e : b->fence) c->event_pool.push_back(e);
     if (b->ready) c->event_pool.push_back(b->ready);
@@ -162,6 +170,36 @@ void retire_block(Cache* c, Block* b) {
     }
 }
 
+// Blocks come from 64 MiB chunks, carved in order: a miss then costs no hipMalloc
+// (about 50-100 us each on MI355X, several per layer while a cache fills). A carved
+// block is recycled through the free lists like any other, but its bytes return to
+// the device only with its chunk, when the cache releases its memory; carving stops
+// once the chunks hold the capacity plus the free lists' cap, and blocks past that
+// are allocated one by one as before.
+constexpr size_t kChunkBytes = size_t(64) << 20;
+
+bool carve_block(Cache* c, Block* b) {
+    const size_t need = (b->bytes + 255) & ~size_t(255);
+    if (c->chunks.empty() || c->chunks.back().size - c->chunks.back().used < need) {
+        size_t held = 0;
+        for (const auto& ch : c->chunks) held += ch.size;
+        const size_t size = need > kChunkBytes ? need : kChunkBytes;
+        if (held + size > static_cast<size_t>(c->st.capacity_bytes) + free_list_cap(c)) return false;
+        void* p = nullptr;
+        if (hipMalloc(&p, size) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        c->chunks.push_back({static_cast<char*>(p), size, 0});
+        c->device_bytes += size;
+    }
+    auto& ch = c->chunks.back();
+    b->ptr = ch.base + ch.used;
+    b->carved = true;
+    ch.used += need;
+    return true;
+}
+
 // A block of exactly `bytes` whose previous contents may be overwritten by work
 // enqueued on `s` from now on.
 int32_t acquire_block(Cache* c, size_t bytes, hipStream_t s, Block** out) {
@@ -170,12 +208,21 @@ int32_t acquire_block(Cache* c, size_t bytes, hipStream_t s, Block** out) {
         Block* b = it->second;
         c->free_blocks.erase(it);
         c->free_bytes -= b->bytes;
-        for (hipEvent_t e : b->fence) OBJ_HIP(hipStreamWaitEvent(s, e, 0), "fence recycled cache block");
+        for (hipEvent_t e : b->fence) {  // a fence already passed needs no wait
+            const hipError_t q = hipEventQuery(e);
+            if (q == hipSuccess) continue;
+            if (q != hipErrorNotReady) (void)hipGetLastError();
+            OBJ_HIP(hipStreamWaitEvent(s, e, 0), "fence recycled cache block");
+        }
         *out = b;
         return 0;
     }
     Block* b = new Block();
     b->bytes = bytes;
+    if (c->ctx && bytes && carve_block(c, b)) {
+        *out = b;
+        return 0;
+    }
     if (c->ctx && bytes) {
         hipError_t e = hipMalloc(&b->ptr, bytes);
         if (e != hipSuccess && !c->free_blocks.empty()) {
@@ -365,6 +412,9 @@ void release_device(Cache* c) {
     for (auto& kv : c->free_blocks) all.push_back(kv.second);
     for (auto& kv : c->transients) all.push_back(kv.second);
     for (Block* b : all) destroy_block(c, b);
+    for (const auto& ch : c->chunks) (void)hipFree(ch.base);  // every block is synchronised above
+    c->device_bytes = 0;
+    c->chunks.clear();
     c->map.clear();
     c->order.clear();
     c->pinned.clear();
@@ -749,6 +799,7 @@ struct StagedExperts {
     uint64_t by_kind[3] = {0, 0, 0};
     bool any_copy = false;
 
+    Cache* events = nullptr;                      // where the ready events come from and go back
     void release() {
         for (auto& hb : held) {
             hb.second->refs -= 1;
@@ -757,8 +808,10 @@ struct StagedExperts {
         held.clear();
     }
     ~StagedExperts() {
-        for (hipEvent_t r : ready)
-            if (r) (void)hipEventDestroy(r);
+        for (hipEvent_t r : ready) {
+            if (r && events) events->event_pool.push_back(r);
+            else if (r) (void)hipEventDestroy(r);
+        }
     }
 };
 
@@ -771,6 +824,10 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
     const bool fp4 = format == OBJETA_HIP_FP4_E2M1;
     Cache* pool = transient_pool(ctx);
     st.ready.assign(k, nullptr);
+    st.events = pool;
+    // the copies are ordered after `s` once, at the first miss (each copy's own wait
+    // would be one more stream wait per tensor)
+    hipStream_t order_after = s;
     for (uint64_t j = 0; j < k; ++j) {
         const uint64_t e = sel_ids[j];
         TensorRef t[6];
@@ -806,7 +863,8 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
             }
             Cache* home = cache && !bypass ? cache : pool;
             if (!hit) {
-                OBJ_TRY(stage_tensor(home, t[q].h, t[q].len, s, &b));
+                OBJ_TRY(stage_tensor(home, t[q].h, t[q].len, order_after, &b));
+                order_after = nullptr;
                 copied = true;
                 if (cache && !bypass) (void)insert_block(cache, key, b, t[q].len);
             }
@@ -818,11 +876,10 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
         }
         if (copied) {
             st.any_copy = true;
-            hipEvent_t r = nullptr;
-            if (hipEventCreateWithFlags(&r, hipEventDisableTiming) != hipSuccess ||
-                hipEventRecord(r, ctx->copy_stream) != hipSuccess) {
+            hipEvent_t r = take_event(pool);
+            if (!r || hipEventRecord(r, ctx->copy_stream) != hipSuccess) {
                 (void)hipGetLastError();
-                if (r) (void)hipEventDestroy(r);
+                if (r) pool->event_pool.push_back(r);
                 OBJ_FAIL(kDriver, "record copy event", "event failure");
             }
             st.ready[j] = r;

@@ -380,6 +380,14 @@ static int32_t copy_async(objeta_hip_context* ctx, objeta_hip_stream stream, voi
 
 int32_t objeta_hip_copy_h2d(objeta_hip_context* ctx, objeta_hip_stream stream, void* d_dst,
                             const void* h_src, uint64_t bytes) {
+    // pinned, 16-byte aligned sources through a kernel (copy.hip), the rest by HIP's copy
+    if (ctx && d_dst && reinterpret_cast<uintptr_t>(d_dst) % 16 == 0) {
+        OBJ_TRY(check_ctx(ctx, "copy host to device"));
+        if (const void* src = objeta::pinned_device_ptr(h_src, bytes)) {
+            OBJ_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+            return objeta::launch_h2d_copy(resolve_stream(ctx, stream), d_dst, src, bytes);
+        }
+    }
     return copy_async(ctx, stream, d_dst, h_src, bytes, hipMemcpyHostToDevice, "copy host to device");
 }
 
