@@ -412,7 +412,10 @@ void release_device(Cache* c) {
     for (auto& kv : c->free_blocks) all.push_back(kv.second);
     for (auto& kv : c->transients) all.push_back(kv.second);
     for (Block* b : all) destroy_block(c, b);
-    for (const auto& ch : c->chunks) (void)hipFree(ch.base);  // every block is synchronised above
+    // a carved block still held by a call in flight is in none of the lists above: wait
+    // for the device before its chunk goes
+    if (!c->chunks.empty()) (void)hipDeviceSynchronize();
+    for (const auto& ch : c->chunks) (void)hipFree(ch.base);
     c->device_bytes = 0;
     c->chunks.clear();
     c->map.clear();
