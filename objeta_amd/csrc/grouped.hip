@@ -1035,15 +1035,28 @@ hipError_t launch_gemv_mfma_sv(hipStream_t s, const void* w, const void* ws, con
     return hipGetLastError();
 }
 
-// 8 slabs (128 rows) per workgroup when that still gives two workgroups per CU,
-// else 4; 16-byte weight units when every range is full and its rows 16-byte aligned.
+// 8 slabs (128 rows) per workgroup for Q4_0 / Q5_0 when that still gives two
+// workgroups per CU, else 4; 16-byte weight units when every range is full and its
+// rows 16-byte aligned. IQ3_0 and split FP4 keep 4 slabs: their 8-slab forms need
+// 212 and 256 VGPRs (one or two waves per SIMD), and measured slower at 14336 x 4096
+// and 8 vectors (IQ3_0 29.3 against 22.9 us, FP4 38.8 against 18.5 us), where Q4_0
+// and Q5_0 gain from 8 (19.0 against 23.9, 23.0 against 33.4 us).
+template <class R>
+constexpr bool kGemvWideTiles = false;
+template <>
+constexpr bool kGemvWideTiles<QRows<kQ4>> = true;
+template <>
+constexpr bool kGemvWideTiles<QRows<kQ5>> = true;
+
 template <class R>
 hipError_t launch_gemv_mfma_t(hipStream_t s, const void* w, const void* ws, const float* x, float* y, float* part,
                               uint32_t rows, uint32_t cols, uint32_t nv, uint32_t ks, uint32_t cus) {
-    const bool s8 = static_cast<uint64_t>((rows + 127) / 128) * ks >= 2ull * cus;
     const bool v4 = cols % kGemvRange == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
-    if (s8) return v4 ? launch_gemv_mfma_sv<R, 8, 4>(s, w, ws, x, y, part, rows, cols, nv, ks)
+    if constexpr (kGemvWideTiles<R>) {
+        if (static_cast<uint64_t>((rows + 127) / 128) * ks >= 2ull * cus)
+            return v4 ? launch_gemv_mfma_sv<R, 8, 4>(s, w, ws, x, y, part, rows, cols, nv, ks)
                       : launch_gemv_mfma_sv<R, 8, 1>(s, w, ws, x, y, part, rows, cols, nv, ks);
+    }
     return v4 ? launch_gemv_mfma_sv<R, 4, 4>(s, w, ws, x, y, part, rows, cols, nv, ks)
               : launch_gemv_mfma_sv<R, 4, 1>(s, w, ws, x, y, part, rows, cols, nv, ks);
 }

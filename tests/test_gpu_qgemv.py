@@ -224,8 +224,9 @@ def test_gemv_batched_mfma_column_ranges(backend, quant, fmt, rows, cols, batch)
 @pytest.mark.parametrize("cols", [4096, 4160])
 def test_gemv_batched_mfma_wide_tiles(backend, quant, fmt, cols):
     """8200 rows over 8 or 9 column ranges give enough workgroups for 128-row tiles
-    (8 slabs per workgroup, the last tile 8 rows deep): 16-byte weight units when every
-    range is full (4096 columns), dword units with a 64-column last range (4160)."""
+    (8 slabs per workgroup, the last tile 8 rows deep) for Q4_0 and Q5_0; IQ3_0 keeps
+    64-row tiles: 16-byte weight units when every range is full (4096 columns), dword
+    units with a 64-column last range (4160)."""
     rows, batch = 8200, 8
     m = orc.gauss(rows * cols, 50 + cols, 0.02)
     q = orc.quantize_matrix(int(fmt), m, rows, cols)
