@@ -335,6 +335,44 @@ __device__ __forceinline__ void fp4_to_h2x4(uint32_t n, h2 (&p)[4]) {
     p[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(n, 1.0f, 3);
 }
 
+// Four of the reference's E4M3 codes (rules::f8e4m3_to_f32, deepseek.rs:799-829)
+// rewritten to the OCP E4M3 codes of the same values, so that gfx950's hardware E4M3
+// conversion decodes them: exponent field 0 means m * 2^-5 in the reference (m * 2^-9
+// in OCP), so m goes to the code of m / 32 (0, 0x10, 0x18, 0x1C, 0x20, 0x22, 0x24,
+// 0x26, picked by v_perm); field 15 means +-448 for every mantissa (OCP: 256 (1 +
+// m/8), NaN at m = 7), so it goes to 0x7E. Signs are kept; other codes pass through.
+__device__ __forceinline__ uint32_t fp8_ref_to_ocp(uint32_t d) {
+    const uint32_t e = d & 0x78787878u;
+    const uint32_t z = ~(e + 0x78787878u) & 0x80808080u;  // bit 7 of the bytes whose field is 0
+    const uint32_t f = (e + 0x08080808u) & 0x80808080u;   // bit 7 of the bytes whose field is 15
+    const uint32_t zb = z >> 7, fb = f >> 7;
+    const uint32_t zm = (zb << 8) - zb, fm = (fb << 8) - fb;  // 0xFF in those bytes
+    const uint32_t sign = d & 0x80808080u;
+    const uint32_t small = __builtin_amdgcn_perm(0x26242220u, 0x1C181000u, d & 0x07070707u) | sign;
+    const uint32_t t = (small & zm) | (d & ~zm);
+    return ((0x7E7E7E7Eu | sign) & fm) | (t & ~fm);
+}
+
+// The reference's decode of the 4 E4M3 codes of a dword (byte i -> w[i]), exact.
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t d, float (&w)[4]) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const uint32_t r = fp8_ref_to_ocp(d);
+    const f2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(r, 1.0f, false);
+    const f2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(r, 1.0f, true);
+    w[0] = lo.x;
+    w[1] = lo.y;
+    w[2] = hi.x;
+    w[3] = hi.y;
+}
+
+// The same as fp16 pairs (bytes 0, 1 and 2, 3): every value the reference decodes is
+// an exact fp16 (|v| in [2^-5, 448], or 0).
+__device__ __forceinline__ void fp8x4_to_h2x2(uint32_t d, h2& lo, h2& hi) {
+    const uint32_t r = fp8_ref_to_ocp(d);
+    lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(r, 1.0f, false);
+    hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(r, 1.0f, true);
+}
+
 // sum_i E2M1(q_i) * x_i over 8 weights (xa = x0..x3, xb = x4..x7); the caller
 // multiplies by the block scale.
 template <int NT>

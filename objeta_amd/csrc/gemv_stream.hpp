@@ -134,8 +134,7 @@ struct Fp8Rows {
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
             float wv[4];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) wv[b] = rules::f8e4m3_to_f32((d[q] >> (8 * b)) & 0xFFu);
+            fp8x4_to_f32(d[q], wv);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const float4 xv = *reinterpret_cast<const float4*>(xs[t] + 4 * q);

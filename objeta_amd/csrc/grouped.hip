@@ -441,13 +441,10 @@ struct Tile<Fp8Rows> {
         scale = e8m0_to_f32((ts >> (8 * (b >> 2))) & 0xFFu);
         const uint32_t d0 = *reinterpret_cast<const uint32_t*>(w + 32 * b + 8 * kg);
         const uint32_t d1 = *reinterpret_cast<const uint32_t*>(w + 32 * b + 8 * kg + 4);
-        half8 h;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // element order
-            h[i] = static_cast<_Float16>(rules::f8e4m3_to_f32((d0 >> (8 * i)) & 0xFFu));
-            h[4 + i] = static_cast<_Float16>(rules::f8e4m3_to_f32((d1 >> (8 * i)) & 0xFFu));
-        }
-        return h;
+        h2 p[4];  // element order
+        fp8x4_to_h2x2(d0, p[0], p[1]);
+        fp8x4_to_h2x2(d1, p[2], p[3]);
+        return pack8(p[0], p[1], p[2], p[3]);
     }
 };
 

@@ -174,6 +174,30 @@ def test_fp8_act_fp4_gemv_random(backend, quant, rows, cols, batch):
         assert_gemv_close(y[b], ref)
 
 
+def test_fp8_weight_codes_exhaustive(backend, quant):
+    """Every E4M3 weight code through the device decode: row r holds code r in column
+    r mod 16 (so each code sits at several byte positions of a dword across rows) and
+    zeros elsewhere, against x = 1.0 (code 0x38, scale 2^0) and weight scale 2^0, so
+    y[r] is the decoded value of code r. Expected values from the format's closed form
+    (deepseek.rs:799-829): field 0 -> m / 32, field 15 -> 448, else 2^(e-7) (1 + m/8)."""
+    rows, cols = 256, 128
+    w = np.zeros((rows, cols), np.uint8)
+    w[np.arange(rows), np.arange(rows) % 16] = np.arange(rows)
+    ws = np.array([0x7F, 0x7F], np.uint8)
+    av = np.full(cols, 0x38, np.uint8)
+    asc = np.array([127], np.uint8)
+    want = []
+    for c in range(rows):
+        e, m = (c >> 3) & 15, c & 7
+        v = m / 32 if e == 0 else (448.0 if e == 15 else 2.0 ** (e - 7) * (1 + m / 8))
+        want.append(-v if c & 0x80 else v)
+    assert orc.f8e4m3_to_f32(np.arange(rows, dtype=np.uint8)).tolist() == want
+    dy = backend.alloc(4 * rows)
+    quant.fp8_act_fp8_weight_gemv_device(None, backend.to_device(av), backend.to_device(asc),
+                                         backend.to_device(w.ravel()), backend.to_device(ws), dy, rows, cols)
+    assert dy.download(F32, rows).tolist() == want
+
+
 def test_fp8_act_fp8_gemv_tile_scaled_kat(backend, quant):
     """test_fp8_gemv_tile_scaled (deepseek.rs:1359-1380) padded to one 128-column tile:
     rows (1, 2) and (3, 4) at scale 1 against x = (1, 1) quantized. act_quant(1.0) at
