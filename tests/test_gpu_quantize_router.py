@@ -182,10 +182,10 @@ def test_router_underflowing_probabilities_order_by_index(backend, ne, hidden, s
     assert zero_tail > 0  # the index-ordered zero-probability case is exercised
 
 
-def _close_calls(ne, hidden, seed, gaps):
+def _close_calls(ne, hidden, seed, gaps, sd=0.02):
     """W_r whose logits for one token have adjacent top-ranked pairs `gaps` apart
     (closer than the parallel error bound, farther than the probability margin)."""
-    w = orc.gauss(ne * hidden, seed, 0.02).reshape(ne, hidden).copy()
+    w = orc.gauss(ne * hidden, seed, sd).reshape(ne, hidden).copy()
     x = orc.gauss(hidden, seed + 1, 1.0)
     j = int(np.argmax(np.abs(x)))
     for r, gap in gaps:
@@ -196,16 +196,29 @@ def _close_calls(ne, hidden, seed, gaps):
     return w, x
 
 
-@pytest.mark.parametrize("seed", [31, 32, 33, 34])
-def test_router_close_calls_are_settled_exactly(backend, seed):
+@pytest.mark.parametrize("ne,hidden,seed", [(128, 2048, 31), (128, 2048, 32), (128, 2048, 33), (128, 2048, 34),
+                                            (256, 7168, 35), (64, 512, 36), (96, 1000, 37), (96, 999, 38)])
+def test_router_close_calls_are_settled_exactly(backend, ne, hidden, seed):
     """Selected experts 3e-5 apart (and one pair at the top-8 boundary): the kernel
-    recomputes just those logits in the reference's order and must still agree."""
-    ne, hidden, k = 128, 2048, 8
-    w, x = _close_calls(ne, hidden, seed, [(1, 3e-5), (4, 2e-5), (7, 3e-5)])
+    recomputes just those logits in the reference's order and must still agree. The
+    shapes take each kernel (one workgroup per expert at hidden 2048 and 7168, one
+    wave per expert at 512, the generic kernel at 1000 and 999), rows recomputed in
+    one chunk or in several, through 16-byte or (999) 4-byte reads."""
+    k = 8
+    # shorter rows have smaller bounds: larger weights keep the pairs inside them
+    w, x = _close_calls(ne, hidden, seed, [(1, 3e-5), (4, 2e-5), (7, 3e-5)], sd=0.08 if hidden < 2048 else 0.02)
     ids, ws = _router(backend, w.ravel(), x, None, ne, hidden, k, 1)
     rid, rw, logits, _ = orc.router(w.ravel(), x, ne, hidden, k)
     order = np.argsort(-logits.astype(np.float64), kind="stable")
-    assert float(logits[order[7]] - logits[order[8]]) < 1e-4  # the construction made a close call
+    # each constructed pair lies within the sum of its two logits' error bounds
+    # (Higham's recursive-summation bound u * sum_k |S_k| / (1 - n u) over the exact
+    # prefix sums S_k of the rounded products), so no bound alone can order it
+    u = 2.0 ** -24
+    prods = (w * x[None, :]).astype(np.float32).astype(np.float64)
+    bound = u * np.abs(np.cumsum(prods, axis=1)).sum(axis=1) / (1 - hidden * u)
+    for r in (1, 4, 7):
+        a, b = order[r], order[r + 1]
+        assert float(logits[a]) - float(logits[b]) < bound[a] + bound[b], (r, hidden)
     assert list(ids[0]) == list(rid)
     assert np.allclose(ws[0], rw, rtol=2e-5, atol=1e-6)
 
