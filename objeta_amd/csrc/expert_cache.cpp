@@ -71,6 +71,11 @@ struct Block {
     bool carved = false;    // inside one of the cache's chunks (freed with the chunk)
     std::vector<hipEvent_t> fence;
     hipEvent_t ready = nullptr;  // recorded on the copy stream after the fill; NULL once known complete
+    // The streams whose work may read the block since its fill: those of the library's
+    // calls that used it, or every stream of the context once its pointer went out
+    // through the cache API (the caller's streams are not known).
+    std::vector<hipStream_t> users;
+    bool all_streams = true;
 };
 
 }  // namespace
@@ -123,22 +128,40 @@ hipEvent_t take_event(Cache* c) {
     return e;
 }
 
-// Records, on every stream of the context, the point after which `b` is free.
+// Records, on every stream that may read `b`, the point after which `b` is free. The
+// copy stream needs none: every fill of a block is a copy on it, so a refill follows
+// the last fill in stream order, and `ready` (kept) still marks that fill's end for
+// destroy_block.
 void fence_block(Cache* c, Block* b) {
     for (hipEvent_t e : b->fence) c->event_pool.push_back(e);
     b->fence.clear();
-    if (b->ready) {  // the copy-stream fence below orders after the fill
-        c->event_pool.push_back(b->ready);
-        b->ready = nullptr;
-    }
     if (!c->ctx) return;
     auto rec = [&](hipStream_t s) {
         hipEvent_t e = take_event(c);
-        if (e && hipEventRecord(e, s) == hipSuccess) b->fence.push_back(e);
-        else if (e) c->event_pool.push_back(e);
+        if (e && hipEventRecord(e, s) == hipSuccess) {
+            b->fence.push_back(e);
+            return;
+        }
+        (void)hipGetLastError();
+        if (e) c->event_pool.push_back(e);
     };
-    for (hipStream_t s : c->ctx->streams) rec(s);
-    rec(c->ctx->copy_stream);
+    if (b->all_streams)
+        for (hipStream_t s : c->ctx->streams) rec(s);
+    else
+        for (hipStream_t s : b->users) rec(s);
+    b->users.clear();
+}
+
+// Work enqueued on `s` from now on reads `b` (s NULL: work on streams not known).
+void use_block(Block* b, hipStream_t s) {
+    if (!s) {
+        b->all_streams = true;
+        return;
+    }
+    if (b->all_streams) return;
+    for (hipStream_t u : b->users)
+        if (u == s) return;
+    b->users.push_back(s);
 }
 
 void destroy_block(Cache* c, Block* b) {
@@ -253,6 +276,8 @@ int32_t acquire_block(Cache* c, size_t bytes, hipStream_t s, Block** out) {
 int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t s) {
     if (!c->ctx || n == 0) return 0;
     if (!h_src) OBJ_FAIL(kInvalidInput, "copy tensor into the cache", "NULL host pointer");
+    b->users.clear();  // new contents: no reader yet
+    b->all_streams = false;
     hipStream_t cs = c->ctx->copy_stream;
     hipError_t r = hipSuccess;
     if (s) {
@@ -502,6 +527,7 @@ int32_t objeta_hip_cache_get(objeta_hip_expert_cache* c, const objeta_hip_cache_
     Block* b = lookup(c, to_key(*key));
     *hit = b ? 1 : 0;
     if (b && c->ctx) OBJ_TRY(wait_ready(c, b, nullptr));  // a prefetch may still be copying
+    if (b) use_block(b, nullptr);  // the pointer leaves the library
     if (d_ptr) *d_ptr = b ? b->ptr : nullptr;
     if (nbytes) *nbytes = b ? c->map.find(to_key(*key))->second.size : 0;
     return 0;
@@ -522,6 +548,7 @@ int32_t objeta_hip_cache_insert(objeta_hip_expert_cache* c, const objeta_hip_cac
     OBJ_TRY(stage_tensor(c, h_src, nbytes, s, &b));
     if (c->ctx) OBJ_TRY(join_copies(c, s));
     const bool ok = insert_block(c, to_key(*key), b, nbytes);
+    use_block(b, nullptr);  // the pointer leaves the library
     if (!ok && b->ptr) c->transients[b->ptr] = b;
     else if (!ok) retire_block(c, b);
     *cached = ok ? 1 : 0;
@@ -542,6 +569,7 @@ int32_t objeta_hip_cache_get_or_insert(objeta_hip_expert_cache* c, const objeta_
             hipStream_t s = resolve_stream(c->ctx, stream);
             OBJ_TRY(wait_ready(c, b, s));
         }
+        use_block(b, nullptr);  // the pointer leaves the library
         *hit = 1;
         *cached = 1;
         *d_ptr = b->ptr;
@@ -575,6 +603,7 @@ int32_t objeta_hip_cache_insert_pinned(objeta_hip_expert_cache* c, const objeta_
     c->st.resident_bytes += nbytes;
     c->st.pinned_bytes += nbytes;
     c->pinned.insert(k);
+    use_block(b, nullptr);  // the pointer leaves the library
     *d_ptr = b->ptr;
     return 0;
     OBJ_GUARD_END
@@ -873,6 +902,7 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
             }
             b->refs += 1;
             st.held.push_back({home, b});
+            use_block(b, s);
             dptr[q] = b->ptr;
             if (hit) (t[q].scale ? st.s_reused : st.w_reused) += t[q].len;
             else (t[q].scale ? st.s_loaded : st.w_loaded) += t[q].len;
@@ -1208,6 +1238,7 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
             if (cache->ctx) rc = wait_ready(cache, b, s);
             b->refs += 1;
             st.held.push_back({cache, b});
+            use_block(b, s);
             p[q] = b->ptr;
             sz[q] = cache->map.find(key)->second.size;
             sh_cached_bytes += sz[q];
