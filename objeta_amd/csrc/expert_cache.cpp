@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstring>
+#include <deque>
 #include <list>
 #include <map>
 #include <unordered_map>
@@ -71,10 +72,11 @@ struct Block {
     bool carved = false;    // inside one of the cache's chunks (freed with the chunk)
     std::vector<hipEvent_t> fence;
     hipEvent_t ready = nullptr;  // recorded on the copy stream after the fill; NULL once known complete
-    // The streams whose work may read the block since its fill: those of the library's
-    // calls that used it, or every stream of the context once its pointer went out
-    // through the cache API (the caller's streams are not known).
-    std::vector<hipStream_t> users;
+    // The reads since the fill: per stream, the mark that ends the last library call
+    // that used the block there (0: no mark, fence at reuse), or every stream of the
+    // context once its pointer went out through the cache API (the caller's streams are
+    // not known).
+    std::vector<std::pair<hipStream_t, uint64_t>> last_use;
     bool all_streams = true;
 };
 
@@ -102,6 +104,13 @@ struct objeta_hip_expert_cache {
         size_t size, used;
     };
     std::vector<Chunk> chunks;  // blocks are carved from these (see acquire_block)
+    // Per stream, the events that end the library's calls on it (the context's transient
+    // pool keeps these): mark n is done once its event has completed.
+    struct UseLog {
+        uint64_t next = 1, done = 0;
+        std::deque<std::pair<uint64_t, hipEvent_t>> pending;
+    };
+    std::unordered_map<hipStream_t, UseLog> uses;
 };
 
 namespace objeta {
@@ -128,10 +137,53 @@ hipEvent_t take_event(Cache* c) {
     return e;
 }
 
-// Records, on every stream that may read `b`, the point after which `b` is free. The
-// copy stream needs none: every fill of a block is a copy on it, so a refill follows
-// the last fill in stream order, and `ready` (kept) still marks that fill's end for
-// destroy_block.
+Cache* transient_pool(objeta_hip_context* ctx);
+
+// Retires the completed marks of `u` up to `id`, oldest first (the marks of one stream
+// complete in order); their events go back to `log`'s pool.
+void retire_marks(Cache* log, Cache::UseLog& u, uint64_t id) {
+    while (u.done < id && !u.pending.empty()) {
+        const hipError_t q = hipEventQuery(u.pending.front().second);
+        if (q != hipSuccess) {
+            if (q != hipErrorNotReady) (void)hipGetLastError();
+            break;
+        }
+        u.done = u.pending.front().first;
+        log->event_pool.push_back(u.pending.front().second);
+        u.pending.pop_front();
+    }
+}
+
+// A new mark on `s` in `log`'s use log: an event recorded after the work enqueued so
+// far (the completed older marks are retired first, so the log stays short). 0 when
+// the record failed.
+uint64_t mark_use(Cache* log, hipStream_t s) {
+    auto& u = log->uses[s];
+    retire_marks(log, u, u.next);
+    hipEvent_t e = take_event(log);
+    if (!e) return 0;
+    if (hipEventRecord(e, s) != hipSuccess) {
+        (void)hipGetLastError();
+        log->event_pool.push_back(e);
+        return 0;
+    }
+    u.pending.emplace_back(u.next, e);
+    return u.next++;
+}
+
+// Whether the work before mark `id` on `s` has completed.
+bool use_done(Cache* log, hipStream_t s, uint64_t id) {
+    auto it = log->uses.find(s);
+    if (id == 0 || it == log->uses.end()) return false;
+    retire_marks(log, it->second, id);
+    return it->second.done >= id;
+}
+
+// Records, on every stream whose reads of `b` may still be running, the point after
+// which `b` is free: a read by a library call whose mark has completed needs no fence.
+// The copy stream needs none: every fill of a block is a copy on it, so a refill
+// follows the last fill in stream order, and `ready` (kept) still marks that fill's
+// end for destroy_block.
 void fence_block(Cache* c, Block* b) {
     for (hipEvent_t e : b->fence) c->event_pool.push_back(e);
     b->fence.clear();
@@ -145,23 +197,28 @@ void fence_block(Cache* c, Block* b) {
         (void)hipGetLastError();
         if (e) c->event_pool.push_back(e);
     };
-    if (b->all_streams)
+    if (b->all_streams) {
         for (hipStream_t s : c->ctx->streams) rec(s);
-    else
-        for (hipStream_t s : b->users) rec(s);
-    b->users.clear();
+    } else {
+        Cache* log = transient_pool(c->ctx);
+        for (const auto& u : b->last_use)
+            if (!use_done(log, u.first, u.second)) rec(u.first);
+    }
+    b->last_use.clear();
 }
 
-// Work enqueued on `s` from now on reads `b` (s NULL: work on streams not known).
-void use_block(Block* b, hipStream_t s) {
-    if (!s) {
-        b->all_streams = true;
-        return;
-    }
+// The block's pointer went out through the cache API: its readers are not known.
+void use_block_anywhere(Block* b) { b->all_streams = true; }
+
+// A library call on `s` that read `b` ends at mark `id`.
+void set_last_use(Block* b, hipStream_t s, uint64_t id) {
     if (b->all_streams) return;
-    for (hipStream_t u : b->users)
-        if (u == s) return;
-    b->users.push_back(s);
+    for (auto& u : b->last_use)
+        if (u.first == s) {
+            u.second = id;
+            return;
+        }
+    b->last_use.emplace_back(s, id);
 }
 
 void destroy_block(Cache* c, Block* b) {
@@ -276,7 +333,7 @@ int32_t acquire_block(Cache* c, size_t bytes, hipStream_t s, Block** out) {
 int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t s) {
     if (!c->ctx || n == 0) return 0;
     if (!h_src) OBJ_FAIL(kInvalidInput, "copy tensor into the cache", "NULL host pointer");
-    b->users.clear();  // new contents: no reader yet
+    b->last_use.clear();  // new contents: no reader yet
     b->all_streams = false;
     hipStream_t cs = c->ctx->copy_stream;
     hipError_t r = hipSuccess;
@@ -451,6 +508,9 @@ void release_device(Cache* c) {
     c->free_bytes = 0;
     c->st.resident_bytes = 0;
     c->st.pinned_bytes = 0;
+    for (auto& kv : c->uses)
+        for (auto& pe : kv.second.pending) c->event_pool.push_back(pe.second);
+    c->uses.clear();
     for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
     c->event_pool.clear();
     c->ctx = nullptr;
@@ -527,7 +587,7 @@ int32_t objeta_hip_cache_get(objeta_hip_expert_cache* c, const objeta_hip_cache_
     Block* b = lookup(c, to_key(*key));
     *hit = b ? 1 : 0;
     if (b && c->ctx) OBJ_TRY(wait_ready(c, b, nullptr));  // a prefetch may still be copying
-    if (b) use_block(b, nullptr);  // the pointer leaves the library
+    if (b) use_block_anywhere(b);  // the pointer leaves the library
     if (d_ptr) *d_ptr = b ? b->ptr : nullptr;
     if (nbytes) *nbytes = b ? c->map.find(to_key(*key))->second.size : 0;
     return 0;
@@ -548,7 +608,7 @@ int32_t objeta_hip_cache_insert(objeta_hip_expert_cache* c, const objeta_hip_cac
     OBJ_TRY(stage_tensor(c, h_src, nbytes, s, &b));
     if (c->ctx) OBJ_TRY(join_copies(c, s));
     const bool ok = insert_block(c, to_key(*key), b, nbytes);
-    use_block(b, nullptr);  // the pointer leaves the library
+    use_block_anywhere(b);  // the pointer leaves the library
     if (!ok && b->ptr) c->transients[b->ptr] = b;
     else if (!ok) retire_block(c, b);
     *cached = ok ? 1 : 0;
@@ -569,7 +629,7 @@ int32_t objeta_hip_cache_get_or_insert(objeta_hip_expert_cache* c, const objeta_
             hipStream_t s = resolve_stream(c->ctx, stream);
             OBJ_TRY(wait_ready(c, b, s));
         }
-        use_block(b, nullptr);  // the pointer leaves the library
+        use_block_anywhere(b);  // the pointer leaves the library
         *hit = 1;
         *cached = 1;
         *d_ptr = b->ptr;
@@ -603,7 +663,7 @@ int32_t objeta_hip_cache_insert_pinned(objeta_hip_expert_cache* c, const objeta_
     c->st.resident_bytes += nbytes;
     c->st.pinned_bytes += nbytes;
     c->pinned.insert(k);
-    use_block(b, nullptr);  // the pointer leaves the library
+    use_block_anywhere(b);  // the pointer leaves the library
     *d_ptr = b->ptr;
     return 0;
     OBJ_GUARD_END
@@ -832,7 +892,15 @@ struct StagedExperts {
     bool any_copy = false;
 
     Cache* events = nullptr;                      // where the ready events come from and go back
+    hipStream_t stream = nullptr;                 // the call's stream, which reads the held blocks
+    // Called once the call's kernels are enqueued: one mark on the call's stream ends
+    // every held block's use by this call (so that a block evicted later needs no
+    // fence once the mark has completed), then the references go.
     void release() {
+        if (!held.empty() && stream && events) {
+            const uint64_t id = mark_use(events, stream);
+            for (auto& hb : held) set_last_use(hb.second, stream, id);
+        }
         for (auto& hb : held) {
             hb.second->refs -= 1;
             retire_block(hb.first, hb.second);
@@ -857,6 +925,7 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
     Cache* pool = transient_pool(ctx);
     st.ready.assign(k, nullptr);
     st.events = pool;
+    st.stream = s;
     // the copies are ordered after `s` once, at the first miss (each copy's own wait
     // would be one more stream wait per tensor)
     hipStream_t order_after = s;
@@ -902,7 +971,6 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
             }
             b->refs += 1;
             st.held.push_back({home, b});
-            use_block(b, s);
             dptr[q] = b->ptr;
             if (hit) (t[q].scale ? st.s_reused : st.w_reused) += t[q].len;
             else (t[q].scale ? st.s_loaded : st.w_loaded) += t[q].len;
@@ -1238,7 +1306,6 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
             if (cache->ctx) rc = wait_ready(cache, b, s);
             b->refs += 1;
             st.held.push_back({cache, b});
-            use_block(b, s);
             p[q] = b->ptr;
             sz[q] = cache->map.find(key)->second.size;
             sh_cached_bytes += sz[q];
