@@ -327,10 +327,26 @@ int32_t acquire_block(Cache* c, size_t bytes, hipStream_t s, Block** out) {
     return 0;
 }
 
+// The pinned-source copies of one call, launched together by flush_copies; each
+// block's ready event is recorded after that launch. `key` names the cache entry a
+// block was inserted under (keyed), so that a failed launch can take it out again.
+struct CopyBatch {
+    struct Pending {
+        Cache* c;
+        Block* b;
+        Key key;
+        bool keyed;
+    };
+    std::vector<H2dCopy> copies;
+    std::vector<Pending> blocks;
+    ~CopyBatch();  // takes out the entries of copies never launched (an error on the way)
+};
+
 // Copies host bytes into a block on the copy stream, ordered after `s` (s NULL: after
 // nothing but earlier copy-stream work, for prefetches), and records the block's
-// ready event after the copy.
-int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t s) {
+// ready event after the copy. With `batch`, a pinned source's copy is added to it
+// instead (launched, and the ready event recorded, by flush_copies).
+int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t s, CopyBatch* batch = nullptr) {
     if (!c->ctx || n == 0) return 0;
     if (!h_src) OBJ_FAIL(kInvalidInput, "copy tensor into the cache", "NULL host pointer");
     b->last_use.clear();  // new contents: no reader yet
@@ -346,6 +362,11 @@ int32_t fill_block(Cache* c, Block* b, const void* h_src, size_t n, hipStream_t 
     }
     // pinned sources by a kernel (a DMA copy behind a cross-stream wait starts late)
     const void* dsrc = r == hipSuccess ? pinned_device_ptr(h_src, n) : nullptr;
+    if (dsrc && batch) {
+        batch->copies.push_back(H2dCopy{b->ptr, dsrc, n});
+        batch->blocks.push_back(CopyBatch::Pending{c, b, Key{}, false});
+        return 0;
+    }
     if (dsrc) OBJ_TRY(launch_h2d_copy(cs, b->ptr, dsrc, n));
     else if (r == hipSuccess) r = hipMemcpyAsync(b->ptr, h_src, n, hipMemcpyHostToDevice, cs);
     if (r == hipSuccess) {
@@ -433,6 +454,14 @@ void remove_existing(Cache* c, const Key& k) {
     retire_block(c, b);
 }
 
+CopyBatch::~CopyBatch() {
+    for (const auto& p : blocks) {
+        if (!p.keyed) continue;
+        auto m = p.c->map.find(p.key);
+        if (m != p.c->map.end() && m->second.blk == p.b) remove_existing(p.c, p.key);
+    }
+}
+
 void make_room(Cache* c, size_t size) {
     while (c->st.resident_bytes + size > c->st.capacity_bytes && !c->order.empty())
         if (!evict_lru(c, nullptr)) break;
@@ -468,16 +497,42 @@ bool insert_block(Cache* c, const Key& k, Block* b, size_t size) {
     return true;
 }
 
-// A filled block for host bytes: recycled or new, copy enqueued after `s`.
-int32_t stage_tensor(Cache* c, const void* h_src, size_t n, hipStream_t s, Block** out) {
+// A filled block for host bytes: recycled or new, copy enqueued after `s` (or added to
+// `batch`).
+int32_t stage_tensor(Cache* c, const void* h_src, size_t n, hipStream_t s, Block** out, CopyBatch* batch = nullptr) {
     Block* b = nullptr;
     OBJ_TRY(acquire_block(c, n, c->ctx ? c->ctx->copy_stream : nullptr, &b));
-    int32_t rc = fill_block(c, b, h_src, n, s);
+    int32_t rc = fill_block(c, b, h_src, n, s, batch);
     if (rc) {
         retire_block(c, b);
         return rc;
     }
     *out = b;
+    return 0;
+}
+
+// Launches the batch's copies on the copy stream and records each block's ready event
+// after them. On failure the error is returned with the batch left full, and its
+// destructor takes the blocks' cache entries out (their bytes may not have arrived).
+int32_t flush_copies(objeta_hip_context* ctx, CopyBatch& batch) {
+    if (batch.copies.empty()) return 0;
+    int32_t rc = launch_h2d_copy_batch(ctx->copy_stream, batch.copies.data(), batch.copies.size());
+    for (size_t i = 0; i < batch.blocks.size() && rc == 0; ++i) {
+        Cache* c = batch.blocks[i].c;
+        Block* b = batch.blocks[i].b;
+        if (b->ready) c->event_pool.push_back(b->ready);
+        b->ready = take_event(c);
+        if (!b->ready || hipEventRecord(b->ready, ctx->copy_stream) != hipSuccess) {
+            (void)hipGetLastError();
+            rc = set_error(kDriver, __FILE__, __LINE__, __func__, "copy tensor into the cache", "event failure");
+        }
+    }
+    if (rc) {
+        (void)hipStreamSynchronize(ctx->copy_stream);
+        return rc;  // the batch's destructor takes the entries out
+    }
+    batch.copies.clear();
+    batch.blocks.clear();
     return 0;
 }
 
@@ -915,12 +970,27 @@ struct StagedExperts {
     }
 };
 
+// st.ready[j]: an event on the copy stream after slot j's copies.
+int32_t record_ready(objeta_hip_context* ctx, Cache* pool, StagedExperts& st, uint64_t j) {
+    hipEvent_t r = take_event(pool);
+    if (!r || hipEventRecord(r, ctx->copy_stream) != hipSuccess) {
+        (void)hipGetLastError();
+        if (r) pool->event_pool.push_back(r);
+        OBJ_FAIL(kDriver, "record copy event", "event failure");
+    }
+    st.ready[j] = r;
+    return 0;
+}
+
 // count_oversize: an expert larger than the capacity counts as an oversized-expert
 // bypass (bypass enabled) or a self-eviction risk, as the block-format and native
 // FP4 executors count them (moe.rs:485-492); the official executor counts neither.
+// batch: the pinned-source copies of all k experts go in one launch after the
+// lookups, and every expert's ready event is recorded after it (for callers that wait
+// for all k before computing); else each copy is launched as its expert is staged.
 int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_host_expert* experts,
                        const uint64_t* sel_ids, uint64_t k, int32_t format, uint64_t layer_id, bool count_oversize,
-                       hipStream_t s, objeta_hip_expert_ptrs* h_tab, StagedExperts& st) {
+                       hipStream_t s, objeta_hip_expert_ptrs* h_tab, StagedExperts& st, bool batch = false) {
     const bool fp4 = format == OBJETA_HIP_FP4_E2M1;
     Cache* pool = transient_pool(ctx);
     st.ready.assign(k, nullptr);
@@ -929,6 +999,8 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
     // the copies are ordered after `s` once, at the first miss (each copy's own wait
     // would be one more stream wait per tensor)
     hipStream_t order_after = s;
+    CopyBatch copies;
+    std::vector<uint64_t> copied_slots;
     for (uint64_t j = 0; j < k; ++j) {
         const uint64_t e = sel_ids[j];
         TensorRef t[6];
@@ -964,10 +1036,15 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
             }
             Cache* home = cache && !bypass ? cache : pool;
             if (!hit) {
-                OBJ_TRY(stage_tensor(home, t[q].h, t[q].len, order_after, &b));
+                const size_t pending = copies.blocks.size();
+                OBJ_TRY(stage_tensor(home, t[q].h, t[q].len, order_after, &b, batch ? &copies : nullptr));
                 order_after = nullptr;
                 copied = true;
-                if (cache && !bypass) (void)insert_block(cache, key, b, t[q].len);
+                const bool inserted = cache && !bypass && insert_block(cache, key, b, t[q].len);
+                if (inserted && copies.blocks.size() > pending) {
+                    copies.blocks.back().key = key;
+                    copies.blocks.back().keyed = true;
+                }
             }
             b->refs += 1;
             st.held.push_back({home, b});
@@ -977,17 +1054,16 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
         }
         if (copied) {
             st.any_copy = true;
-            hipEvent_t r = take_event(pool);
-            if (!r || hipEventRecord(r, ctx->copy_stream) != hipSuccess) {
-                (void)hipGetLastError();
-                if (r) pool->event_pool.push_back(r);
-                OBJ_FAIL(kDriver, "record copy event", "event failure");
-            }
-            st.ready[j] = r;
+            copied_slots.push_back(j);
+            if (!batch) OBJ_TRY(record_ready(ctx, pool, st, j));
         }
         objeta_hip_expert_ptrs& p = h_tab[j];
         if (fp4) p = {dptr[0], dptr[2], dptr[4], dptr[1], dptr[3], dptr[5]};
         else p = {dptr[0], dptr[1], dptr[2], nullptr, nullptr, nullptr};
+    }
+    if (batch) {
+        OBJ_TRY(flush_copies(ctx, copies));
+        for (uint64_t j : copied_slots) OBJ_TRY(record_ready(ctx, pool, st, j));
     }
     return 0;
 }
@@ -1286,7 +1362,8 @@ extern "C" int32_t objeta_hip_moe_execute_official_fp4(
     OBJ_HIP(hipEventRecord(ev[X1], s), "record event");
 
     StagedExperts st;
-    int32_t rc = stage_selected(ctx, cache, experts, sel_ids, k, OBJETA_HIP_FP4_E2M1, layer_id, false, s, h_tab, st);
+    int32_t rc =
+        stage_selected(ctx, cache, experts, sel_ids, k, OBJETA_HIP_FP4_E2M1, layer_id, false, s, h_tab, st, true);
     // The shared expert: with shared_from_cache, the cache's six Shared* entries of
     // this layer first (get in key order, stopping at the first miss, as the sketch
     // in crates/objeta-cuda/src/moe_tmp.txt:1-35 resolves it), else the argument.
@@ -1549,7 +1626,7 @@ extern "C" int32_t objeta_hip_moe_stack_cached(objeta_hip_context* ctx, int32_t 
         OBJ_HIP(hipEventRecord(c0, ctx->copy_stream), "record event");
         StagedExperts st;
         int32_t rc = stage_selected(ctx, cache, L.experts, uni.data(), uni.size(), format, L.layer_id, true, s, h_tab,
-                                    st);
+                                    st, true);
         if (rc == 0 && hipEventRecord(c1, ctx->copy_stream) != hipSuccess) {
             (void)hipGetLastError();
             rc = set_error(kDriver, __FILE__, __LINE__, __func__, "record event", "copy-stream event failed");

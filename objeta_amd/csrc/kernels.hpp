@@ -25,6 +25,16 @@ const void* pinned_device_ptr(const void* h, size_t n);
 // dst[0, n) = the pinned host bytes at device address src_dev, by a kernel on `s`
 // (n, dst and src_dev 16-byte multiples).
 int32_t launch_h2d_copy(hipStream_t s, void* dst, const void* src_dev, size_t n);
+// One copy of a batch: n bytes from a pinned source's device address to dst.
+struct H2dCopy {
+    void* dst;
+    const void* src_dev;
+    size_t n;
+};
+constexpr int kH2dBatch = 32;  // copies per launch (kernel arguments of 768 bytes)
+// The n copies of c[] in ceil(n / kH2dBatch) launches on s (pointers and sizes 16-byte
+// multiples, as for launch_h2d_copy).
+int32_t launch_h2d_copy_batch(hipStream_t s, const H2dCopy* c, size_t n);
 
 // GEMV over an FP8 E4M3 matrix with 128 x 128 E8M0 scale tiles (cols % 128 == 0).
 int32_t launch_fp8_rows(objeta_hip_context* ctx, hipStream_t s, const void* d_w, const void* d_s,
