@@ -986,8 +986,9 @@ int32_t record_ready(objeta_hip_context* ctx, Cache* pool, StagedExperts& st, ui
 // bypass (bypass enabled) or a self-eviction risk, as the block-format and native
 // FP4 executors count them (moe.rs:485-492); the official executor counts neither.
 // batch: the pinned-source copies of all k experts go in one launch after the
-// lookups, and every expert's ready event is recorded after it (for callers that wait
-// for all k before computing); else each copy is launched as its expert is staged.
+// lookups, and one ready event after it stands for all of them (on the last slot with
+// copies; for callers that wait for every slot before computing); else each copy is
+// launched as its expert is staged and every slot with copies gets its own event.
 int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_host_expert* experts,
                        const uint64_t* sel_ids, uint64_t k, int32_t format, uint64_t layer_id, bool count_oversize,
                        hipStream_t s, objeta_hip_expert_ptrs* h_tab, StagedExperts& st, bool batch = false) {
@@ -1063,7 +1064,9 @@ int32_t stage_selected(objeta_hip_context* ctx, Cache* cache, const objeta_hip_h
     }
     if (batch) {
         OBJ_TRY(flush_copies(ctx, copies));
-        for (uint64_t j : copied_slots) OBJ_TRY(record_ready(ctx, pool, st, j));
+        // the one launch ends every copy of the call: one ready event, on the last slot
+        // with copies, serves a caller that waits for all slots (one stream wait, not k)
+        if (!copied_slots.empty()) OBJ_TRY(record_ready(ctx, pool, st, copied_slots.back()));
     }
     return 0;
 }
