@@ -451,8 +451,10 @@ typedef struct {
 
 /* A single-GPU VRAM expert cache: LRU over tensors, pinned (never evicted) entries,
  * admission by size. Device memory comes from blocks that are recycled after an
- * eviction only once every stream of the context has passed the point of the
- * eviction (event fences, no host waits). Not internally locked (the reference's
+ * eviction only once the work that may read them has passed (event fences, no host
+ * waits): every stream of the context for a block whose pointer this API returned,
+ * the streams of the library calls that read it otherwise (a call whose end has
+ * already passed needs no fence). Not internally locked (the reference's
  * &mut CudaExpertCache). With ctx == NULL the cache keeps the accounting only and
  * owns no device memory (device pointers are NULL): the counters and LRU order
  * behave identically. */
