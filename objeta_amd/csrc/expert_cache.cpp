@@ -73,9 +73,9 @@ struct Block {
     std::vector<hipEvent_t> fence;
     hipEvent_t ready = nullptr;  // recorded on the copy stream after the fill; NULL once known complete
     // The reads since the fill: per stream, the mark that ends the last library call
-    // that used the block there (0: no mark, fence at reuse), or every stream of the
-    // context once its pointer went out through the cache API (the caller's streams are
-    // not known).
+    // that used the block there (0: no mark, fence at reuse); and, once its pointer went
+    // out through the cache API (the caller's streams are not known), every stream of
+    // the context.
     std::vector<std::pair<hipStream_t, uint64_t>> last_use;
     bool all_streams = true;
 };
@@ -197,12 +197,14 @@ void fence_block(Cache* c, Block* b) {
         (void)hipGetLastError();
         if (e) c->event_pool.push_back(e);
     };
-    if (b->all_streams) {
+    if (b->all_streams)
         for (hipStream_t s : c->ctx->streams) rec(s);
-    } else {
-        Cache* log = transient_pool(c->ctx);
-        for (const auto& u : b->last_use)
-            if (!use_done(log, u.first, u.second)) rec(u.first);
+    Cache* log = transient_pool(c->ctx);
+    for (const auto& u : b->last_use) {
+        if (b->all_streams &&
+            std::find(c->ctx->streams.begin(), c->ctx->streams.end(), u.first) != c->ctx->streams.end())
+            continue;  // fenced above
+        if (!use_done(log, u.first, u.second)) rec(u.first);
     }
     b->last_use.clear();
 }
@@ -210,9 +212,9 @@ void fence_block(Cache* c, Block* b) {
 // The block's pointer went out through the cache API: its readers are not known.
 void use_block_anywhere(Block* b) { b->all_streams = true; }
 
-// A library call on `s` that read `b` ends at mark `id`.
+// A library call on `s` that read `b` ends at mark `id` (kept also for a block handed
+// out through the API: `s` may be a stream outside the context).
 void set_last_use(Block* b, hipStream_t s, uint64_t id) {
-    if (b->all_streams) return;
     for (auto& u : b->last_use)
         if (u.first == s) {
             u.second = id;
