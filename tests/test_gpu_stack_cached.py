@@ -49,14 +49,15 @@ def stack(backend):
     pin.free()
 
 
-def run(backend, st, T, k, cache=None, prefetch=False, seed=970):
+def run(backend, st, T, k, cache=None, prefetch=False, seed=970, stream=None):
     H = st["H"]
     x = orc.gauss(T * H, seed + T, 1.0)
     d_h = backend.to_device(x)
     d_trace = backend.alloc(4 * st["L"] * T * H)
     moe = MoeExecutor(backend)
     ids, ws, tel = moe.stack_cached(Q4, st["layers"], k, T, d_h, H, st["I"], cache=cache, prefetch_next=prefetch,
-                                    d_trace=d_trace)
+                                    d_trace=d_trace, stream=stream)
+    backend.synchronize(stream)
     trace = d_trace.download(F32, st["L"] * T * H).reshape(st["L"], T, H)
     assert np.array_equal(d_h.download(F32, T * H).reshape(T, H), trace[-1])
     assert moe.device_error() == 0
@@ -146,3 +147,21 @@ def test_stack_cached_rejects_a_wrong_expert_before_any_launch(backend, stack):
         moe.stack_cached(Q4, layers, 4, 1, d_h, stack["H"], stack["I"])
     assert e.value.status == 5 and "w_up len" in str(e.value)
     assert np.array_equal(d_h.download(F32, stack["H"]), before)  # nothing ran
+
+
+def test_stack_cached_streams_in_turn_share_the_cache(backend, stack):
+    """Calls on the context's two streams in turn through one quarter-size cache: blocks
+    that a call on one stream read are evicted and refilled for a call on the other, their
+    reuse ordered by the calls' end marks (or fences while those are pending). Every
+    hidden state equals the no-cache run's bit for bit, with and without prefetch."""
+    T, k = 3, 4
+    L, E, eb = stack["L"], stack["E"], stack["eb"]
+    _, ids0, _, tr0, _ = run(backend, stack, T, k, cache=None)
+    cache = ExpertCache(L * E * eb // 4, backend)
+    for rep in range(6):
+        _, ids, _, tr, tel = run(backend, stack, T, k, cache=cache, prefetch=rep >= 3, stream=backend.stream(rep % 2))
+        assert np.array_equal(ids, ids0), rep
+        assert np.array_equal(tr.view(np.uint32), tr0.view(np.uint32)), rep
+        check_accounting(stack, tel, T, k)
+    assert cache.stats()["eviction_count"] > 0
+    cache.close()
