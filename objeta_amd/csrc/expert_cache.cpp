@@ -1641,6 +1641,7 @@ extern "C" int32_t objeta_hip_moe_stack_cached(objeta_hip_context* ctx, int32_t 
             const objeta_hip_cached_layer& N = layers[l + 1];
             predicted.assign(h_pids, h_pids + tk);
             seen.assign(N.n_experts, 0);
+            CopyBatch pf_copies;  // the predictions' copies, in one launch after the lookups
             for (uint64_t i = 0; i < tk && rc == 0; ++i) {
                 const uint32_t p = h_pids[i];
                 if (p >= N.n_experts || seen[p]) continue;
@@ -1651,15 +1652,18 @@ extern "C" int32_t objeta_hip_moe_stack_cached(objeta_hip_context* ctx, int32_t 
                     const Key key{N.layer_id, p, tr[q].kind, format};
                     if (cache->map.count(key) || tr[q].len > cache->st.capacity_bytes) continue;
                     Block* b = nullptr;
-                    if ((rc = stage_tensor(cache, tr[q].h, tr[q].len, nullptr, &b))) break;
-                    if (!insert_block(cache, key, b, tr[q].len)) {
-                        retire_block(cache, b);
-                        continue;
+                    const size_t pending = pf_copies.blocks.size();
+                    if ((rc = stage_tensor(cache, tr[q].h, tr[q].len, nullptr, &b, &pf_copies))) break;
+                    (void)insert_block(cache, key, b, tr[q].len);  // fits: larger tensors were skipped
+                    if (pf_copies.blocks.size() > pending) {
+                        pf_copies.blocks.back().key = key;
+                        pf_copies.blocks.back().keyed = true;
                     }
                     t.prefetch_tensors_issued += 1;
                     t.prefetch_bytes_issued += tr[q].len;
                 }
             }
+            if (rc == 0) rc = flush_copies(ctx, pf_copies);
         } else {
             predicted.clear();
         }
